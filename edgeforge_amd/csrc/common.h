@@ -1,0 +1,84 @@
+// Shared internals of libedgeforge_hip.so: device context, error reporting, weight handles and
+// small device helpers used by several kernels.  gfx950 (MI355X) only: wave64, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ef_hip.h"
+
+namespace efh {
+
+constexpr int kWave = 64;
+
+// ---- error reporting (per calling thread) ---------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int fail_hip(hipError_t e, const char* what);
+
+#define EFH_HIP(call)                                         \
+  do {                                                        \
+    hipError_t efh_e_ = (call);                               \
+    if (efh_e_ != hipSuccess) return ::efh::fail_hip(efh_e_, #call); \
+  } while (0)
+
+#define EFH_CHECK(cond, msg)                                  \
+  do {                                                        \
+    if (!(cond)) return ::efh::fail(EF_HIP_EINVAL, (msg));    \
+  } while (0)
+
+// ---- context ----------------------------------------------------------------------------------
+struct Context {
+  bool ready = false;
+  int device = -1;
+  int cu_count = 0;
+  size_t lds_per_block = 0;
+  hipStream_t stream = nullptr;  // library default stream (default priority)
+  char name[256] = {};
+};
+Context& ctx();
+int require_ready();
+inline hipStream_t pick(void* s) { return s ? static_cast<hipStream_t>(s) : ctx().stream; }
+
+}  // namespace efh
+
+// ---- weight handle (opaque in the C-ABI) ------------------------------------------------------
+struct ef_hip_weight_s {
+  int qtype = 0;
+  size_t rows = 0, cols = 0, row_bytes = 0;
+  const uint8_t* dev = nullptr;
+  bool owned = false;
+  uint32_t magic = 0;
+};
+
+namespace efh {
+
+constexpr uint32_t kWeightMagic = 0x45464857u;  // "EFHW"
+int check_weight(ef_hip_weight w);
+size_t row_bytes_of(int qtype, size_t cols);  // 0 when invalid
+
+// ---- device helpers ---------------------------------------------------------------------------
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
+  // v_cvt_f32_f16 is exact for every binary16 value (subnormals, inf, NaN).
+  _Float16 h;
+  const uint16_t b = static_cast<uint16_t>(h16);
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+}  // namespace efh

@@ -1,0 +1,463 @@
+// Next-token selection on the device: kern::argmax and ef::Sampler::sample for a batch of
+// independent sequences, one workgroup per sequence (src/sampler.cpp:13-70, src/kernels.cpp:105-111).
+//
+// Bit-exactness with the reference, given identical logits:
+//  * penalty (l > 0 ? l / p : l * p), temperature (l / T) and w - mx are single IEEE float ops
+//    (correctly rounded divide, no contraction);
+//  * the kept set and its order follow the reference comparator exactly: every logit becomes a
+//    unique 64-bit key (order-preserving float bits with +0 == -0, then the inverted id), so
+//    "higher logit, then lower id" is plain descending key order.  Top-k (k <= 1024) is a radix
+//    select over the keys plus a bitonic sort of the k winners in LDS; top-k off (or > 1024) is a
+//    full bitonic sort of all keys in the workspace;
+//  * the softmax over the kept ids, the top-p cut, its renormalisation and the CDF walk are the
+//    reference's sequential double loops, run by one thread in the same order.  They stop early
+//    only when every remaining term is below half an ulp of the running sum, since such terms
+//    (non-increasing, as the keys are sorted) can no longer change it;
+//  * the draw is std::uniform_real_distribution<double>(0, 1) over a std::mt19937_64 kept on the
+//    device (one state per sequence), advanced once per call exactly when temperature > 0.
+// The one libm call is exp(double); the device's exp and glibc's agree to the last bit except in
+// rare cases, where a flip of the chosen id would also need r to lie within an ulp of a
+// cumulative sum.
+#include <cmath>
+
+#include "common.h"
+#include "sampler.h"
+
+#pragma clang fp contract(off)
+
+namespace efh {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kMaxTopK = 1024;
+constexpr int kMtN = 312, kMtM = 156;
+
+// ---- std::mt19937_64 on the device (ISO C++ [rand.predef]) -------------------------------------------
+struct MtState {
+  uint64_t mt[kMtN];
+  int idx;
+  int pad[3];
+};
+static_assert(sizeof(MtState) <= kRngStateBytes, "rng state size");
+
+__device__ void mt_seed(MtState* s, uint64_t seed) {
+  s->mt[0] = seed;
+  for (int i = 1; i < kMtN; ++i) s->mt[i] = 6364136223846793005ull * (s->mt[i - 1] ^ (s->mt[i - 1] >> 62)) + i;
+  s->idx = kMtN;
+}
+
+__device__ uint64_t mt_next(MtState* s) {
+  if (s->idx >= kMtN) {
+    for (int i = 0; i < kMtN; ++i) {
+      const uint64_t y = (s->mt[i] & 0xFFFFFFFF80000000ull) | (s->mt[(i + 1) % kMtN] & 0x7FFFFFFFull);
+      s->mt[i] = s->mt[(i + kMtM) % kMtN] ^ (y >> 1) ^ ((y & 1ull) ? 0xB5026F5AA96619E9ull : 0ull);
+    }
+    s->idx = 0;
+  }
+  uint64_t y = s->mt[s->idx++];
+  y ^= (y >> 29) & 0x5555555555555555ull;
+  y ^= (y << 17) & 0x71D67FFFEDA60000ull;
+  y ^= (y << 37) & 0xFFF7EEE000000000ull;
+  y ^= y >> 43;
+  return y;
+}
+
+// libstdc++ generate_canonical<double, 53> with one 64-bit word, then uniform (0, 1).
+__device__ double mt_uniform(MtState* s) {
+  const double r = __ull2double_rn(mt_next(s)) * 0x1p-64;
+  return r >= 1.0 ? 0x1.fffffffffffffp-1 : r;
+}
+
+__global__ void rng_seed_kernel(uint8_t* states, const uint64_t* seeds, int batch) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < batch) mt_seed(reinterpret_cast<MtState*>(states + static_cast<size_t>(b) * kRngStateBytes), seeds[b]);
+}
+
+// ---- keys ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t order_bits(float v) {
+  uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);  // +0 and -0 compare equal in the reference
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t make_key(float v, uint32_t id) {
+  return (static_cast<uint64_t>(order_bits(v)) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - id);
+}
+__device__ __forceinline__ uint32_t key_id(uint64_t k) { return 0xFFFFFFFFu - static_cast<uint32_t>(k); }
+
+// First maximum (strict >, scan order) of x[0..n): returns the index.  NaN never replaces the
+// running best; a NaN at index 0 is the answer, as in the sequential scan.
+__device__ int block_argmax(const float* x, int n, float* s_val, int* s_idx) {
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = x[i];
+    if (v == v && (bi == 0x7FFFFFFF || v > bv)) {  // scanning upwards: equal values keep the lower index
+      bv = v;
+      bi = i;
+    }
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || ov > bv || (ov == bv && oi < bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    s_val[w] = bv;
+    s_idx[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = s_val[0];
+    int i = s_idx[0];
+    for (int k = 1; k < nw; ++k) {
+      if (s_idx[k] != 0x7FFFFFFF && (i == 0x7FFFFFFF || s_val[k] > v || (s_val[k] == v && s_idx[k] < i))) {
+        v = s_val[k];
+        i = s_idx[k];
+      }
+    }
+    const float x0 = x[0];
+    s_idx[0] = (x0 != x0 || i == 0x7FFFFFFF) ? 0 : i;
+  }
+  __syncthreads();
+  const int r = s_idx[0];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* x, int n, long ld, int32_t* out) {
+  __shared__ float s_val[kThreads / kWave];
+  __shared__ int s_idx[kThreads / kWave];
+  const int r = block_argmax(x + blockIdx.x * ld, n, s_val, s_idx);
+  if (threadIdx.x == 0) out[blockIdx.x] = r;
+}
+
+// ---- bitonic sorts (descending) --------------------------------------------------------------------------
+__device__ void bitonic_lds(uint64_t* a, int n) {  // n power of two, <= 2 * blockDim
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t x = a[i], y = a[l];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            a[i] = y;
+            a[l] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Full sort of n (power of two) keys in global memory.  Every compare-exchange distance below
+// kChunk runs on kChunk-element chunks held in LDS; larger distances go through memory.
+constexpr int kChunk = 4096;
+__device__ void bitonic_global(uint64_t* g, int n, uint64_t* lds) {
+  const int chunk = n < kChunk ? n : kChunk;
+  auto local_pass = [&](int base, int k, int jmax) {
+    for (int j = jmax; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < chunk; i += blockDim.x) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t x = lds[i], y = lds[l];
+          const bool desc = ((base + i) & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            lds[i] = y;
+            lds[l] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  };
+  for (int base = 0; base < n; base += chunk) {  // every k <= chunk inside the chunk
+    for (int i = threadIdx.x; i < chunk; i += blockDim.x) lds[i] = g[base + i];
+    __syncthreads();
+    for (int k = 2; k <= chunk; k <<= 1) local_pass(base, k, k >> 1);
+    for (int i = threadIdx.x; i < chunk; i += blockDim.x) g[base + i] = lds[i];
+    __syncthreads();
+  }
+  for (int k = chunk * 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j >= chunk; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t x = g[i], y = g[l];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            g[i] = y;
+            g[l] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    for (int base = 0; base < n; base += chunk) {
+      for (int i = threadIdx.x; i < chunk; i += blockDim.x) lds[i] = g[base + i];
+      __syncthreads();
+      local_pass(base, k, chunk >> 1);
+      for (int i = threadIdx.x; i < chunk; i += blockDim.x) g[base + i] = lds[i];
+      __syncthreads();
+    }
+  }
+}
+
+// Half an ulp of a positive finite double s: adding any t < half_ulp(s) leaves s unchanged.
+__device__ __forceinline__ double half_ulp(double s) {
+  int e;
+  (void)frexp(s, &e);  // s = m * 2^e, m in [0.5, 1)
+  return ldexp(1.0, e - 54);
+}
+
+// ---- the sampler --------------------------------------------------------------------------------------------
+struct SampleArgs {
+  const float* logits;
+  long ld;
+  int vocab;
+  float temperature, top_p, penalty;
+  int top_k;
+  const int32_t* hist;
+  const int32_t* hist_len;
+  long hist_ld;
+  uint8_t* rng;
+  int32_t* out;
+  uint8_t* ws;  // workspace base
+  size_t ws_stride;
+  int npow2;
+};
+
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
+  __shared__ uint64_t s_keys[kChunk];  // 32 KB: top-k candidates / sort chunk
+  __shared__ uint32_t s_hist[256];
+  __shared__ float s_val[kThreads / kWave];
+  __shared__ int s_idx[kThreads / kWave];
+  __shared__ int s_cnt, s_keep;
+  __shared__ uint64_t s_prefix, s_mask;
+  __shared__ int s_need, s_done;
+  __shared__ double s_sum;
+  __shared__ uint32_t s_seen[(32768 + 31) / 32];
+
+  const int b = blockIdx.x, V = a.vocab;
+  uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
+  float* work = reinterpret_cast<float*>(ws);                                   // [V]
+  double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));        // [V]
+  uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + ((V * 8 + 255) & ~255));  // [npow2]
+  const float* lg = a.logits + b * a.ld;
+
+  for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = lg[i];
+  __syncthreads();
+  // repetition penalty: each unique in-range history id once, in history order (src/sampler.cpp:16-24)
+  if (a.penalty != 1.0f) {
+    const int n = a.hist_len[b];
+    const int32_t* h = a.hist + b * a.hist_ld;
+    if (V <= 32768) {
+      for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        for (int i = 0; i < n; ++i) {
+          const int t = h[i];
+          if (t < 0 || t >= V || (s_seen[t >> 5] >> (t & 31) & 1u)) continue;
+          s_seen[t >> 5] |= 1u << (t & 31);
+          const float l = work[t];
+          work[t] = l > 0.0f ? __fdiv_rn(l, a.penalty) : l * a.penalty;
+        }
+      }
+    } else if (threadIdx.x == 0) {  // large vocabularies: first-occurrence test by scanning
+      for (int i = 0; i < n; ++i) {
+        const int t = h[i];
+        if (t < 0 || t >= V) continue;
+        bool dup = false;
+        for (int j = 0; j < i && !dup; ++j) dup = h[j] == t;
+        if (dup) continue;
+        const float l = work[t];
+        work[t] = l > 0.0f ? __fdiv_rn(l, a.penalty) : l * a.penalty;
+      }
+    }
+    __threadfence_block();
+    __syncthreads();
+  }
+  if (!(a.temperature > 0.0f)) {  // greedy: argmax, no draw (src/sampler.cpp:25)
+    const int r = block_argmax(work, V, s_val, s_idx);
+    if (threadIdx.x == 0) a.out[b] = r;
+    return;
+  }
+  for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = __fdiv_rn(work[i], a.temperature);
+  __threadfence_block();
+  __syncthreads();
+
+  const bool topk = a.top_k > 0 && a.top_k < V && a.top_k <= kMaxTopK;
+  int keep = V;
+  const uint64_t* sorted = nullptr;
+  if (topk) {
+    // radix select of the k-th largest key, 8 bits per pass from the top
+    if (threadIdx.x == 0) {
+      s_prefix = 0;
+      s_mask = 0;
+      s_need = a.top_k;
+      s_done = 0;
+      s_cnt = 0;
+    }
+    __syncthreads();
+    for (int shift = 56; shift >= 0 && !s_done; shift -= 8) {
+      for (int i = threadIdx.x; i < 256; i += blockDim.x) s_hist[i] = 0u;
+      __syncthreads();
+      const uint64_t prefix = s_prefix, mask = s_mask;
+      for (int i = threadIdx.x; i < V; i += blockDim.x) {
+        const uint64_t k = make_key(work[i], i);
+        if ((k & mask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int need = s_need, d = 255;
+        for (; d > 0; --d) {
+          if (static_cast<int>(s_hist[d]) >= need) break;
+          need -= static_cast<int>(s_hist[d]);
+        }
+        s_need = need;
+        s_prefix = prefix | (static_cast<uint64_t>(d) << shift);
+        s_mask = mask | (255ull << shift);
+        if (static_cast<int>(s_hist[d]) == need) s_done = 1;
+      }
+      __syncthreads();
+    }
+    const uint64_t prefix = s_prefix, mask = s_mask;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+      const uint64_t k = make_key(work[i], i);
+      if ((k & mask) >= prefix) {
+        const int pos = atomicAdd(&s_cnt, 1);
+        if (pos < kChunk) s_keys[pos] = k;
+      }
+    }
+    __syncthreads();
+    int n2 = 1;
+    while (n2 < a.top_k) n2 <<= 1;
+    for (int i = a.top_k + threadIdx.x; i < n2; i += blockDim.x) s_keys[i] = 0ull;
+    __syncthreads();
+    bitonic_lds(s_keys, n2);
+    keep = a.top_k;
+    sorted = s_keys;
+  } else {
+    if (a.top_k > 0 && a.top_k < V) keep = a.top_k;  // k above the LDS path: full sort, keep k
+    for (int i = threadIdx.x; i < a.npow2; i += blockDim.x) keys[i] = i < V ? make_key(work[i], i) : 0ull;
+    __threadfence_block();
+    __syncthreads();
+    bitonic_global(keys, a.npow2, s_keys);
+    sorted = keys;
+  }
+  // softmax over the kept ids in double (src/sampler.cpp:42-49)
+  const float mx = work[key_id(sorted[0])];
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(work[key_id(sorted[i])] - mx));
+  __threadfence_block();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int i = 0; i < keep; ++i) {
+      if (prob[i] < half_ulp(sum) && sum > 0.0) break;
+      sum += prob[i];
+    }
+    s_sum = sum;
+  }
+  __syncthreads();
+  const double sum = s_sum;
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / sum;
+  __threadfence_block();
+  __syncthreads();
+  if (a.top_p < 1.0f) {  // nucleus (src/sampler.cpp:50-61)
+    if (threadIdx.x == 0) {
+      double cum = 0.0;
+      int n = 0;
+      while (n < keep) {
+        if (cum > 0.0 && prob[n] < half_ulp(cum)) {
+          n = keep;  // cum is final and below top_p: the loop would run to the end
+          break;
+        }
+        cum += prob[n++];
+        if (cum >= static_cast<double>(a.top_p)) break;
+      }
+      const int kp = n > 1 ? n : 1;
+      double s2 = 0.0;
+      for (int i = 0; i < kp; ++i) {
+        if (s2 > 0.0 && prob[i] < half_ulp(s2)) break;
+        s2 += prob[i];
+      }
+      s_keep = kp;
+      s_sum = s2;
+    }
+    __syncthreads();
+    keep = s_keep;
+    const double s2 = s_sum;
+    for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / s2;
+    __threadfence_block();
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {  // draw and CDF walk (src/sampler.cpp:62-69)
+    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
+    const double r = mt_uniform(st);
+    int res = static_cast<int>(key_id(sorted[keep - 1]));
+    double cum = 0.0;
+    for (int i = 0; i < keep; ++i) {
+      if (cum > 0.0 && prob[i] < half_ulp(cum)) break;  // cum is final: r >= cum, so the last id
+      cum += prob[i];
+      if (r < cum) {
+        res = static_cast<int>(key_id(sorted[i]));
+        break;
+      }
+    }
+    a.out[b] = res;
+  }
+}
+
+}  // namespace
+
+size_t sample_workspace_stride(int vocab) {
+  size_t n2 = 1;
+  while (n2 < static_cast<size_t>(vocab)) n2 <<= 1;
+  const size_t v = static_cast<size_t>(vocab);
+  return ((v * 4 + 255) & ~size_t{255}) + ((v * 8 + 255) & ~size_t{255}) + ((n2 * 8 + 255) & ~size_t{255});
+}
+
+int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t s) {
+  hipLaunchKernelGGL(rng_seed_kernel, dim3((batch + 63) / 64), dim3(64), 0, s, static_cast<uint8_t*>(rng), seeds_dev,
+                     batch);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_argmax(const float* x, int n, long ld, int batch, int32_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(kThreads), 0, s, x, n, ld, out);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_hip_sampler_config& cfg,
+                  const int32_t* hist, const int32_t* hist_len, long hist_ld, void* rng, int32_t* out, void* ws,
+                  hipStream_t s) {
+  SampleArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.vocab = vocab;
+  a.temperature = cfg.temperature;
+  a.top_p = cfg.top_p;
+  a.penalty = cfg.repetition_penalty;
+  a.top_k = cfg.top_k;
+  a.hist = hist;
+  a.hist_len = hist_len;
+  a.hist_ld = hist_ld;
+  a.rng = static_cast<uint8_t*>(rng);
+  a.out = out;
+  a.ws = static_cast<uint8_t*>(ws);
+  a.ws_stride = sample_workspace_stride(vocab);
+  int n2 = 1;
+  while (n2 < vocab) n2 <<= 1;
+  a.npow2 = n2;
+  hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+}  // namespace efh

@@ -1,0 +1,174 @@
+/* EdgeForge on MI355X: C-ABI of the HIP quantized-decode hot path (libedgeforge_hip.so).
+ *
+ * Plain C types only (pointers, sizes, ints).  Every entry point returns an int status: 0 is OK,
+ * negative values are the EF_HIP_E* codes below, and ef_hip_last_error() gives the message of the
+ * calling thread's last failure.  Device pointers ("*_dev") are HIP device addresses on the
+ * current device; "stream" is a hipStream_t (NULL = the library's default stream of the device).
+ *
+ * Each declaration names the reference interface it replaces (paths relative to the EdgeForge
+ * repository root).  The C++ signatures of the reference are kept one level up, by the host shim
+ * in edgeforge_amd/host (ef::kern::matvec / matvec_jobs, ef::Sampler), which calls these.
+ */
+#ifndef EF_HIP_H
+#define EF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------------- */
+#define EF_HIP_OK 0
+#define EF_HIP_EINVAL (-1)  /* bad argument: shape, type, null pointer, size limit             */
+#define EF_HIP_ERUNTIME (-2) /* a HIP runtime call failed                                      */
+#define EF_HIP_ENODEV (-3)  /* no usable gfx950 device                                          */
+#define EF_HIP_ENOMEM (-4)  /* device allocation failed                                         */
+#define EF_HIP_ESTATE (-5)  /* library not initialised / handle already released                */
+
+/* Storage types, numbered as ef::QType (include/ef/quant.h:35). */
+#define EF_QTYPE_F32 0
+#define EF_QTYPE_F16 1
+#define EF_QTYPE_BF16 2
+#define EF_QTYPE_Q8_0 3
+#define EF_QTYPE_Q4_0 4
+
+/* ---- context (no reference counterpart: the reference is CPU-only; these replace the process-global
+ *      backend switch kern::set_backend, src/qkernels.cpp:80-99) ------------------------------ */
+int ef_hip_init(int device);
+int ef_hip_shutdown(void);
+const char* ef_hip_last_error(void);
+int ef_hip_device_name(char* buf, size_t cap);
+int ef_hip_version(int* major, int* minor);
+
+/* ---- device memory and streams (plumbing for callers without their own allocator) ----------- */
+int ef_hip_malloc(void** dev, size_t bytes);
+int ef_hip_free(void* dev);
+int ef_hip_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes, void* stream);
+int ef_hip_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes, void* stream);
+int ef_hip_memcpy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
+int ef_hip_memset(void* dev, int value, size_t bytes, void* stream);
+int ef_hip_stream_create(void** stream);
+int ef_hip_stream_destroy(void* stream);
+int ef_hip_stream_sync(void* stream);
+/* HIP events, for timing kernels on the stream they run on. */
+int ef_hip_event_create(void** ev);
+int ef_hip_event_destroy(void* ev);
+int ef_hip_event_record(void* ev, void* stream);
+int ef_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ---- weights ----------------------------------------------------------------------------------
+ * Replaces ef::WeightView (include/ef/qkernels.h:28-34): a row-major [rows][cols] matrix in one of
+ * the storage types above (row bytes as src/quant.cpp:136-149; Q4_0/Q8_0 need cols % 32 == 0).
+ * register_host uploads the bytes once; register_device wraps device bytes the caller owns (no
+ * copy).  The handle is what the GEMV entry points take. */
+typedef struct ef_hip_weight_s* ef_hip_weight;
+int ef_hip_weight_register_host(const void* host_bytes, int qtype, size_t rows, size_t cols, ef_hip_weight* out);
+int ef_hip_weight_register_device(const void* dev_bytes, int qtype, size_t rows, size_t cols, ef_hip_weight* out);
+int ef_hip_weight_release(ef_hip_weight w);
+int ef_hip_weight_info(ef_hip_weight w, int* qtype, size_t* rows, size_t* cols, const void** dev_bytes);
+int ef_hip_row_bytes(int qtype, size_t cols, size_t* out); /* src/quant.cpp:136-149 */
+
+/* ---- packed GEMV -----------------------------------------------------------------------------
+ * y[b][r] = sum_c W[r][c] * x[b][c] for b < batch, r < rows (FP32 activations, FP32 result).
+ * Replaces kern::matvec (include/ef/qkernels.h:66, src/qkernels.cpp:275-278) and, with batch > 1,
+ * the loop over independent sequences the reference would run.  ldx / ldy are the row strides
+ * (in floats) of x and y.  Q4_0 / Q8_0 read the 18 / 34-byte blocks in place.  Results agree with
+ * the reference's FP32 kernels to the rounding of a different summation order (the dot products
+ * are reproducible: the same inputs give the same bits on every call). */
+int ef_hip_matvec(ef_hip_weight W, const float* x_dev, float* y_dev, int batch, size_t ldx, size_t ldy, void* stream);
+
+/* Several products in one launch, one per job (kern::matvec_jobs + kern::MatvecJob,
+ * include/ef/qkernels.h:70-75, src/qkernels.cpp:280-297).  Each job has its own x / y; every job's
+ * rows are computed exactly as ef_hip_matvec would. */
+typedef struct {
+  float* y_dev;
+  ef_hip_weight W;
+  const float* x_dev;
+} ef_hip_job;
+int ef_hip_matvec_jobs(const ef_hip_job* jobs, size_t n_jobs, int batch, size_t ldx, size_t ldy, void* stream);
+
+/* Fused epilogues of the products Transformer::forward chains (src/model.cpp:227-262):
+ *  - residual:  y += W x            (matvec + kern::add_inplace, model.cpp:247-249, 260-262)
+ *  - swiglu:    y  = silu(G x) * (U x)  (matvec_jobs{gate,up} + kern::swiglu, model.cpp:255-258)
+ *  - rmsnorm on the input: x' = w * (x * rsqrt(mean(x^2) + eps)) computed per launch before the
+ *    product (kern::rmsnorm, src/kernels.cpp:69-75, model.cpp:227,253,269).  norm_w_dev NULL = off. */
+int ef_hip_matvec_residual(ef_hip_weight W, const float* x_dev, float* y_dev, int batch, size_t ldx, size_t ldy,
+                           void* stream);
+int ef_hip_matvec_swiglu(ef_hip_weight G, ef_hip_weight U, const float* x_dev, const float* norm_w_dev, float eps,
+                         float* y_dev, int batch, size_t ldx, size_t ldy, void* stream);
+int ef_hip_matvec_jobs_rmsnorm(const ef_hip_job* jobs, size_t n_jobs, const float* norm_w_dev, float eps, int batch,
+                               size_t ldx, size_t ldy, void* stream);
+
+/* Row r of W as FP32 (kern::row_f32, include/ef/qkernels.h:78): exact for F32/F16/BF16,
+ * dequantized for Q4_0/Q8_0.  One row per batch entry, ids on the device. */
+int ef_hip_rows_f32(ef_hip_weight W, const int32_t* ids_dev, int batch, float* out_dev, size_t ldo, void* stream);
+
+/* ---- quantizer (src/quant.cpp:26-99 q4_group, :151-175) ----------------------------------------
+ * Packs a row-major FP32 [rows][cols] matrix on the device into Q4_0 / Q8_0 / BF16 / F16 / F32
+ * rows; byte-identical to the reference's quantize_row (search = the reference's Q4 scale search). */
+int ef_hip_quantize(int qtype, const float* w_dev, size_t rows, size_t cols, int search, void* out_dev, void* stream);
+
+/* ---- sampler ----------------------------------------------------------------------------------
+ * ef::SamplerConfig (include/ef/sampler.h:13-19) and Sampler::sample (src/sampler.cpp:13-70) for
+ * `batch` independent sequences: logits [batch][ld] on the device; history [batch][hist_ld] int32
+ * with hist_len[batch] valid entries (device); one std::mt19937_64 state per sequence in rng_dev
+ * (created by ef_hip_rng_seed), advanced by one draw exactly when temperature > 0, as the
+ * reference does.  Token ids are bit-identical to the reference's on identical logits. */
+typedef struct {
+  float temperature;
+  int top_k;
+  float top_p;
+  float repetition_penalty;
+  uint64_t seed;
+} ef_hip_sampler_config;
+size_t ef_hip_rng_state_bytes(void); /* per sequence */
+int ef_hip_rng_seed(void* rng_dev, const uint64_t* seeds_host, int batch, void* stream);
+/* ws_dev: ef_hip_sample_workspace_bytes(vocab, batch) bytes of device scratch, or NULL for the
+ * library's own scratch (then calls that overlap on one device must not run concurrently). */
+size_t ef_hip_sample_workspace_bytes(size_t vocab, int batch);
+int ef_hip_sample(const float* logits_dev, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
+                  const int32_t* hist_dev, const int32_t* hist_len_dev, size_t hist_ld, void* rng_dev,
+                  int32_t* out_dev, void* ws_dev, void* stream);
+/* kern::argmax (src/kernels.cpp:105-111): first maximum wins. */
+int ef_hip_argmax(const float* x_dev, size_t n, int batch, size_t ld, int32_t* out_dev, void* stream);
+
+/* ---- decode engine ----------------------------------------------------------------------------
+ * Transformer::forward (src/model.cpp:184-276) on the device for `batch` independent sequences
+ * that share weights, with an FP32 KV cache [L][batch][max_seq][KV*hd] and a per-step HIP graph.
+ * Weights are registered handles; norms and the BF16 embedding are device arrays. */
+typedef struct {
+  size_t D, F, H, KV, hd, V, L, max_pos;
+  float eps, rope_theta;
+} ef_hip_model_config;
+
+typedef struct {
+  ef_hip_weight wq, wk, wv, wo, w_gate, w_up, w_down;
+  const float* attn_norm_dev;
+  const float* ffn_norm_dev;
+} ef_hip_layer;
+
+typedef struct ef_hip_engine_s* ef_hip_engine;
+int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* layers, ef_hip_weight embed,
+                         ef_hip_weight lm_head, const float* final_norm_dev, size_t max_seq, int batch,
+                         ef_hip_engine* out);
+int ef_hip_engine_destroy(ef_hip_engine e);
+/* One forward at position pos for all sequences: tokens[batch] (host).  Logits [batch][V] stay on
+ * the device (ef_hip_engine_logits); compute_logits = 0 skips the lm_head, as prefill does. */
+int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens_host, size_t pos, int compute_logits);
+int ef_hip_engine_logits(ef_hip_engine e, const float** logits_dev);
+int ef_hip_engine_hidden(ef_hip_engine e, const float** hidden_dev); /* final-norm output [batch][D] */
+/* The reference decode protocol (src/bench_decode.cpp:30-49, generate_greedy src/model.cpp:278-304)
+ * run on the device: prompt [batch][n_prompt] one position at a time (logits only at the last),
+ * then n tokens per sequence picked by argmax (cfg NULL or temperature <= 0) or by the sampler
+ * (rng_dev as in ef_hip_sample; the history is the prompt plus the tokens picked so far).
+ * tokens_out [batch][n] host.  Each step is one HIP graph launch; timings in seconds. */
+int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n_prompt, size_t n,
+                           const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
+                           double* prefill_s, double* decode_s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

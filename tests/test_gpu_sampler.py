@@ -1,0 +1,112 @@
+"""GPU parity of argmax and the sampler: token ids bit-identical to the reference's, on identical
+logits and seeds (src/sampler.cpp:13-70; oracle/efo_sampler.c pinned to the reference build)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from edgeforge_amd import _lib as EL
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+
+def _argmax(H, x):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, x.shape[-1])
+    out = H.DeviceArray((x.shape[0],), np.int32)
+    H.argmax(H.DeviceArray.from_host(x), x.shape[1], out, batch=x.shape[0])
+    return out.numpy()
+
+
+def test_argmax_first_max_ties_nan(hip):
+    assert _argmax(hip, np.array([0.5, 3.0, -1.0, 3.0], np.float32))[0] == 1  # tests/test_kernels.cpp:251
+    x = np.full(32000, -np.inf, np.float32)
+    assert _argmax(hip, x)[0] == 0
+    x[31999] = 0.0
+    x[17] = 0.0
+    assert _argmax(hip, x)[0] == 17
+    y = D.normal(1, 32000)
+    y[5] = np.nan
+    assert _argmax(hip, y)[0] == O.lib().efo_argmax(O.ptr(y, O._f32p), 32000)
+    y[0] = np.nan  # a NaN first element is never replaced in the sequential scan
+    assert _argmax(hip, y)[0] == 0
+    many = D.normal(2, (64, 32000), 3.0)
+    got = _argmax(hip, many)
+    assert [int(v) for v in got] == [int(np.argmax(r)) for r in many]
+
+
+CONFIGS = [
+    dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),  # config 3
+    dict(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0),  # CLI defaults with --temp 1
+    dict(temperature=0.7, top_k=0, top_p=0.9, repetition_penalty=1.3),
+    dict(temperature=1.5, top_k=1000, top_p=1.0, repetition_penalty=1.0),
+    dict(temperature=0.0, top_k=0, top_p=1.0, repetition_penalty=1.2),  # greedy with penalty
+    dict(temperature=5.0, top_k=1, top_p=1.0, repetition_penalty=1.0),
+    dict(temperature=1.0, top_k=0, top_p=1e-6, repetition_penalty=1.0),
+    dict(temperature=2.0, top_k=2000, top_p=0.5, repetition_penalty=1.0),  # k above the LDS path
+]
+
+
+@pytest.mark.parametrize("ci", range(len(CONFIGS)))
+def test_sampler_ids_bit_exact_over_steps(hip, ci):
+    cfg = CONFIGS[ci]
+    V, steps, batch = 32000, 12, 4
+    print(f"[case] sampler {cfg}", flush=True)
+    seeds = [1234 + 17 * b for b in range(batch)]
+    rng = hip.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    ws = hip.DeviceArray((EL.lib().ef_hip_sample_workspace_bytes(V, batch),), np.uint8)
+    g = D.rng(100 + ci)
+    for step in range(steps):
+        scale = 3.0 if step % 2 == 0 else 1.0
+        logits = (g.standard_normal((batch, V), dtype=np.float32) * np.float32(scale)).astype(np.float32)
+        if step == 3:
+            logits[:, 100:110] = logits[:, 100:101]  # exact ties resolved by lower id
+        hist = g.integers(0, V, size=(batch, 64)).astype(np.int32)
+        hist[:, 0] = -1  # out-of-range ids are skipped
+        hist[:, 1] = hist[:, 2]  # repeated ids penalised once
+        hlen = np.full(batch, 64, np.int32)
+        out = hip.DeviceArray((batch,), np.int32)
+        hip.sample(hip.DeviceArray.from_host(logits), V, cfg, out, batch=batch, hist=hip.DeviceArray.from_host(hist),
+                   hist_len=hip.DeviceArray.from_host(hlen), hist_ld=64, rng=rng, ws=ws)
+        got = out.numpy()
+        want = [cpu[b].sample(logits[b], hist[b]) for b in range(batch)]
+        assert [int(v) for v in got] == want, (step, cfg)
+
+
+def test_sampler_reference_kats(hip):
+    """tests/test_tokenizer.cpp:152-172 on the device."""
+    def one(logits, cfg, hist=(), seed=0):
+        logits = np.asarray(logits, np.float32)
+        n = len(logits)
+        h = np.asarray(list(hist) or [0], np.int32)
+        out = hip.DeviceArray((1,), np.int32)
+        rng = hip.RngStates([seed])
+        hip.sample(hip.DeviceArray.from_host(logits), n, cfg, out, hist=hip.DeviceArray.from_host(h),
+                   hist_len=hip.DeviceArray.from_host(np.array([len(hist)], np.int32)), hist_ld=len(h), rng=rng)
+        return int(out.numpy()[0])
+
+    l = [1.0, 3.0, 2.0, -1.0]
+    assert one(l, {}) == 1
+    assert one(l, dict(temperature=5.0, top_k=1)) == 1
+    assert one(l, dict(temperature=1.0, top_p=1e-6)) == 1
+    assert one(l, dict(repetition_penalty=2.0), hist=[1, 1]) == 2
+    assert one([-1.0, -1.5], dict(repetition_penalty=2.0), hist=[0]) == 1
+
+
+def test_sampler_seeded_distribution(hip):
+    """0.7 / 0.2 / 0.1 within 0.02 over 20000 draws, and the GPU sequence equals the CPU one
+    (tests/test_tokenizer.cpp:174-191)."""
+    l = np.log(np.array([0.7, 0.2, 0.1], np.float32)).astype(np.float32)
+    n = 4000
+    cfg = dict(temperature=1.0, seed=42)
+    rng = hip.RngStates([42])
+    cpu = O.Sampler(temperature=1.0, seed=42)
+    dl = hip.DeviceArray.from_host(l)
+    out = hip.DeviceArray((1,), np.int32)
+    counts = np.zeros(3)
+    for i in range(n):
+        hip.sample(dl, 3, cfg, out, rng=rng)
+        t = int(out.numpy()[0])
+        assert t == cpu.sample(l)
+        counts[t] += 1
+    assert np.all(np.abs(counts / n - [0.7, 0.2, 0.1]) < 0.03)
