@@ -81,12 +81,15 @@ SIGNATURES = {
     "ef_hip_matvec_jobs_rmsnorm": (C.c_int, [C.POINTER(ef_hip_job), _sz, _P, C.c_float, C.c_int, _sz, _sz, _P]),
     "ef_hip_rows_f32": (C.c_int, [_P, _P, C.c_int, _P, _sz, _P]),
     "ef_hip_quantize": (C.c_int, [C.c_int, _P, _sz, _sz, C.c_int, _P, _P]),
+    "ef_hip_fill_normal": (C.c_int, [_P, _sz, C.c_uint64, C.c_uint64, C.c_float, C.c_float, _P]),
     "ef_hip_rng_state_bytes": (_sz, []),
     "ef_hip_rng_seed": (C.c_int, [_P, _u64p, C.c_int, _P]),
     "ef_hip_sample_workspace_bytes": (_sz, [_sz, C.c_int]),
     "ef_hip_sample": (C.c_int, [_P, _sz, C.c_int, _sz, C.POINTER(ef_hip_sampler_config), _P, _P, _sz, _P, _P, _P,
                                 _P]),
     "ef_hip_argmax": (C.c_int, [_P, _sz, C.c_int, _sz, _P, _P]),
+    "ef_hip_profile_matvec": (C.c_int, [C.c_int, C.POINTER(_P), C.POINTER(_P), _sz, _P, _P, C.c_float, _P, C.c_int,
+                                        C.c_int, _P, _f32p]),
     "ef_hip_engine_create": (C.c_int, [C.POINTER(ef_hip_model_config), C.POINTER(ef_hip_layer), _P, _P, _P, _sz,
                                        C.c_int, C.POINTER(_P)]),
     "ef_hip_engine_destroy": (C.c_int, [_P]),

@@ -61,11 +61,6 @@ using namespace efh;
     if (efh_rc_ != EF_HIP_OK) return efh_rc_; \
   } while (0)
 
-#define EFH_RC(expr)                 \
-  do {                               \
-    int efh_rc_ = (expr);            \
-    if (efh_rc_ != EF_HIP_OK) return efh_rc_; \
-  } while (0)
 
 extern "C" {
 
@@ -348,6 +343,40 @@ int ef_hip_matvec_swiglu(ef_hip_weight G, ef_hip_weight U, const float* x, const
   return launch_gemv(&j, 1, kEpiSwiglu, norm_w, eps, batch, ldx, ldy, pick(stream));
 }
 
+int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* W2, size_t n_weights,
+                          const float* x, const float* norm_w, float eps, float* y, int batch, int launches,
+                          void* stream, float* avg_ms) {
+  EFH_READY();
+  EFH_CHECK(W && n_weights > 0 && x && y && avg_ms && launches > 0, "profile_matvec: bad argument");
+  EFH_CHECK(epi >= kEpiStore && epi <= kEpiSwiglu, "profile_matvec: unknown epilogue");
+  EFH_CHECK(epi != kEpiSwiglu || W2 != nullptr, "profile_matvec: swiglu needs the up matrices");
+  for (size_t i = 0; i < n_weights; ++i) {
+    EFH_RC(check_weight(W[i]));
+    if (W2) EFH_RC(check_weight(W2[i]));
+  }
+  hipStream_t s = pick(stream);
+  hipEvent_t e0, e1;
+  EFH_HIP(hipEventCreate(&e0));
+  EFH_HIP(hipEventCreate(&e1));
+  int rc = EF_HIP_OK;
+  const size_t ldx = W[0]->cols, ldy = W[0]->rows;
+  EFH_HIP(hipEventRecord(e0, s));
+  for (int i = 0; i < launches && rc == EF_HIP_OK; ++i) {
+    const size_t k = static_cast<size_t>(i) % n_weights;
+    const GemvJob j{W[k], epi == kEpiSwiglu ? W2[k] : nullptr, x, y};
+    rc = launch_gemv(&j, 1, epi, norm_w, eps, batch, ldx, ldy, s);
+  }
+  EFH_HIP(hipEventRecord(e1, s));
+  EFH_HIP(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  EFH_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc != EF_HIP_OK) return rc;
+  *avg_ms = ms / static_cast<float>(launches);
+  return EF_HIP_OK;
+}
+
 // ---- codec / row lookup ---------------------------------------------------------------------------
 int ef_hip_quantize(int qtype, const float* w, size_t rows, size_t cols, int search, void* out, void* stream) {
   EFH_READY();
@@ -356,6 +385,13 @@ int ef_hip_quantize(int qtype, const float* w, size_t rows, size_t cols, int sea
   size_t rb = 0;
   EFH_RC(ef_hip_row_bytes(qtype, cols, &rb));
   return launch_quantize(qtype, w, rows, cols, search, out, pick(stream));
+}
+
+int ef_hip_fill_normal(float* out, size_t n, uint64_t seed, uint64_t offset, float mean, float scale, void* stream) {
+  EFH_READY();
+  EFH_CHECK(out != nullptr || n == 0, "fill_normal: null pointer");
+  if (n == 0) return EF_HIP_OK;
+  return launch_fill_normal(out, n, seed, offset, mean, scale, pick(stream));
 }
 
 int ef_hip_rows_f32(ef_hip_weight W, const int32_t* ids, int batch, float* out, size_t ldo, void* stream) {

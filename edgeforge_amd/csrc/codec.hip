@@ -224,3 +224,58 @@ int launch_rows_f32(const ef_hip_weight_s* W, const int32_t* ids, int batch, flo
 }
 
 }  // namespace efh
+
+// ---- synthetic inputs -----------------------------------------------------------------------------------
+// N(mean, scale^2) floats from Philox4x32-10 (Salmon et al., "Parallel random numbers: as easy as
+// 1, 2, 3", SC'11) and the Box-Muller transform: element i uses counter (i / 4, offset), key seed.
+// Deterministic for (seed, offset, i) on every run; used to build synthetic weights and inputs.
+namespace efh {
+namespace {
+
+__device__ __forceinline__ void philox_round(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+  const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c[0];
+  const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c[2];
+  const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c[1] ^ k0;
+  const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c[3] ^ k1;
+  c[1] = static_cast<uint32_t>(p1);
+  c[3] = static_cast<uint32_t>(p0);
+  c[0] = n0;
+  c[2] = n2;
+}
+
+__global__ void fill_normal_kernel(float* __restrict__ out, size_t n, uint64_t seed, uint64_t offset, float mean,
+                                   float scale) {
+  const size_t q = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q * 4 >= n) return;
+  uint32_t c[4] = {static_cast<uint32_t>(q), static_cast<uint32_t>(q >> 32), static_cast<uint32_t>(offset),
+                   static_cast<uint32_t>(offset >> 32)};
+  uint32_t k0 = static_cast<uint32_t>(seed), k1 = static_cast<uint32_t>(seed >> 32);
+  for (int r = 0; r < 10; ++r) {
+    philox_round(c, k0, k1);
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  float z[4];
+  for (int h = 0; h < 2; ++h) {
+    const float u1 = (static_cast<float>(c[2 * h] >> 8) + 0.5f) * 0x1p-24f;  // (0, 1)
+    const float u2 = static_cast<float>(c[2 * h + 1] >> 8) * 0x1p-24f;       // [0, 1)
+    const float r = sqrtf(-2.0f * logf(u1));
+    z[2 * h] = r * cosf(6.28318530717958647692f * u2);
+    z[2 * h + 1] = r * sinf(6.28318530717958647692f * u2);
+  }
+  for (int j = 0; j < 4; ++j)
+    if (q * 4 + j < n) out[q * 4 + j] = mean + scale * z[j];
+}
+
+}  // namespace
+
+int launch_fill_normal(float* out, size_t n, uint64_t seed, uint64_t offset, float mean, float scale,
+                       hipStream_t s) {
+  const size_t quads = (n + 3) / 4;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0, s, out, n,
+                     seed, offset, mean, scale);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+}  // namespace efh

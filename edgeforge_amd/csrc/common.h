@@ -25,6 +25,12 @@ int fail_hip(hipError_t e, const char* what);
     if (efh_e_ != hipSuccess) return ::efh::fail_hip(efh_e_, #call); \
   } while (0)
 
+#define EFH_RC(expr)                                  \
+  do {                                                \
+    int efh_rc_ = (expr);                             \
+    if (efh_rc_ != EF_HIP_OK) return efh_rc_;         \
+  } while (0)
+
 #define EFH_CHECK(cond, msg)                                  \
   do {                                                        \
     if (!(cond)) return ::efh::fail(EF_HIP_EINVAL, (msg));    \

@@ -1,0 +1,396 @@
+// Device decode engine: Transformer::forward (src/model.cpp:184-276) for `batch` independent
+// sequences sharing one set of packed weights, plus the reference decode protocol
+// (src/bench_decode.cpp:30-49) driven entirely on the device.
+//
+// HBM layout: activations [batch][dim] FP32; KV cache [L][batch][max_seq][KV*hd] FP32 (the
+// reference's [L][max_seq][kv_dim] with the sequence index inserted); token history
+// [batch][max_seq] int32 (prompt, then picked tokens); the position is one int32 in device memory.
+// Every kernel of a step reads the position and the input token from device memory, so each step
+// kind is captured once as a HIP graph and replayed: a whole generation is a chain of graph
+// launches with no host round-trip between tokens.
+//
+// One step per layer: [rmsnorm + q/k/v GEMV] -> [RoPE + attention, cache write] -> [o GEMV +
+// residual] -> [rmsnorm + gate/up GEMV + SwiGLU] -> [down GEMV + residual]; then [final rmsnorm +
+// lm_head GEMV] and the token pick (argmax or the sampler) when logits are needed.
+#include <chrono>
+#include <cmath>
+#include <map>
+#include <vector>
+
+#include "codec.h"
+#include "common.h"
+#include "gemv.h"
+#include "glue.h"
+#include "sampler.h"
+
+namespace {
+constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
+enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8 };
+}  // namespace
+
+struct ef_hip_engine_s {
+  uint32_t magic = 0;
+  ef_hip_model_config c{};
+  std::vector<ef_hip_layer> layers;
+  ef_hip_weight embed = nullptr, lm_head = nullptr;
+  const float* final_norm = nullptr;
+  size_t max_seq = 0, kvd = 0, cached = 0;
+  int B = 1;
+  hipStream_t stream = nullptr;
+  float *x = nullptr, *q = nullptr, *knew = nullptr, *vnew = nullptr, *ctx = nullptr, *act = nullptr;
+  float *logits = nullptr, *hidden = nullptr, *kc = nullptr, *vc = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+  int32_t *hist = nullptr, *hist_len = nullptr, *next_tok = nullptr, *pos = nullptr, *n_prompt = nullptr;
+  int32_t* out_tokens = nullptr;
+  void* sample_ws = nullptr;
+  int32_t* stage = nullptr;  // pinned host staging
+  std::vector<void*> allocs;
+  std::map<int, hipGraphExec_t> graphs;
+  ef_hip_sampler_config scfg{};
+  void* rng = nullptr;
+};
+
+namespace efh {
+namespace {
+
+int check_engine(ef_hip_engine e) {
+  if (e == nullptr) return fail(EF_HIP_EINVAL, "null engine");
+  if (e->magic != kEngineMagic) return fail(EF_HIP_ESTATE, "engine was destroyed or is not an engine");
+  return EF_HIP_OK;
+}
+
+template <class T>
+int dev_alloc(ef_hip_engine e, T** p, size_t count) {
+  void* v = nullptr;
+  EFH_HIP(hipMalloc(&v, std::max<size_t>(count, 1) * sizeof(T)));
+  e->allocs.push_back(v);
+  *p = static_cast<T*>(v);
+  return EF_HIP_OK;
+}
+
+int check_matrix(ef_hip_weight w, size_t rows, size_t cols, bool packed, const char* what) {
+  int rc = check_weight(w);
+  if (rc != EF_HIP_OK) return fail(rc, std::string(what) + ": bad weight handle");
+  if (w->rows != rows || w->cols != cols) {
+    return fail(EF_HIP_EINVAL, std::string(what) + ": shape " + std::to_string(w->rows) + "x" +
+                                   std::to_string(w->cols) + ", config needs " + std::to_string(rows) + "x" +
+                                   std::to_string(cols));
+  }
+  if (packed && w->qtype != EF_QTYPE_Q4_0 && w->qtype != EF_QTYPE_Q8_0)
+    return fail(EF_HIP_EINVAL, std::string(what) + ": the decode GEMVs need Q4_0 or Q8_0 weights");
+  return EF_HIP_OK;
+}
+
+
+int enqueue_step(ef_hip_engine e, int mode) {
+  const ef_hip_model_config& c = e->c;
+  const int B = e->B;
+  const size_t D = c.D, F = c.F, V = c.V, kvd = e->kvd, S = e->max_seq;
+  hipStream_t s = e->stream;
+  EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s));
+  AttnArgs a{};
+  a.q = e->q;
+  a.knew = e->knew;
+  a.vnew = e->vnew;
+  a.cos_t = e->cos_t;
+  a.sin_t = e->sin_t;
+  a.pos_dev = e->pos;
+  a.ctx = e->ctx;
+  a.ldq = static_cast<long>(D);
+  a.H = static_cast<int>(c.H);
+  a.KV = static_cast<int>(c.KV);
+  a.hd = static_cast<int>(c.hd);
+  a.max_seq = static_cast<int>(S);
+  a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.hd)));  // src/kernels.cpp:158
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = e->layers[l];
+    const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, D, D},
+                            {w.wk, nullptr, e->x, e->knew, D, kvd},
+                            {w.wv, nullptr, e->x, e->vnew, D, kvd}};
+    EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, B, D, D, s));
+    a.kcache = e->kc + l * B * S * kvd;
+    a.vcache = e->vc + l * B * S * kvd;
+    EFH_RC(launch_attention(a, B, s));
+    const GemvJob o{w.wo, nullptr, e->ctx, e->x, D, D};
+    EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, B, D, D, s));
+    const GemvJob gu{w.w_gate, w.w_up, e->x, e->act, D, F};
+    EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, B, D, F, s));
+    const GemvJob dn{w.w_down, nullptr, e->act, e->x, F, D};
+    EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s));
+  }
+  if (mode & kLogits) {
+    const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, D, V};
+    EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s));
+  }
+  if (mode & (kGreedy | kSample)) {
+    if (mode & kGreedy) {
+      EFH_RC(launch_argmax(e->logits, static_cast<int>(V), static_cast<long>(V), B, e->next_tok, s));
+    } else {
+      EFH_RC(launch_sample(e->logits, static_cast<int>(V), B, static_cast<long>(V), e->scfg, e->hist, e->hist_len,
+                           static_cast<long>(S), e->rng, e->next_tok, e->sample_ws, s));
+    }
+    EFH_RC(launch_finish_step(e->next_tok, B, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens,
+                              static_cast<long>(S), e->n_prompt, e->pos, s));
+  } else if (mode & kAdvance) {
+    EFH_RC(launch_advance(e->pos, s));
+  }
+  return EF_HIP_OK;
+}
+
+int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
+  auto it = e->graphs.find(mode);
+  if (it != e->graphs.end()) {
+    *out = it->second;
+    return EF_HIP_OK;
+  }
+  EFH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_step(e, mode);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(e->stream, &g);
+  if (rc != EF_HIP_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (ec != hipSuccess) return fail_hip(ec, "hipStreamEndCapture");
+  hipGraphExec_t ex = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (ei != hipSuccess) return fail_hip(ei, "hipGraphInstantiate");
+  e->graphs[mode] = ex;
+  *out = ex;
+  return EF_HIP_OK;
+}
+
+int drop_graph(ef_hip_engine e, int mode) {
+  auto it = e->graphs.find(mode);
+  if (it != e->graphs.end()) {
+    EFH_HIP(hipGraphExecDestroy(it->second));
+    e->graphs.erase(it);
+  }
+  return EF_HIP_OK;
+}
+
+int run_step(ef_hip_engine e, int mode) {
+  hipGraphExec_t g;
+  EFH_RC(graph_for(e, mode, &g));
+  EFH_HIP(hipGraphLaunch(g, e->stream));
+  return EF_HIP_OK;
+}
+
+}  // namespace
+}  // namespace efh
+
+using namespace efh;
+
+extern "C" {
+
+int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* layers, ef_hip_weight embed,
+                         ef_hip_weight lm_head, const float* final_norm, size_t max_seq, int batch,
+                         ef_hip_engine* out) {
+  EFH_RC(require_ready());
+  EFH_CHECK(cfg && layers && out && final_norm, "engine_create: null argument");
+  const ef_hip_model_config& c = *cfg;
+  EFH_CHECK(c.D > 0 && c.F > 0 && c.H > 0 && c.KV > 0 && c.hd > 0 && c.V > 0 && c.L > 0, "engine_create: zero dim");
+  EFH_CHECK(c.H * c.hd == c.D && c.H % c.KV == 0 && c.hd % 2 == 0 && c.hd <= 512,
+            "engine_create: need H*hd == D, H % KV == 0, even hd <= 512");
+  EFH_CHECK(max_seq > 0 && max_seq <= c.max_pos, "engine_create: max_seq must be in [1, max_position_embeddings]");
+  EFH_CHECK(max_seq <= 12000, "engine_create: max_seq above 12000 (attention scores are held in LDS)");
+  EFH_CHECK(batch >= 1 && batch <= 1024, "engine_create: batch must be in [1, 1024]");
+  EFH_CHECK(c.V < 0x7FFFFFFF, "engine_create: vocab too large");
+  const size_t kvd = c.KV * c.hd;
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = layers[l];
+    EFH_RC(check_matrix(w.wq, c.D, c.D, true, "q_proj"));
+    EFH_RC(check_matrix(w.wk, kvd, c.D, true, "k_proj"));
+    EFH_RC(check_matrix(w.wv, kvd, c.D, true, "v_proj"));
+    EFH_RC(check_matrix(w.wo, c.D, c.D, true, "o_proj"));
+    EFH_RC(check_matrix(w.w_gate, c.F, c.D, true, "gate_proj"));
+    EFH_RC(check_matrix(w.w_up, c.F, c.D, true, "up_proj"));
+    EFH_RC(check_matrix(w.w_down, c.D, c.F, true, "down_proj"));
+    EFH_CHECK(w.w_gate->qtype == w.w_up->qtype, "gate_proj and up_proj must share a storage type");
+    EFH_CHECK(w.attn_norm_dev && w.ffn_norm_dev, "engine_create: null norm weights");
+  }
+  EFH_RC(check_matrix(lm_head, c.V, c.D, true, "lm_head"));
+  EFH_RC(check_matrix(embed, c.V, c.D, false, "embed_tokens"));
+
+  auto* e = new ef_hip_engine_s;
+  e->c = c;
+  e->layers.assign(layers, layers + c.L);
+  e->embed = embed;
+  e->lm_head = lm_head;
+  e->final_norm = final_norm;
+  e->max_seq = max_seq;
+  e->kvd = kvd;
+  e->B = batch;
+  auto cleanup_fail = [&](int rc) {
+    for (void* p : e->allocs) (void)hipFree(p);
+    if (e->stage) (void)hipHostFree(e->stage);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+    return rc;
+  };
+  const size_t B = static_cast<size_t>(batch), S = max_seq;
+  int rc = EF_HIP_OK;
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup_fail(fail(EF_HIP_ERUNTIME, "engine stream"));
+  if ((rc = dev_alloc(e, &e->x, B * c.D)) || (rc = dev_alloc(e, &e->q, B * c.D)) ||
+      (rc = dev_alloc(e, &e->knew, B * kvd)) || (rc = dev_alloc(e, &e->vnew, B * kvd)) ||
+      (rc = dev_alloc(e, &e->ctx, B * c.D)) || (rc = dev_alloc(e, &e->act, B * c.F)) ||
+      (rc = dev_alloc(e, &e->logits, B * c.V)) || (rc = dev_alloc(e, &e->hidden, B * c.D)) ||
+      (rc = dev_alloc(e, &e->kc, c.L * B * S * kvd)) || (rc = dev_alloc(e, &e->vc, c.L * B * S * kvd)) ||
+      (rc = dev_alloc(e, &e->cos_t, S * c.hd / 2)) || (rc = dev_alloc(e, &e->sin_t, S * c.hd / 2)) ||
+      (rc = dev_alloc(e, &e->hist, B * S)) || (rc = dev_alloc(e, &e->hist_len, B)) ||
+      (rc = dev_alloc(e, &e->next_tok, B)) || (rc = dev_alloc(e, &e->pos, 1)) ||
+      (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S))) {
+    return cleanup_fail(rc);
+  }
+  void* ws = nullptr;
+  if (hipMalloc(&ws, sample_workspace_stride(static_cast<int>(c.V)) * B) != hipSuccess)
+    return cleanup_fail(fail(EF_HIP_ENOMEM, "engine sampler workspace"));
+  e->allocs.push_back(ws);
+  e->sample_ws = ws;
+  if (hipHostMalloc(reinterpret_cast<void**>(&e->stage), (B * S + 8) * sizeof(int32_t), hipHostMallocDefault) !=
+      hipSuccess)
+    return cleanup_fail(fail(EF_HIP_ENOMEM, "engine pinned staging"));
+  // RoPE tables exactly as kern::RopeTable builds them (src/kernels.cpp:113-131): float pow / cos /
+  // sin from the host C library, so the device sees the reference's bits.
+  const size_t half = c.hd / 2;
+  std::vector<float> inv(half), ct(S * half), st(S * half);
+  for (size_t i = 0; i < half; ++i) {
+    const float expo = static_cast<float>(2 * i) / static_cast<float>(c.hd);
+    inv[i] = 1.0f / std::pow(c.rope_theta, expo);
+  }
+  for (size_t p = 0; p < S; ++p) {
+    for (size_t i = 0; i < half; ++i) {
+      const float ang = static_cast<float>(p) * inv[i];
+      ct[p * half + i] = std::cos(ang);
+      st[p * half + i] = std::sin(ang);
+    }
+  }
+  hipError_t he = hipMemcpyAsync(e->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, e->stream);
+  if (he == hipSuccess) he = hipMemcpyAsync(e->sin_t, st.data(), st.size() * 4, hipMemcpyHostToDevice, e->stream);
+  if (he == hipSuccess) he = hipMemsetAsync(e->kc, 0, c.L * B * S * kvd * 4, e->stream);
+  if (he == hipSuccess) he = hipMemsetAsync(e->vc, 0, c.L * B * S * kvd * 4, e->stream);
+  if (he == hipSuccess) he = hipMemsetAsync(e->hist, 0, B * S * 4, e->stream);
+  if (he == hipSuccess) he = hipMemsetAsync(e->pos, 0, 4, e->stream);
+  if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
+  if (he != hipSuccess) return cleanup_fail(fail_hip(he, "engine init"));
+  e->magic = kEngineMagic;
+  *out = e;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_destroy(ef_hip_engine e) {
+  EFH_RC(check_engine(e));
+  e->magic = 0;
+  (void)hipStreamSynchronize(e->stream);
+  for (auto& kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+  for (void* p : e->allocs) (void)hipFree(p);
+  if (e->stage) (void)hipHostFree(e->stage);
+  (void)hipStreamDestroy(e->stream);
+  delete e;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens, size_t pos, int compute_logits) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(tokens != nullptr, "engine_forward: null tokens");
+  for (int b = 0; b < e->B; ++b) {  // src/model.cpp:185-195
+    if (tokens[b] < 0 || static_cast<size_t>(tokens[b]) >= e->c.V)
+      return fail(EF_HIP_EINVAL, "forward: token id " + std::to_string(tokens[b]) + " is outside [0, " +
+                                     std::to_string(e->c.V) + ")");
+  }
+  if (pos >= e->max_seq)
+    return fail(EF_HIP_EINVAL, "forward: position " + std::to_string(pos) + " exceeds the KV-cache capacity " +
+                                   std::to_string(e->max_seq));
+  if (pos > e->cached)
+    return fail(EF_HIP_EINVAL, "forward: position " + std::to_string(pos) + " skips ahead of the " +
+                                   std::to_string(e->cached) + " cached tokens");
+  for (int b = 0; b < e->B; ++b) e->stage[b] = tokens[b];
+  e->stage[e->B] = static_cast<int32_t>(pos);
+  const size_t S = e->max_seq;
+  EFH_HIP(hipMemcpy2DAsync(e->hist + pos, S * 4, e->stage, 4, 4, e->B, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(e->pos, e->stage + e->B, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_RC(run_step(e, compute_logits ? kLogits : 0));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->cached = pos + 1;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_logits(ef_hip_engine e, const float** logits) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(logits != nullptr, "engine_logits: null out pointer");
+  *logits = e->logits;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_hidden(ef_hip_engine e, const float** hidden) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(hidden != nullptr, "engine_hidden: null out pointer");
+  EFH_RC(launch_rmsnorm(e->x, e->final_norm, e->c.eps, static_cast<int>(e->c.D), static_cast<long>(e->c.D), e->B,
+                        e->hidden, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  *hidden = e->hidden;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prompt, size_t n,
+                           const ef_hip_sampler_config* cfg, void* rng, int32_t* tokens_out, double* prefill_s,
+                           double* decode_s) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(prompt && tokens_out, "engine_generate: null argument");
+  if (n_prompt == 0) return fail(EF_HIP_EINVAL, "generate: empty prompt");  // src/model.cpp:280
+  EFH_CHECK(n >= 1, "generate: n must be >= 1");
+  if (n_prompt + n > e->max_seq)
+    return fail(EF_HIP_EINVAL, "generate: prompt (" + std::to_string(n_prompt) + ") + max_new (" + std::to_string(n) +
+                                   ") exceeds the KV-cache capacity " + std::to_string(e->max_seq));
+  const int B = e->B;
+  const size_t S = e->max_seq;
+  for (size_t i = 0; i < n_prompt * B; ++i) {
+    if (prompt[i] < 0 || static_cast<size_t>(prompt[i]) >= e->c.V)
+      return fail(EF_HIP_EINVAL, "generate: prompt token " + std::to_string(prompt[i]) + " out of range");
+  }
+  int pick = kGreedy;
+  if (cfg != nullptr) {
+    EFH_CHECK(cfg->temperature <= 0.0f || rng != nullptr, "generate: sampling needs rng states");
+    const bool same = e->rng == rng && e->scfg.temperature == cfg->temperature && e->scfg.top_k == cfg->top_k &&
+                      e->scfg.top_p == cfg->top_p && e->scfg.repetition_penalty == cfg->repetition_penalty;
+    if (!same) EFH_RC(drop_graph(e, kLogits | kSample));
+    e->scfg = *cfg;
+    e->rng = rng;
+    pick = kSample;
+  }
+  // history <- prompt, hist_len <- n_prompt, position 0
+  for (int b = 0; b < B; ++b) {
+    for (size_t p = 0; p < n_prompt; ++p) e->stage[b * n_prompt + p] = prompt[b * n_prompt + p];
+  }
+  EFH_HIP(hipMemcpy2DAsync(e->hist, S * 4, e->stage, n_prompt * 4, n_prompt * 4, B, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  for (int b = 0; b < B; ++b) e->stage[b] = static_cast<int32_t>(n_prompt);
+  e->stage[B] = 0;
+  e->stage[B + 1] = static_cast<int32_t>(n_prompt);
+  EFH_HIP(hipMemcpyAsync(e->hist_len, e->stage, B * 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(e->pos, e->stage + B, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(e->n_prompt, e->stage + B + 1, 4, hipMemcpyHostToDevice, e->stream));
+  // instantiate the graphs before the clock starts
+  hipGraphExec_t g_pre, g_dec;
+  EFH_RC(graph_for(e, kAdvance, &g_pre));
+  EFH_RC(graph_for(e, kLogits | pick, &g_dec));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  using Clock = std::chrono::steady_clock;
+  const auto t0 = Clock::now();
+  for (size_t p = 0; p + 1 < n_prompt; ++p) EFH_HIP(hipGraphLaunch(g_pre, e->stream));
+  EFH_HIP(hipGraphLaunch(g_dec, e->stream));  // last prompt position: logits and the first pick
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const auto t1 = Clock::now();
+  for (size_t k = 1; k < n; ++k) EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const auto t2 = Clock::now();
+  EFH_HIP(hipMemcpy2DAsync(tokens_out, n * 4, e->out_tokens, S * 4, n * 4, B, hipMemcpyDeviceToHost, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->cached = n_prompt + n - 1;
+  if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
+  if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
+  return EF_HIP_OK;
+}
+
+}  // extern "C"

@@ -14,6 +14,7 @@ struct GemvJob {
   const ef_hip_weight_s* W2 = nullptr;
   const float* x = nullptr;
   float* y = nullptr;
+  size_t ldx = 0, ldy = 0;  // per-job batch strides in floats; 0 = the launch's ldx / ldy
 };
 
 // All jobs of one launch share cols, the epilogue and the optional input RMSNorm (norm_w != null:

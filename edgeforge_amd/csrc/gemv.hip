@@ -40,13 +40,13 @@ struct JobDev {
   int rows_per_tile;
   int tile_begin;
   int row_bytes;
+  long ldx, ldy;
 };
 
 struct Args {
   JobDev job[kMaxJobs];
   int n_jobs;
   int K;
-  long ldx, ldy;
   const float* norm_w;
   float eps;
 };
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(Args a) {
   float* lds_xs = lds + np * kSlot;
   const int tile = blockIdx.x, b = blockIdx.y;
   const JobDev jb = find_job(a, tile);
-  stage_x(jb.x + b * a.ldx, a.norm_w, a.eps, K, lds_x, lds_xs, red);
+  stage_x(jb.x + b * jb.ldx, a.norm_w, a.eps, K, lds_x, lds_xs, red);
 
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int grp = lane / G, t = lane % G;
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(Args a) {
       rows_dot_pairs<EF_QTYPE_Q8_0, G, R>(jb.W2 + row0 * rb, jb.row_bytes, np, t, nvalid, lds_x, lds_xs, acc2);
   }
   if (t != 0) return;
-  float* y = jb.y + b * a.ldy + row0;
+  float* y = jb.y + b * jb.ldy + row0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r >= nvalid) break;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(Args a) {
   float* lds_xs = lds + nslot * kSlot;
   const int tile = blockIdx.x, b = blockIdx.y;
   const JobDev jb = find_job(a, tile);
-  stage_x(jb.x + b * a.ldx, a.norm_w, a.eps, K, lds_x, lds_xs, red);
+  stage_x(jb.x + b * jb.ldx, a.norm_w, a.eps, K, lds_x, lds_xs, red);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int row = (tile - jb.tile_begin) * jb.rows_per_tile + wave;
   if (row >= jb.rows) return;
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(Args a) {
   float v2 = 0.0f;
   if (EPI == kEpiSwiglu) v2 = row_dot_generic(jb.W2 + row * rb, jb.qtype, nb, lds_x, lds_xs, lane);
   if (lane != 0) return;
-  float* y = jb.y + b * a.ldy + row;
+  float* y = jb.y + b * jb.ldy + row;
   if (EPI == kEpiResidual) {
     *y = *y + v;
   } else if (EPI == kEpiSwiglu) {
@@ -363,14 +363,14 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     }
   }
   if (batch > 1) {
-    EFH_CHECK(ldx >= K, "gemv: ldx smaller than cols");
-    for (int j = 0; j < n_jobs; ++j) EFH_CHECK(ldy >= jobs[j].W->rows, "gemv: ldy smaller than rows");
+    for (int j = 0; j < n_jobs; ++j) {
+      EFH_CHECK((jobs[j].ldx ? jobs[j].ldx : ldx) >= K, "gemv: ldx smaller than cols");
+      EFH_CHECK((jobs[j].ldy ? jobs[j].ldy : ldy) >= jobs[j].W->rows, "gemv: ldy smaller than rows");
+    }
   }
   Args a{};
   a.n_jobs = n_jobs;
   a.K = static_cast<int>(K);
-  a.ldx = static_cast<long>(ldx);
-  a.ldy = static_cast<long>(ldy);
   a.norm_w = norm_w;
   a.eps = eps;
   const bool fast = K % 64 == 0;
@@ -401,6 +401,8 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     d.rows = static_cast<int>(W->rows);
     d.qtype = W->qtype;
     d.row_bytes = static_cast<int>(W->row_bytes);
+    d.ldx = static_cast<long>(jobs[j].ldx ? jobs[j].ldx : ldx);
+    d.ldy = static_cast<long>(jobs[j].ldy ? jobs[j].ldy : ldy);
     d.rows_per_tile = fast ? kWaves * (kWave / G) * R : kWaves;
     d.tile_begin = tiles;
     tiles += (d.rows + d.rows_per_tile - 1) / d.rows_per_tile;

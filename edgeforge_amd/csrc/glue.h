@@ -1,0 +1,32 @@
+// Launchers of the decode-step glue kernels (glue.hip).
+#pragma once
+
+#include "common.h"
+
+namespace efh {
+
+struct AttnArgs {
+  const float* q;       // [batch][ldq] un-roped queries (H * hd)
+  const float* knew;    // [batch][KV * hd] un-roped keys of the current position
+  const float* vnew;    // [batch][KV * hd]
+  float* kcache;        // this layer: [batch][max_seq][KV * hd] (roped keys)
+  float* vcache;        // this layer: [batch][max_seq][KV * hd]
+  const float* cos_t;   // [max_seq][hd / 2]
+  const float* sin_t;
+  const int32_t* pos_dev;
+  float* ctx;           // [batch][ldq]
+  long ldq;
+  int H, KV, hd, max_seq;
+  float scale;          // float(1 / sqrt(hd))
+};
+
+int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
+                    float* out, long ldo, hipStream_t s);
+size_t attention_lds_bytes(int hd, int max_seq);
+int launch_attention(const AttnArgs& a, int batch, hipStream_t s);
+int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, int batch, float* out, hipStream_t s);
+int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_ld, int32_t* hist_len, int32_t* out,
+                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s);
+int launch_advance(int32_t* pos_dev, hipStream_t s);
+
+}  // namespace efh

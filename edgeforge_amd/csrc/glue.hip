@@ -1,0 +1,209 @@
+// The FP32 "glue" of one decode step that is not a packed GEMV (src/kernels.cpp, src/model.cpp):
+// embedding row lookup at the current position, RoPE + GQA attention over the KV cache, the
+// final RMSNorm output, and the bookkeeping that feeds a picked token back as the next input.
+// Positions and token ids are read from device memory so one captured HIP graph serves every step.
+//
+// Arithmetic follows the reference's operation order with contraction off: the per-position dot
+// product uses the 8-way partial sums of kern::dot_f32 (src/kernels.cpp:27-43), softmax subtracts
+// the max, uses float exp and a double sum (:77-92), and each output dimension accumulates p * v
+// over positions in order (:168-172).
+#include <cmath>
+
+#include "glue.h"
+
+#pragma clang fp contract(off)
+
+namespace efh {
+namespace {
+
+constexpr int kAttnThreads = 256;
+
+__device__ __forceinline__ float decode_elem(const uint8_t* row, int qtype, long c) {
+  if (qtype == EF_QTYPE_F32) return reinterpret_cast<const float*>(row)[c];
+  if (qtype == EF_QTYPE_BF16) return __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(row)[c]) << 16);
+  if (qtype == EF_QTYPE_F16) return half_bits_to_float(reinterpret_cast<const uint16_t*>(row)[c]);
+  const long blk = c >> 5, j = c & 31;
+  if (qtype == EF_QTYPE_Q4_0) {
+    const uint8_t* p = row + blk * 18;
+    const float d = half_bits_to_float(static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8));
+    const int code = j < 16 ? (p[2 + j] & 15) : (p[2 + j - 16] >> 4);
+    return static_cast<float>(code - 8) * d;
+  }
+  const uint8_t* p = row + blk * 34;
+  const float d = half_bits_to_float(static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8));
+  return static_cast<float>(static_cast<int8_t>(p[2 + j])) * d;
+}
+
+// x[b] = row hist[b][pos] of the embedding table (kern::row_f32 / embedding_bf16).
+__global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long rows, long cols, long rb,
+                                const int32_t* __restrict__ hist, long hist_ld, const int32_t* __restrict__ pos_dev,
+                                float* __restrict__ out, long ldo) {
+  const int b = blockIdx.y;
+  const int32_t id = hist[b * hist_ld + *pos_dev];
+  const bool ok = id >= 0 && id < rows;
+  const uint8_t* row = W + (ok ? id : 0) * rb;
+  for (long c = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols;
+       c += static_cast<long>(gridDim.x) * blockDim.x) {
+    out[b * ldo + c] = ok ? decode_elem(row, qtype, c) : __int_as_float(0x7FC00000);
+  }
+}
+
+// One (query head h, sequence b) per workgroup: RoPE on q and on the new k (half-split pairs,
+// src/kernels.cpp:133-146), the new k / v written into the cache at pos by the first head of each
+// KV group, then causal attention over positions 0..pos (positions < pos from the cache, pos from
+// registers, so no head waits on another).
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int h = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
+  const int pos = *a.pos_dev, n_pos = pos + 1;
+  const int g = h / (a.H / a.KV), kvd = a.KV * hd;
+  float* qs = sm;              // [hd]
+  float* kn = sm + hd;         // [hd] roped new k
+  float* sc = sm + 2 * hd;     // [n_pos] scores / probabilities
+  double* red = reinterpret_cast<double*>(sm + 2 * hd + ((a.max_seq + 1) & ~1));
+  const float* cr = a.cos_t + static_cast<long>(pos) * half;
+  const float* sr = a.sin_t + static_cast<long>(pos) * half;
+  const float* q = a.q + static_cast<long>(b) * a.ldq + h * hd;
+  const float* k_new = a.knew + static_cast<long>(b) * kvd + g * hd;
+  const float* v_new = a.vnew + static_cast<long>(b) * kvd + g * hd;
+  float* kc = a.kcache + (static_cast<long>(b) * a.max_seq) * kvd;  // this layer, this sequence
+  float* vc = a.vcache + (static_cast<long>(b) * a.max_seq) * kvd;
+  const int t = threadIdx.x;
+  if (t < half) {
+    const float qa = q[t], qb = q[t + half], ka = k_new[t], kb = k_new[t + half];
+    qs[t] = qa * cr[t] - qb * sr[t];
+    qs[t + half] = qb * cr[t] + qa * sr[t];
+    kn[t] = ka * cr[t] - kb * sr[t];
+    kn[t + half] = kb * cr[t] + ka * sr[t];
+  }
+  __syncthreads();
+  if (h % (a.H / a.KV) == 0) {  // the group's first head publishes k / v at pos for later steps
+    for (int i = t; i < hd; i += blockDim.x) {
+      kc[static_cast<long>(pos) * kvd + g * hd + i] = kn[i];
+      vc[static_cast<long>(pos) * kvd + g * hd + i] = v_new[i];
+    }
+  }
+  // scores: kern::dot_f32 order (8 partial sums, pairwise), times the 1/sqrt(hd) scale
+  for (int tp = t; tp < n_pos; tp += blockDim.x) {
+    const float* kt = tp == pos ? kn : kc + static_cast<long>(tp) * kvd + g * hd;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int i = 0;
+    for (; i + 8 <= hd; i += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] += qs[i + k] * kt[i + k];
+    }
+    for (; i < hd; ++i) acc[0] += qs[i] * kt[i];
+    sc[tp] = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) * a.scale;
+  }
+  __syncthreads();
+  // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
+  float mx = -INFINITY;
+  for (int tp = t; tp < n_pos; tp += blockDim.x) mx = fmaxf(mx, sc[tp]);
+  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = mx;
+  __syncthreads();
+  mx = static_cast<float>(red[0]);
+  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) mx = fmaxf(mx, static_cast<float>(red[w]));
+  __syncthreads();
+  double s = 0.0;
+  for (int tp = t; tp < n_pos; tp += blockDim.x) {
+    const float e = expf(sc[tp] - mx);
+    sc[tp] = e;
+    s += static_cast<double>(e);
+  }
+  s = wave_sum_d(s);
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
+  __syncthreads();
+  double tot = 0.0;
+  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) tot += red[w];
+  const float inv = static_cast<float>(1.0 / tot);
+  // out[d] = sum_t p_t v_t[d], positions in order
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + h * hd;
+  for (int d = t; d < hd; d += blockDim.x) {
+    float o = 0.0f;
+    for (int tp = 0; tp < n_pos; ++tp) {
+      const float p = sc[tp] * inv;
+      const float v = tp == pos ? v_new[d] : vc[static_cast<long>(tp) * kvd + g * hd + d];
+      o += p * v;
+    }
+    out[d] = o;
+  }
+}
+
+// out[b] = w * (x[b] * rsqrt(mean(x[b]^2) + eps)) (kern::rmsnorm).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      float eps, int n, long ld, float* __restrict__ out) {
+  __shared__ double red[4];
+  const float* xb = x + blockIdx.x * ld;
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ss += static_cast<double>(xb[i]) * static_cast<double>(xb[i]);
+  ss = wave_sum_d(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(n) + static_cast<double>(eps)));
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[blockIdx.x * ld + i] = w[i] * (xb[i] * inv);
+}
+
+// After a token is picked at position p for every sequence: it becomes the input at p + 1, joins
+// the history, lands in the output list at p - (n_prompt - 1), and the position advances.
+__global__ void finish_step_kernel(const int32_t* __restrict__ next, int batch, int32_t* hist, long hist_ld,
+                                   int32_t* hist_len, int32_t* out, long out_ld, const int32_t* n_prompt_dev,
+                                   int32_t* pos_dev) {
+  const int p = *pos_dev;
+  const int k = p - (*n_prompt_dev - 1);
+  for (int b = threadIdx.x; b < batch; b += blockDim.x) {
+    const int32_t tok = next[b];
+    if (p + 1 < hist_ld) hist[b * hist_ld + p + 1] = tok;
+    hist_len[b] = p + 2 < hist_ld ? p + 2 : static_cast<int32_t>(hist_ld);
+    if (k >= 0 && k < out_ld) out[b * out_ld + k] = tok;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *pos_dev = p + 1;
+}
+
+__global__ void advance_kernel(int32_t* pos_dev) { *pos_dev += 1; }
+
+}  // namespace
+
+int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
+                    float* out, long ldo, hipStream_t s) {
+  const unsigned gx = static_cast<unsigned>(std::min<size_t>((W->cols + 255) / 256, 16));
+  hipLaunchKernelGGL(embed_at_kernel, dim3(gx, batch), dim3(256), 0, s, W->dev, W->qtype, static_cast<long>(W->rows),
+                     static_cast<long>(W->cols), static_cast<long>(W->row_bytes), hist, hist_ld, pos_dev, out, ldo);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+size_t attention_lds_bytes(int hd, int max_seq) {
+  return (2 * static_cast<size_t>(hd) + ((max_seq + 1) & ~1)) * sizeof(float) + 4 * sizeof(double);
+}
+
+int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
+  const size_t lds = attention_lds_bytes(a.hd, a.max_seq);
+  hipLaunchKernelGGL(attention_kernel, dim3(a.H, batch), dim3(kAttnThreads), lds, s, a);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, int batch, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(batch), dim3(256), 0, s, x, w, eps, n, ld, out);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_ld, int32_t* hist_len, int32_t* out,
+                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s) {
+  hipLaunchKernelGGL(finish_step_kernel, dim3(1), dim3(256), 0, s, next, batch, hist, hist_ld, hist_len, out, out_ld,
+                     n_prompt_dev, pos_dev);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_advance(int32_t* pos_dev, hipStream_t s) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pos_dev);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+}  // namespace efh

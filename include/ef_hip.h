@@ -110,6 +110,12 @@ int ef_hip_rows_f32(ef_hip_weight W, const int32_t* ids_dev, int batch, float* o
  * rows; byte-identical to the reference's quantize_row (search = the reference's Q4 scale search). */
 int ef_hip_quantize(int qtype, const float* w_dev, size_t rows, size_t cols, int search, void* out_dev, void* stream);
 
+/* ---- synthetic inputs (no reference counterpart: the reference reads real checkpoints) -------
+ * out[i] = mean + scale * z_i, z_i ~ N(0,1) from Philox4x32-10 and Box-Muller; deterministic in
+ * (seed, offset, i).  Builds the benchmark's random-init weights and activations on the device. */
+int ef_hip_fill_normal(float* out_dev, size_t n, uint64_t seed, uint64_t offset, float mean, float scale,
+                       void* stream);
+
 /* ---- sampler ----------------------------------------------------------------------------------
  * ef::SamplerConfig (include/ef/sampler.h:13-19) and Sampler::sample (src/sampler.cpp:13-70) for
  * `batch` independent sequences: logits [batch][ld] on the device; history [batch][hist_ld] int32
@@ -133,6 +139,15 @@ int ef_hip_sample(const float* logits_dev, size_t vocab, int batch, size_t ld, c
                   int32_t* out_dev, void* ws_dev, void* stream);
 /* kern::argmax (src/kernels.cpp:105-111): first maximum wins. */
 int ef_hip_argmax(const float* x_dev, size_t n, int batch, size_t ld, int32_t* out_dev, void* stream);
+
+/* ---- profiling (the reference's per-op timing, src/bench_decode.cpp:164-231) -------------------
+ * Launches `launches` GEMVs back to back on `stream`, cycling over n_weights weight handles (so the
+ * matrices come from HBM, not the 256 MB Infinity Cache), bracketed by HIP events on that stream;
+ * *avg_ms is the mean time per launch.  epi: 0 = y = W x, 1 = y += W x, 2 = y = silu(W x)*(W2 x)
+ * (W2 then holds n_weights up matrices); norm_w_dev as in ef_hip_matvec_swiglu. */
+int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* W2, size_t n_weights,
+                          const float* x_dev, const float* norm_w_dev, float eps, float* y_dev, int batch,
+                          int launches, void* stream, float* avg_ms);
 
 /* ---- decode engine ----------------------------------------------------------------------------
  * Transformer::forward (src/model.cpp:184-276) on the device for `batch` independent sequences

@@ -1,0 +1,88 @@
+"""The CPU oracle's transformer over the packed bytes of a device model (TEST INFRASTRUCTURE ONLY:
+tests, smoke() and bench.py's cpu_baseline leg)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+import oracle as O
+from edgeforge_amd.model import LAYER_MATS, DeviceModel
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+class OracleModel:
+    """efo_model over host copies of the device model's packed weights and norms."""
+
+    def __init__(self, dm: DeviceModel):
+        cfg = dm.cfg
+        self.cfg = cfg
+        self.keep = []
+        layers = (O.efo_layer * cfg.L)()
+        for l in range(cfg.L):
+            ws = []
+            for n in LAYER_MATS:
+                b = dm.host_bytes((l, n))
+                w = dm.weights[(l, n)]
+                self.keep.append(b)
+                ws.append(O.weight(w.qtype, b, w.rows, w.cols))
+            an, fn = dm.host_norm((l, "attn")), dm.host_norm((l, "ffn"))
+            self.keep += [an, fn]
+            layers[l] = O.efo_layer(*ws, O.ptr(an, O._f32p), O.ptr(fn, O._f32p))
+        eb, lb, fnorm = dm.host_bytes("embed"), dm.host_bytes("lm_head"), dm.host_norm("final")
+        self.keep += [eb, lb, fnorm, layers]
+        e, lm = dm.weights["embed"], dm.weights["lm_head"]
+        c = O.efo_config(cfg.D, cfg.F, cfg.H, cfg.KV, cfg.hd, cfg.V, cfg.L, cfg.max_pos, cfg.eps, cfg.rope_theta)
+        self.m = O.efo_model(c, O.weight(e.qtype, eb, e.rows, e.cols), O.weight(lm.qtype, lb, lm.rows, lm.cols),
+                             O.ptr(fnorm, O._f32p), layers)
+
+    def run_once(self, prompt, n: int, threads: int | None = None, backend: int = O.AVX2):
+        """Reference decode protocol: (tokens [n], logits [n][V], prefill_s, decode_s)."""
+        prompt = np.ascontiguousarray(np.asarray(prompt, np.int32))
+        toks = np.empty(n, np.int32)
+        logits = np.empty((n, self.cfg.V), np.float32)
+        pre, dec = C.c_double(), C.c_double()
+        pool = O.Pool(threads or cpu_threads())
+        rc = O.lib().efo_run_once(C.byref(self.m), O.ptr(prompt, O._i32p), prompt.size, n, pool.h, backend,
+                                  O.ptr(toks, O._i32p), O.ptr(logits, O._f32p), C.byref(pre), C.byref(dec))
+        pool.close()
+        assert rc == 0
+        return toks, logits, pre.value, dec.value
+
+    def transformer(self, max_seq: int, threads: int | None = None, backend: int = O.AVX2):
+        return OracleTransformer(self, max_seq, threads or cpu_threads(), backend)
+
+
+class OracleTransformer:
+    def __init__(self, om: OracleModel, max_seq: int, threads: int, backend: int):
+        self.om = om
+        self.pool = O.Pool(threads)
+        self.t = O.lib().efo_transformer_create(C.byref(om.m), max_seq, self.pool.h, backend)
+        assert self.t
+
+    def forward(self, token: int, pos: int, compute_logits: bool = True):
+        err = C.c_int()
+        p = O.lib().efo_transformer_forward(self.t, token, pos, int(compute_logits), C.byref(err))
+        if err.value:
+            raise ValueError("forward rejected the token or position")
+        if not compute_logits:
+            return None
+        return np.ctypeslib.as_array(p, shape=(self.om.cfg.V,)).copy()
+
+    def hidden(self) -> np.ndarray:
+        p = O.lib().efo_transformer_hidden(self.t)
+        return np.ctypeslib.as_array(p, shape=(self.om.cfg.D,)).copy()
+
+    def close(self):
+        if self.t:
+            O.lib().efo_transformer_destroy(self.t)
+            self.t = None
+        self.pool.close()
