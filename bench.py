@@ -123,6 +123,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--batch64", type=int, default=64, help="sequences of the batched decode line (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-kernel", action="store_true",
+                    help="profiling mode: a 256 MiB device copy (counter calibration), then only the rotating "
+                         "gate/up GEMV launches; prints their average time")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -141,6 +144,15 @@ def main() -> int:
     model = DeviceModel.synthetic(TINYLLAMA, seed=2024)
     log(f"[bench] synthetic TinyLlama-1.1B built and quantized on the device in {time.time() - t0:.1f}s")
     wbytes = TINYLLAMA.weight_bytes_per_token()
+    if args.only_kernel:
+        n = 256 << 20
+        a, b = H.DeviceArray((n,), np.uint8), H.DeviceArray((n,), np.uint8)
+        L.call("ef_hip_memcpy_d2d", b.ptr, a.ptr, n, None)
+        H.sync()
+        avg_ms, nbytes, reps = profile_gate_up(H, L, model, batch=1)
+        print(json.dumps({"copy_bytes": n, "gate_up_avg_us": round(avg_ms * 1e3, 3), "bytes_per_launch": nbytes,
+                          "replicas": reps}), flush=True)
+        return 0
     rng = np.random.default_rng(23)
     prompt = rng.integers(0, TINYLLAMA.V, 23).astype(np.int32)
 
