@@ -4,6 +4,7 @@
 // The quantizer is the reference's per-block algorithm (src/quant.cpp:26-99, 151-175), one thread
 // per 32-weight block, written so every float and double operation is the same IEEE operation in
 // the same order (correctly rounded divides, no contraction), so the packed bytes are identical.
+#include <climits>
 #include <cmath>
 
 #include "codec.h"
@@ -45,11 +46,15 @@ __device__ float fp16_round(float d) { return half_bits_to_float(f32_to_fp16_bit
 
 __device__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+// static_cast<int>(float) as the reference's x86-64 build executes it (cvttss2si): NaN and
+// out-of-range values give INT_MIN ("integer indefinite"); v_cvt_i32_f32 would saturate instead.
+__device__ int to_int_x86(float v) { return fabsf(v) < 2147483648.0f ? static_cast<int>(v) : INT_MIN; }
+
 __device__ double q4_try(const float* x, float d, uint8_t* codes) {
   const float inv = __fdiv_rn(1.0f, d);
   double sse = 0.0;
   for (int j = 0; j < 32; ++j) {
-    const int c = clampi(static_cast<int>(rintf(x[j] * inv)) + 8, 0, 15);
+    const int c = clampi(to_int_x86(rintf(x[j] * inv)) + 8, 0, 15);
     codes[j] = static_cast<uint8_t>(c);
     const double e = static_cast<double>(x[j]) - static_cast<double>(static_cast<float>(c - 8) * d);
     sse += e * e;
@@ -148,7 +153,7 @@ __global__ void quantize_blocks_kernel(int qtype, const float* __restrict__ w, l
     o[1] = static_cast<uint8_t>(h >> 8);
     const float inv = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
     for (int j = 0; j < 32; ++j) {
-      o[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(clampi(static_cast<int>(rintf(x[j] * inv)), -127, 127)));
+      o[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(clampi(to_int_x86(rintf(x[j] * inv)), -127, 127)));
     }
   }
 }

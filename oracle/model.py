@@ -8,7 +8,7 @@ import os
 import numpy as np
 
 import oracle as O
-from edgeforge_amd.model import LAYER_MATS, DeviceModel
+LAYER_MATS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
 
 
 def cpu_threads() -> int:
@@ -20,9 +20,9 @@ def cpu_threads() -> int:
 
 
 class OracleModel:
-    """efo_model over host copies of the device model's packed weights and norms."""
+    """efo_model over host copies of a model's packed weights and norms (DeviceModel or HostModel)."""
 
-    def __init__(self, dm: DeviceModel):
+    def __init__(self, dm):
         cfg = dm.cfg
         self.cfg = cfg
         self.keep = []
@@ -86,3 +86,48 @@ class OracleTransformer:
             O.lib().efo_transformer_destroy(self.t)
             self.t = None
         self.pool.close()
+
+
+class _W:
+    def __init__(self, qtype, rows, cols):
+        self.qtype, self.rows, self.cols = qtype, rows, cols
+
+
+class HostModel:
+    """A synthetic model built on the host with the oracle's quantizer (CPU-only tests): the same
+    accessors as edgeforge_amd.model.DeviceModel (weights[key] -> qtype/rows/cols, host_bytes,
+    host_norm).  Weights N(0, std), norms 1 + 0.1 N(0, 1), from numpy's PCG64 with `seed`."""
+
+    def __init__(self, cfg, seed: int, q8=(), std: float = 0.02, layer_type: int = O.Q4_0,
+                 lm_type: int = O.Q8_0, embed_type: int = O.BF16, keep_floats: bool = False):
+        g = np.random.default_rng(seed)
+        self.cfg = cfg
+        self.weights, self._bytes, self._norms, self._floats = {}, {}, {}, {}
+
+        def pack(key, qt, rows, cols):
+            w = (g.standard_normal((rows, cols), dtype=np.float32) * np.float32(std)).astype(np.float32)
+            if keep_floats:
+                self._floats[key] = w
+            self._bytes[key] = O.quantize(qt, w)
+            self.weights[key] = _W(qt, rows, cols)
+
+        pack("embed", embed_type, cfg.V, cfg.D)
+        for l in range(cfg.L):
+            for n in LAYER_MATS:
+                rows, cols = cfg.shape(n)
+                pack((l, n), O.Q8_0 if (l, n) in set(q8) else layer_type, rows, cols)
+            for nn in ("attn", "ffn"):
+                self._norms[(l, nn)] = (1.0 + 0.1 * g.standard_normal(cfg.D)).astype(np.float32)
+        self._norms["final"] = (1.0 + 0.1 * g.standard_normal(cfg.D)).astype(np.float32)
+        pack("lm_head", lm_type, cfg.V, cfg.D)
+
+    def host_bytes(self, key):
+        return self._bytes[key]
+
+    def host_norm(self, key):
+        return self._norms[key]
+
+    def efq_tensors(self):
+        t = {k: (self.weights[k].qtype, self._bytes[k]) for k in self._bytes}
+        t.update(self._norms)
+        return t
