@@ -65,6 +65,7 @@ SIGNATURES = {
     "ef_hip_stream_create": (C.c_int, [C.POINTER(_P)]),
     "ef_hip_stream_destroy": (C.c_int, [_P]),
     "ef_hip_stream_sync": (C.c_int, [_P]),
+    "ef_hip_pointer_kind": (C.c_int, [_P, C.POINTER(C.c_int)]),
     "ef_hip_event_create": (C.c_int, [C.POINTER(_P)]),
     "ef_hip_event_destroy": (C.c_int, [_P]),
     "ef_hip_event_record": (C.c_int, [_P, _P]),

@@ -15,6 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libedgeforge_hip.so")
+SHIM = os.path.join(HERE, "libedgeforge_kern.so")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -54,8 +55,16 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # C++ host shim (ef::hip, EdgeForge's signatures) over the C-ABI only: plain g++, no HIP headers
+    shim_src = os.path.join(HERE, "host", "ef_hip_kern.cpp")
+    cmd = ["g++", "-O2", "-std=c++20", "-fPIC", "-shared", "-Wall", "-DEF_HIP_STANDALONE", "-o", SHIM + ".tmp",
+           shim_src, f"-L{HERE}", "-ledgeforge_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host shim build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(SHIM + ".tmp", SHIM)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources and {SHIM}")
     return LIB
 
 

@@ -183,6 +183,21 @@ int ef_hip_stream_sync(void* stream) {
   return EF_HIP_OK;
 }
 
+int ef_hip_pointer_kind(const void* p, int* kind) {
+  EFH_READY();
+  EFH_CHECK(kind != nullptr, "pointer_kind: null out pointer");
+  *kind = 0;
+  if (p == nullptr) return EF_HIP_OK;
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();  // unregistered host memory: not an error for this query
+    return EF_HIP_OK;
+  }
+  if (a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged) *kind = 1;
+  else if (a.type == hipMemoryTypeHost) *kind = 2;
+  return EF_HIP_OK;
+}
+
 int ef_hip_event_create(void** ev) {
   EFH_READY();
   EFH_CHECK(ev != nullptr, "event_create: null out pointer");

@@ -52,6 +52,8 @@ int ef_hip_memset(void* dev, int value, size_t bytes, void* stream);
 int ef_hip_stream_create(void** stream);
 int ef_hip_stream_destroy(void* stream);
 int ef_hip_stream_sync(void* stream);
+/* *kind = 1 when p is device memory, 2 for pinned host memory, 0 otherwise (pageable host). */
+int ef_hip_pointer_kind(const void* p, int* kind);
 /* HIP events, for timing kernels on the stream they run on. */
 int ef_hip_event_create(void** ev);
 int ef_hip_event_destroy(void* ev);

@@ -39,3 +39,17 @@ def test_row_bytes_matches_reference_rule():
     assert lib.ef_hip_row_bytes(L.BF16, 2048, C.byref(out)) == 0 and out.value == 4096
     assert lib.ef_hip_row_bytes(L.Q4_0, 30, C.byref(out)) == L.EINVAL
     assert b"divisible by 32" in lib.ef_hip_last_error()
+
+
+def test_cpp_shim_exports_the_reference_signatures():
+    """libedgeforge_kern.so defines ef::hip::{matvec, matvec_jobs, row_f32, argmax, Sampler::sample}
+    with the reference's parameter lists (checked on the mangled names)."""
+    import subprocess
+    shim = os.path.join(os.path.dirname(L.LIB_PATH), "libedgeforge_kern.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", shim], capture_output=True, text=True).stdout
+    for sig in ("ef::hip::matvec(float*, ef::WeightView const&, float const*, ef::ThreadPool*)",
+                "ef::hip::matvec_jobs(ef::kern::MatvecJob const*, unsigned long, ef::ThreadPool*)",
+                "ef::hip::row_f32(float*, ef::WeightView const&, unsigned long)",
+                "ef::hip::argmax(float const*, unsigned long)",
+                "ef::hip::Sampler::sample(float const*, unsigned long, std::vector<int, std::allocator<int> > const&)"):
+        assert sig in out, sig
