@@ -375,14 +375,22 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
   EFH_HIP(hipEventCreate(&e1));
   int rc = EF_HIP_OK;
   const size_t ldx = W[0]->cols, ldy = W[0]->rows;
+  // batched launches get their activation workspace up front, as the decode engine does
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (batch > 1) {
+    ws_bytes = gemv_mfma_workspace_bytes(batch, ldx, true, true);
+    EFH_HIP(hipMalloc(&ws, ws_bytes));
+  }
   EFH_HIP(hipEventRecord(e0, s));
   for (int i = 0; i < launches && rc == EF_HIP_OK; ++i) {
     const size_t k = static_cast<size_t>(i) % n_weights;
     const GemvJob j{W[k], epi == kEpiSwiglu ? W2[k] : nullptr, x, y};
-    rc = launch_gemv(&j, 1, epi, norm_w, eps, batch, ldx, ldy, s);
+    rc = launch_gemv(&j, 1, epi, norm_w, eps, batch, ldx, ldy, s, ws, ws_bytes);
   }
   EFH_HIP(hipEventRecord(e1, s));
   EFH_HIP(hipEventSynchronize(e1));
+  if (ws != nullptr) (void)hipFree(ws);
   float ms = 0.0f;
   EFH_HIP(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0);

@@ -75,6 +75,22 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
   return static_cast<float>(h);
 }
 
+// Raw buffer resources (CDNA dword-3 format bits for 32-bit raw data).  Accesses at or beyond
+// num_records return zeros without touching memory, so loads through them need no branch and the
+// compiler can count outstanding loads exactly.
+constexpr int kRawBufferFlags = 0x00020000;
+constexpr int kNonTemporal = 2;  // cache policy of streamed, read-once data
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kRawBufferFlags);
+}
+
+__device__ __forceinline__ float4 buf_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

@@ -40,8 +40,11 @@ struct ef_hip_engine_s {
   float *x = nullptr, *q = nullptr, *knew = nullptr, *vnew = nullptr, *ctx = nullptr, *act = nullptr;
   float *logits = nullptr, *hidden = nullptr, *kc = nullptr, *vc = nullptr, *cos_t = nullptr, *sin_t = nullptr;
   int32_t *hist = nullptr, *hist_len = nullptr, *next_tok = nullptr, *pos = nullptr, *n_prompt = nullptr;
+  uint32_t* step_counter = nullptr;  // zero between steps (argmax_finish re-arms it)
   int32_t* out_tokens = nullptr;
   void* sample_ws = nullptr;
+  void* gemv_ws = nullptr;  // prepared activation fragments of the batched GEMVs (B > 1)
+  size_t gemv_ws_bytes = 0;
   int32_t* stage = nullptr;  // pinned host staging
   std::vector<void*> allocs;
   std::map<int, hipGraphExec_t> graphs;
@@ -106,30 +109,32 @@ int enqueue_step(ef_hip_engine e, int mode) {
     const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, D, D},
                             {w.wk, nullptr, e->x, e->knew, D, kvd},
                             {w.wv, nullptr, e->x, e->vnew, D, kvd}};
-    EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, B, D, D, s));
+    EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
     a.kcache = e->kc + l * B * S * kvd;
     a.vcache = e->vc + l * B * S * kvd;
     EFH_RC(launch_attention(a, B, s));
     const GemvJob o{w.wo, nullptr, e->ctx, e->x, D, D};
-    EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, B, D, D, s));
+    EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
     const GemvJob gu{w.w_gate, w.w_up, e->x, e->act, D, F};
-    EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, B, D, F, s));
+    EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, B, D, F, s, e->gemv_ws, e->gemv_ws_bytes));
     const GemvJob dn{w.w_down, nullptr, e->act, e->x, F, D};
-    EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s));
+    EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s, e->gemv_ws, e->gemv_ws_bytes));
   }
   if (mode & kLogits) {
     const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, D, V};
-    EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s));
+    EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s, e->gemv_ws, e->gemv_ws_bytes));
   }
   if (mode & (kGreedy | kSample)) {
     if (mode & kGreedy) {
-      EFH_RC(launch_argmax(e->logits, static_cast<int>(V), static_cast<long>(V), B, e->next_tok, s));
+      StepArgs f{e->next_tok, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens, static_cast<long>(S),
+                 e->n_prompt, e->pos, e->step_counter};
+      EFH_RC(launch_argmax_finish(e->logits, static_cast<int>(V), static_cast<long>(V), B, f, s));
     } else {
       EFH_RC(launch_sample(e->logits, static_cast<int>(V), B, static_cast<long>(V), e->scfg, e->hist, e->hist_len,
                            static_cast<long>(S), e->rng, e->next_tok, e->sample_ws, s));
+      EFH_RC(launch_finish_step(e->next_tok, B, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens,
+                                static_cast<long>(S), e->n_prompt, e->pos, s));
     }
-    EFH_RC(launch_finish_step(e->next_tok, B, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens,
-                              static_cast<long>(S), e->n_prompt, e->pos, s));
   } else if (mode & kAdvance) {
     EFH_RC(launch_advance(e->pos, s));
   }
@@ -190,10 +195,12 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   EFH_CHECK(cfg && layers && out && final_norm, "engine_create: null argument");
   const ef_hip_model_config& c = *cfg;
   EFH_CHECK(c.D > 0 && c.F > 0 && c.H > 0 && c.KV > 0 && c.hd > 0 && c.V > 0 && c.L > 0, "engine_create: zero dim");
-  EFH_CHECK(c.H * c.hd == c.D && c.H % c.KV == 0 && c.hd % 2 == 0 && c.hd <= 512,
-            "engine_create: need H*hd == D, H % KV == 0, even hd <= 512");
+  EFH_CHECK(c.H * c.hd == c.D && c.H % c.KV == 0 && c.hd % 4 == 0 && c.hd <= 256,
+            "engine_create: need H*hd == D, H % KV == 0, hd a multiple of 4 up to 256");
   EFH_CHECK(max_seq > 0 && max_seq <= c.max_pos, "engine_create: max_seq must be in [1, max_position_embeddings]");
-  EFH_CHECK(max_seq <= 12000, "engine_create: max_seq above 12000 (attention scores are held in LDS)");
+  EFH_CHECK(max_seq <= 12000 && attention_lds_bytes(static_cast<int>(c.hd), static_cast<int>(max_seq)) <=
+                                    std::max<size_t>(ctx().lds_per_block, 65536),
+            "engine_create: max_seq too large (attention scores and staged rows are held in LDS)");
   EFH_CHECK(batch >= 1 && batch <= 1024, "engine_create: batch must be in [1, 1024]");
   EFH_CHECK(c.V < 0x7FFFFFFF, "engine_create: vocab too large");
   const size_t kvd = c.KV * c.hd;
@@ -240,7 +247,8 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
       (rc = dev_alloc(e, &e->cos_t, S * c.hd / 2)) || (rc = dev_alloc(e, &e->sin_t, S * c.hd / 2)) ||
       (rc = dev_alloc(e, &e->hist, B * S)) || (rc = dev_alloc(e, &e->hist_len, B)) ||
       (rc = dev_alloc(e, &e->next_tok, B)) || (rc = dev_alloc(e, &e->pos, 1)) ||
-      (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S))) {
+      (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S)) ||
+      (rc = dev_alloc(e, &e->step_counter, 1))) {
     return cleanup_fail(rc);
   }
   void* ws = nullptr;
@@ -248,6 +256,14 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
     return cleanup_fail(fail(EF_HIP_ENOMEM, "engine sampler workspace"));
   e->allocs.push_back(ws);
   e->sample_ws = ws;
+  if (B > 1) {
+    e->gemv_ws_bytes = gemv_mfma_workspace_bytes(B, std::max(c.D, c.F), true, true);
+    void* gw = nullptr;
+    if (hipMalloc(&gw, e->gemv_ws_bytes) != hipSuccess)
+      return cleanup_fail(fail(EF_HIP_ENOMEM, "engine GEMV workspace"));
+    e->allocs.push_back(gw);
+    e->gemv_ws = gw;
+  }
   if (hipHostMalloc(reinterpret_cast<void**>(&e->stage), (B * S + 8) * sizeof(int32_t), hipHostMallocDefault) !=
       hipSuccess)
     return cleanup_fail(fail(EF_HIP_ENOMEM, "engine pinned staging"));
@@ -272,6 +288,7 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   if (he == hipSuccess) he = hipMemsetAsync(e->vc, 0, c.L * B * S * kvd * 4, e->stream);
   if (he == hipSuccess) he = hipMemsetAsync(e->hist, 0, B * S * 4, e->stream);
   if (he == hipSuccess) he = hipMemsetAsync(e->pos, 0, 4, e->stream);
+  if (he == hipSuccess) he = hipMemsetAsync(e->step_counter, 0, 4, e->stream);
   if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
   if (he != hipSuccess) return cleanup_fail(fail_hip(he, "engine init"));
   e->magic = kEngineMagic;

@@ -20,7 +20,21 @@ struct GemvJob {
 // All jobs of one launch share cols, the epilogue and the optional input RMSNorm (norm_w != null:
 // x' = norm_w * (x * rsqrt(mean(x^2) + eps)), kern::rmsnorm order).  batch sequences with row
 // strides ldx / ldy.  Enqueues on `stream`; returns an EF_HIP_* status.
+struct ShapeOverride {
+  int G = 0, R = 0;  // 0: the launcher's own choice
+  int path = 0;      // 0 auto, 1 LDS-DMA kernel, 2 register-fetch kernel
+};
+const ShapeOverride& shape_override();
+bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU kernels
+
+// Matrix-core path for batches of 2 or more sequences (gemv_mfma.hip).  Sets *taken when it enqueued
+// the launches; otherwise the caller uses the vector-ALU kernels.  ws (>= gemv_mfma_workspace_bytes)
+// holds the prepared activation fragments; without it the launch allocates stream-ordered memory.
+size_t gemv_mfma_workspace_bytes(int batch, size_t K, bool q4, bool q8);
+int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
+                     size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
+
 int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
-                size_t ldy, hipStream_t stream);
+                size_t ldy, hipStream_t stream, void* ws = nullptr, size_t ws_bytes = 0);
 
 }  // namespace efh

@@ -18,6 +18,10 @@
 // order differs from the reference's CPU kernels (src/qkernels.cpp:39-65, 131-180) only by
 // rounding; the result is deterministic for a given shape.
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <algorithm>
 
 #include "gemv.h"
 
@@ -49,48 +53,99 @@ struct Args {
   int K;
   const float* norm_w;
   float eps;
+  // LDS layout of the DMA path (byte offsets from the dynamic LDS base)
+  uint32_t raw_x_off, raw_nw_off, w_off, w_stride;
 };
 
 // ---- staging of x in LDS ------------------------------------------------------------------------
 // lds_x: K/64 slots of kSlot floats (a partial last slot for K % 64 == 32); lds_xs: K/32 block sums.
-__device__ void stage_x(const float* __restrict__ x, const float* __restrict__ nw, float eps, int K, float* lds_x,
-                        float* lds_xs, double* red) {
+// Thread t owns the float4s at 4t + 1024k.  The first kXRegs of them (and their norm weights) are
+// requested by xload_issue() before the caller issues its weight loads: vector-memory loads retire
+// in order on CDNA, so loads requested after the weights could only be consumed once every weight
+// load had landed.  xload_finish() then forms the RMSNorm, writes LDS and the block sums (formed in
+// registers: the 8 consecutive threads that store a 32-float block add their partials with lane
+// shuffles).  One barrier without a norm, two with it.
+constexpr int kXRegs = 6;  // K <= 6144 staged from registers; the rest is loaded during staging
+
+struct XLoad {
+  float4 x[kXRegs];
+  float4 w[kXRegs];
+};
+
+// x (and the norm weights: a zero-length resource when there is no norm) for K <= kXRegs*1024.
+__device__ __forceinline__ void xload_issue(const float* __restrict__ x, const float* __restrict__ nw, int K,
+                                            XLoad& r) {
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(K) * 4u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(nw != nullptr ? nw : x, nw != nullptr ? static_cast<uint32_t>(K) * 4u : 0u);
+#pragma unroll
+  for (int k = 0; k < kXRegs; ++k) r.x[k] = buf_f4(rx, (threadIdx.x * 4u + k * kThreads * 4u) * 4u);
+#pragma unroll
+  for (int k = 0; k < kXRegs; ++k) r.w[k] = buf_f4(rw, (threadIdx.x * 4u + k * kThreads * 4u) * 4u);
+}
+
+__device__ __forceinline__ void store_x4(float4 v, int i, float* lds_x, float* lds_xs) {
+  *reinterpret_cast<float4*>(lds_x + (i >> 6) * kSlot + (i & 63)) = v;
+  // K % 32 == 0, so the 8 threads of a block are active together and the xor partners stay
+  // inside the aligned group of 8.
+  float s = (v.x + v.y) + (v.z + v.w);
+  s += __shfl_xor(s, 1, kWave);
+  s += __shfl_xor(s, 2, kWave);
+  s += __shfl_xor(s, 4, kWave);
+  if ((threadIdx.x & 7) == 0) lds_xs[i >> 5] = s;
+}
+
+__device__ __forceinline__ double sq_d(float4 v) {
+  double ss = static_cast<double>(v.x) * static_cast<double>(v.x);
+  ss += static_cast<double>(v.y) * static_cast<double>(v.y);
+  ss += static_cast<double>(v.z) * static_cast<double>(v.z);
+  ss += static_cast<double>(v.w) * static_cast<double>(v.w);
+  return ss;
+}
+
+__device__ __forceinline__ float4 norm4(float4 v, float4 w, float inv) {  // HF order: w * (x * inv)
+  v.x = w.x * (v.x * inv);
+  v.y = w.y * (v.y * inv);
+  v.z = w.z * (v.z * inv);
+  v.w = w.w * (v.w * inv);
+  return v;
+}
+
+__device__ void xload_finish(const float* __restrict__ x, const float* __restrict__ nw, float eps, int K,
+                             const XLoad& r, float* lds_x, float* lds_xs, double* red) {
+  constexpr int kReg = kXRegs * kThreads * 4;
   float inv = 1.0f;
   if (nw != nullptr) {  // kern::rmsnorm: double sum of squares, inv = float(1 / sqrt(mean + eps))
     double ss = 0.0;
-    for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) {
-      const float4 v = *reinterpret_cast<const float4*>(x + i);
-      ss += static_cast<double>(v.x) * static_cast<double>(v.x);
-      ss += static_cast<double>(v.y) * static_cast<double>(v.y);
-      ss += static_cast<double>(v.z) * static_cast<double>(v.z);
-      ss += static_cast<double>(v.w) * static_cast<double>(v.w);
+#pragma unroll
+    for (int k = 0; k < kXRegs; ++k) {
+      const int i = threadIdx.x * 4 + k * kThreads * 4;
+      if (i < K) ss += sq_d(r.x[k]);
     }
+    for (int i = threadIdx.x * 4 + kReg; i < K; i += kThreads * 4) ss += sq_d(*reinterpret_cast<const float4*>(x + i));
     ss = wave_sum_d(ss);
     if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
     __syncthreads();
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
     inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(eps)));
   }
-  for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) {
-    float4 v = *reinterpret_cast<const float4*>(x + i);
-    if (nw != nullptr) {  // HF order: w * (x * inv)
-      const float4 w = *reinterpret_cast<const float4*>(nw + i);
-      v.x = w.x * (v.x * inv);
-      v.y = w.y * (v.y * inv);
-      v.z = w.z * (v.z * inv);
-      v.w = w.w * (v.w * inv);
-    }
-    *reinterpret_cast<float4*>(lds_x + (i >> 6) * kSlot + (i & 63)) = v;
-  }
-  __syncthreads();
-  for (int b = threadIdx.x; b < K / 32; b += kThreads) {
-    const float* s = lds_x + (b >> 1) * kSlot + (b & 1) * 32;
-    float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) acc += s[j];
-    lds_xs[b] = acc;
+  for (int k = 0; k < kXRegs; ++k) {
+    const int i = threadIdx.x * 4 + k * kThreads * 4;
+    if (i < K) store_x4(nw != nullptr ? norm4(r.x[k], r.w[k], inv) : r.x[k], i, lds_x, lds_xs);
+  }
+  for (int i = threadIdx.x * 4 + kReg; i < K; i += kThreads * 4) {
+    float4 v = *reinterpret_cast<const float4*>(x + i);
+    if (nw != nullptr) v = norm4(v, *reinterpret_cast<const float4*>(nw + i), inv);
+    store_x4(v, i, lds_x, lds_xs);
   }
   __syncthreads();
+}
+
+__device__ void stage_x(const float* __restrict__ x, const float* __restrict__ nw, float eps, int K, float* lds_x,
+                        float* lds_xs, double* red) {
+  XLoad r;
+  xload_issue(x, nw, K, r);
+  xload_finish(x, nw, eps, K, r, lds_x, lds_xs, red);
 }
 
 __device__ __forceinline__ float byte_f(uint32_t v, int k) { return static_cast<float>((v >> (8 * k)) & 0xFFu); }
@@ -150,65 +205,46 @@ __device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&d)[N]) 
   for (int i = 0; i < N; ++i) d[i] = __builtin_nontemporal_load(q + i);
 }
 
-// Dot of R rows (stride rb bytes, starting at W) with x over the pairs p = t, t+G, ... of a row.
-template <int QT, int G, int R>
-__device__ __forceinline__ void rows_dot_pairs(const uint8_t* __restrict__ W, int rb, int np, int t, int nvalid,
-                                               const float* lds_x, const float* lds_xs, float (&acc)[R]) {
-  constexpr int PD = QT == EF_QTYPE_Q4_0 ? 9 : 17;  // dwords per block pair
-  constexpr int PB = PD * 4;
+template <int QT>
+struct PairOf {
+  static constexpr int PD = QT == EF_QTYPE_Q4_0 ? 9 : 17;  // dwords per block pair (36 / 68 bytes)
+};
+
+// Adds one staged block pair's dot product with the RR weight rows held in d.
+template <int QT, int RR>
+__device__ __forceinline__ void pair_dot(const uint32_t (&d)[RR][PairOf<QT>::PD], const float* slot, float xsA,
+                                         float xsB, float (&acc)[RR]) {
+  float4 xv[8];
+  // block A of the pair: scale in bytes 0-1, codes from byte 2 (realigned by 2 bytes)
+  load_x_block(slot, xv);
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-  for (int p = t; p < np; p += G) {
-    uint32_t d[R][PD];
+  for (int r = 0; r < RR; ++r) {
+    const float dA = half_bits_to_float(d[r][0] & 0xFFFFu);
+    if (QT == EF_QTYPE_Q4_0) {
+      uint32_t q[4];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (r < nvalid) {
-        load_dwords<PD>(W + static_cast<size_t>(r) * rb + static_cast<size_t>(p) * PB, d[r]);
-      } else {
+      for (int k = 0; k < 4; ++k) q[k] = __builtin_amdgcn_alignbyte(d[r][k + 1], d[r][k], 2);
+      acc[r] = fmaf(dA, fmaf(-8.0f, xsA, q4_codes_dot(q, xv)), acc[r]);
+    } else {
+      uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < PD; ++i) d[r][i] = 0u;
-      }
-    }
-    const float* slot = lds_x + p * kSlot;
-    float4 xv[8];
-    // block A of the pair: scale in bytes 0-1, codes from byte 2 (realigned by 2 bytes)
-    load_x_block(slot, xv);
-    const float xsA = lds_xs[2 * p];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float dA = half_bits_to_float(d[r][0] & 0xFFFFu);
-      if (QT == EF_QTYPE_Q4_0) {
-        uint32_t q[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = __builtin_amdgcn_alignbyte(d[r][k + 1], d[r][k], 2);
-        acc[r] = fmaf(dA, fmaf(-8.0f, xsA, q4_codes_dot(q, xv)), acc[r]);
-      } else {
-        uint32_t q[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = __builtin_amdgcn_alignbyte(d[r][k + 1], d[r][k], 2);
-        acc[r] = fmaf(dA, q8_codes_dot(q, xv), acc[r]);
-      }
-    }
-    // block B: scale in the high half of the dword that ends block A's codes, codes aligned
-    load_x_block(slot + 32, xv);
-    const float xsB = lds_xs[2 * p + 1];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (QT == EF_QTYPE_Q4_0) {
-        const float dB = half_bits_to_float(d[r][4] >> 16);
-        const uint32_t q[4] = {d[r][5], d[r][6], d[r][7], d[r][8]};
-        acc[r] = fmaf(dB, fmaf(-8.0f, xsB, q4_codes_dot(q, xv)), acc[r]);
-      } else {
-        const float dB = half_bits_to_float(d[r][8] >> 16);
-        const uint32_t q[8] = {d[r][9], d[r][10], d[r][11], d[r][12], d[r][13], d[r][14], d[r][15], d[r][16]};
-        acc[r] = fmaf(dB, q8_codes_dot(q, xv), acc[r]);
-      }
+      for (int k = 0; k < 8; ++k) q[k] = __builtin_amdgcn_alignbyte(d[r][k + 1], d[r][k], 2);
+      acc[r] = fmaf(dA, q8_codes_dot(q, xv), acc[r]);
     }
   }
+  // block B: scale in the high half of the dword that ends block A's codes, codes aligned
+  load_x_block(slot + 32, xv);
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, kWave);
+  for (int r = 0; r < RR; ++r) {
+    if (QT == EF_QTYPE_Q4_0) {
+      const float dB = half_bits_to_float(d[r][4] >> 16);
+      const uint32_t q[4] = {d[r][5], d[r][6], d[r][7], d[r][8]};
+      acc[r] = fmaf(dB, fmaf(-8.0f, xsB, q4_codes_dot(q, xv)), acc[r]);
+    } else {
+      const float dB = half_bits_to_float(d[r][8] >> 16);
+      const uint32_t q[8] = {d[r][9], d[r][10], d[r][11], d[r][12], d[r][13], d[r][14], d[r][15], d[r][16]};
+      acc[r] = fmaf(dB, q8_codes_dot(q, xv), acc[r]);
+    }
   }
 }
 
@@ -223,35 +259,67 @@ __device__ __forceinline__ JobDev find_job(const Args& a, int tile) {
   return j;
 }
 
-// Fast path: cols % 64 == 0.  grid = (tiles, batch).
-template <int EPI, int G, int R>
-__global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(Args a) {
-  extern __shared__ float lds[];
-  __shared__ double red[kWaves];
+// Body of the fast path for one weight type.  A lane group of G lanes owns R output rows; with the
+// SwiGLU epilogue it also owns the matching R up-projection rows, so RR = 2R weight rows share each
+// x read from LDS.  Pairs are processed in chunks of G * NPL: lane t holds pairs t, t + G, ...,
+// t + (NPL-1) G of the chunk for all RR rows in registers.  The first chunk is requested before x
+// is staged, so its HBM latency overlaps the staging.
+template <int QT, int EPI, int G, int R, int NPL>
+__device__ __forceinline__ void pairs_body(const Args& a, const JobDev& jb, int b, int row0, int nvalid, int t,
+                                           float* lds_x, float* lds_xs, double* red) {
+  constexpr int PD = PairOf<QT>::PD, PB = PD * 4;
+  constexpr int RR = EPI == kEpiSwiglu ? 2 * R : R;
   const int K = a.K, np = K >> 6;
-  float* lds_x = lds;
-  float* lds_xs = lds + np * kSlot;
-  const int tile = blockIdx.x, b = blockIdx.y;
-  const JobDev jb = find_job(a, tile);
-  stage_x(jb.x + b * jb.ldx, a.norm_w, a.eps, K, lds_x, lds_xs, red);
-
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
-  const int grp = lane / G, t = lane % G;
-  const int row0 = (tile - jb.tile_begin) * jb.rows_per_tile + (wave * (kWave / G) + grp) * R;
-  if (row0 >= jb.rows) return;
-  const int nvalid = min(R, jb.rows - row0);
   const size_t rb = static_cast<size_t>(jb.row_bytes);
-  float acc[R], acc2[R];
-  if (jb.qtype == EF_QTYPE_Q4_0) {
-    rows_dot_pairs<EF_QTYPE_Q4_0, G, R>(jb.W + row0 * rb, jb.row_bytes, np, t, nvalid, lds_x, lds_xs, acc);
-    if (EPI == kEpiSwiglu)
-      rows_dot_pairs<EF_QTYPE_Q4_0, G, R>(jb.W2 + row0 * rb, jb.row_bytes, np, t, nvalid, lds_x, lds_xs, acc2);
-  } else {
-    rows_dot_pairs<EF_QTYPE_Q8_0, G, R>(jb.W + row0 * rb, jb.row_bytes, np, t, nvalid, lds_x, lds_xs, acc);
-    if (EPI == kEpiSwiglu)
-      rows_dot_pairs<EF_QTYPE_Q8_0, G, R>(jb.W2 + row0 * rb, jb.row_bytes, np, t, nvalid, lds_x, lds_xs, acc2);
+  // One resource per matrix: rows at or past jb.rows read as zeros.  Pairs past np of a valid row
+  // would read the next row, so they are skipped in the dot loop.
+  const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * static_cast<uint32_t>(rb);
+  const __amdgpu_buffer_rsrc_t rw1 = make_rsrc(jb.W, mat_bytes);
+  const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(EPI == kEpiSwiglu ? jb.W2 : jb.W, mat_bytes);
+  uint32_t buf[NPL][RR][PD];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const uint32_t p = static_cast<uint32_t>(c * (G * NPL) + i * G + t);
+#pragma unroll
+      for (int r = 0; r < RR; ++r) {
+        const __amdgpu_buffer_rsrc_t rs = r < R ? rw1 : rw2;
+        const uint32_t off = static_cast<uint32_t>(row0 + r % R) * static_cast<uint32_t>(rb) + p * PB;
+#pragma unroll
+        for (int k = 0; k + 4 <= PD; k += 4) {
+          const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4u * k, 0, kNonTemporal);
+          buf[i][r][k] = v.x;
+          buf[i][r][k + 1] = v.y;
+          buf[i][r][k + 2] = v.z;
+          buf[i][r][k + 3] = v.w;
+        }
+        buf[i][r][PD - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4u * (PD - 1), 0, kNonTemporal);
+      }
+    }
+  };
+  const float* xb = jb.x + b * jb.ldx;
+  XLoad xr;
+  xload_issue(xb, a.norm_w, K, xr);
+  load_chunk(0);
+  xload_finish(xb, a.norm_w, a.eps, K, xr, lds_x, lds_xs, red);
+  float acc[RR];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) acc[r] = 0.0f;
+  const int nch = (np + G * NPL - 1) / (G * NPL);
+  for (int c = 0; c < nch; ++c) {
+    if (c > 0) load_chunk(c);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int p = c * (G * NPL) + i * G + t;
+      if (p < np) pair_dot<QT, RR>(buf[i], lds_x + p * kSlot, lds_xs[2 * p], lds_xs[2 * p + 1], acc);
+    }
   }
-  if (t != 0) return;
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, kWave);
+  }
+  if (t != 0 || nvalid <= 0) return;
   float* y = jb.y + b * jb.ldy + row0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -259,7 +327,166 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(Args a) {
     if (EPI == kEpiResidual) {
       y[r] = y[r] + acc[r];
     } else if (EPI == kEpiSwiglu) {
-      y[r] = silu_f(acc[r]) * acc2[r];
+      y[r] = silu_f(acc[r]) * acc[R + r];
+    } else {
+      y[r] = acc[r];
+    }
+  }
+}
+
+// Fast path: cols % 64 == 0.  grid = (tiles, batch).
+template <int EPI, int G, int R, int NPL>
+__global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(Args a) {
+  extern __shared__ float lds[];
+  __shared__ double red[kWaves];
+  const int np = a.K >> 6;
+  float* lds_x = lds;
+  float* lds_xs = lds + np * kSlot;
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const JobDev jb = find_job(a, tile);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int grp = lane / G, t = lane % G;
+  const int row0 = (tile - jb.tile_begin) * jb.rows_per_tile + (wave * (kWave / G) + grp) * R;
+  const int nvalid = max(0, min(R, jb.rows - row0));
+  // Every thread stays to the end: stage_x has block-wide barriers.
+  if (jb.qtype == EF_QTYPE_Q4_0) {
+    pairs_body<EF_QTYPE_Q4_0, EPI, G, R, NPL>(a, jb, b, row0, nvalid, t, lds_x, lds_xs, red);
+  } else {
+    pairs_body<EF_QTYPE_Q8_0, EPI, G, R, NPL>(a, jb, b, row0, nvalid, t, lds_x, lds_xs, red);
+  }
+}
+
+// ---- DMA path: whole rows fetched with coalesced LDS-DMA loads ----------------------------------
+// A wave owns RW = (64/G) R consecutive rows of each matrix (gate and up for SwiGLU): RW * row_bytes
+// contiguous bytes, fetched as 1 KB buffer_load ... lds instructions (lane l's 16 bytes land at
+// base + 16 l), so every HBM request is a fully used, contiguous 1 KB.  The raw activations and
+// the norm weights are fetched the same way.  All fetches are issued before anything waits; after
+// one wait and a barrier, x is normalised into the padded slots, and each lane reads its block
+// pairs from LDS (row stride row_bytes: lanes of a group read pairs 36 / 68 bytes apart, a stride
+// co-prime with the bank count).
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int AUX>
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
+  // lds_dst is wave-uniform: the 16 bytes of lane l land at lds_dst + 16 l
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(lds_dst), 16, voff, 0, 0, AUX);
+}
+
+// Copies `bytes` (a multiple of 16) from buffer offset src_off to LDS as 1 KB wave instructions.
+template <int AUX>
+__device__ __forceinline__ void dma_span(__amdgpu_buffer_rsrc_t r, uint32_t src_off, uint8_t* lds_dst, uint32_t bytes,
+                                         int lane) {
+  for (uint32_t o = 0; o < bytes; o += 1024u) {
+    if (o + 16u * lane < bytes) dma16<AUX>(r, lds_dst + o, src_off + o + 16u * lane);
+  }
+}
+
+template <int QT, int RR>
+__device__ __forceinline__ void lds_pair(const uint8_t* p, uint32_t (&d)[RR][PairOf<QT>::PD], int r) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+  for (int k = 0; k < PairOf<QT>::PD; ++k) d[r][k] = q[k];
+}
+
+template <int QT, int EPI, int G, int R>
+__device__ __forceinline__ void dma_body(const float* lds_x, const float* lds_xs, const uint8_t* wl, uint32_t wstride,
+                                         int np, int rb, int t, int grp, float (&acc)[EPI == kEpiSwiglu ? 2 * R : R]) {
+  constexpr int PD = PairOf<QT>::PD, PB = PD * 4;
+  constexpr int RR = EPI == kEpiSwiglu ? 2 * R : R;
+#pragma unroll
+  for (int r = 0; r < RR; ++r) acc[r] = 0.0f;
+  for (int p = t; p < np; p += G) {
+    uint32_t d[RR][PD];
+#pragma unroll
+    for (int r = 0; r < RR; ++r) {
+      const int m = r < R ? 0 : 1;
+      lds_pair<QT, RR>(wl + m * wstride + (grp * R + r % R) * rb + p * PB, d, r);
+    }
+    pair_dot<QT, RR>(d, lds_x + p * kSlot, lds_xs[2 * p], lds_xs[2 * p + 1], acc);
+  }
+}
+
+template <int EPI, int G, int R>
+__global__ __launch_bounds__(kThreads) void gemv_dma_kernel(Args a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ double red[kWaves];
+  constexpr int RW = (kWave / G) * R;
+  constexpr int RR = EPI == kEpiSwiglu ? 2 * R : R;
+  const int K = a.K, np = K >> 6;
+  uint8_t* lb = reinterpret_cast<uint8_t*>(lds);
+  float* lds_x = lds;
+  float* lds_xs = lds + np * kSlot;
+  const float* raw_x = reinterpret_cast<const float*>(lb + a.raw_x_off);
+  const float* raw_nw = reinterpret_cast<const float*>(lb + a.raw_nw_off);
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const JobDev jb = find_job(a, tile);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x & (kWave - 1);
+  const uint32_t rb = static_cast<uint32_t>(jb.row_bytes);
+  const int wrow0 = (tile - jb.tile_begin) * jb.rows_per_tile + wave * RW;
+  uint8_t* wl = lb + a.w_off + static_cast<uint32_t>(wave) * (EPI == kEpiSwiglu ? 2u : 1u) * a.w_stride;
+
+  // 1. every fetch of the workgroup, weights first (the largest latency)
+  {
+    const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * rb;
+    const uint32_t region = static_cast<uint32_t>(RW) * rb;
+    const uint32_t src = static_cast<uint32_t>(wrow0) * rb;  // rows past the end read as zeros
+    dma_span<kNonTemporal>(make_rsrc(jb.W, mat_bytes), src, wl, (region + 15u) & ~15u, lane);
+    if (EPI == kEpiSwiglu)
+      dma_span<kNonTemporal>(make_rsrc(jb.W2, mat_bytes), src, wl + a.w_stride, (region + 15u) & ~15u, lane);
+    const uint32_t xq = static_cast<uint32_t>(K);  // bytes of x per wave (a quarter of 4K)
+    const float* xb = jb.x + b * jb.ldx;
+    dma_span<0>(make_rsrc(xb, static_cast<uint32_t>(K) * 4u), wave * xq, lb + a.raw_x_off + wave * xq, xq, lane);
+    if (a.norm_w != nullptr)
+      dma_span<0>(make_rsrc(a.norm_w, static_cast<uint32_t>(K) * 4u), wave * xq, lb + a.raw_nw_off + wave * xq, xq,
+                  lane);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // 2. normalise x into the padded slots (+ block sums)
+  {
+    float inv = 1.0f;
+    if (a.norm_w != nullptr) {
+      double ss = 0.0;
+      for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) ss += sq_d(*reinterpret_cast<const float4*>(raw_x + i));
+      ss = wave_sum_d(ss);
+      if (lane == 0) red[wave] = ss;
+      __syncthreads();
+      const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+      inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)));
+    }
+    for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) {
+      float4 v = *reinterpret_cast<const float4*>(raw_x + i);
+      if (a.norm_w != nullptr) v = norm4(v, *reinterpret_cast<const float4*>(raw_nw + i), inv);
+      store_x4(v, i, lds_x, lds_xs);
+    }
+    __syncthreads();
+  }
+
+  // 3. dot products
+  const int grp = lane / G, t = lane % G;
+  const int row0 = wrow0 + grp * R;
+  const int nvalid = max(0, min(R, jb.rows - row0));
+  float acc[RR];
+  if (jb.qtype == EF_QTYPE_Q4_0) {
+    dma_body<EF_QTYPE_Q4_0, EPI, G, R>(lds_x, lds_xs, wl, a.w_stride, np, static_cast<int>(rb), t, grp, acc);
+  } else {
+    dma_body<EF_QTYPE_Q8_0, EPI, G, R>(lds_x, lds_xs, wl, a.w_stride, np, static_cast<int>(rb), t, grp, acc);
+  }
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, kWave);
+  }
+  if (t != 0 || nvalid <= 0) return;
+  float* y = jb.y + b * jb.ldy + row0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r >= nvalid) break;
+    if (EPI == kEpiResidual) {
+      y[r] = y[r] + acc[r];
+    } else if (EPI == kEpiSwiglu) {
+      y[r] = silu_f(acc[r]) * acc[R + r];
     } else {
       y[r] = acc[r];
     }
@@ -328,24 +555,75 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(Args a) {
 }
 
 // ---- launch ---------------------------------------------------------------------------------------
+// Pairs per lane per chunk are capped so that RR rows x NPL pairs of Q8_0 data (17 dwords each)
+// stay within about 136 VGPRs; larger rows run in several chunks.
+template <int EPI, int G, int R>
+void* pick_pairs_kernel_n(int npl) {
+  constexpr int RR = EPI == kEpiSwiglu ? 2 * R : R;
+  constexpr int cap = RR >= 8 ? 1 : (RR >= 4 ? 2 : 4);
+  if constexpr (cap >= 4) {
+    if (npl >= 4) return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, R, 4>);
+  }
+  if constexpr (cap >= 2) {
+    if (npl >= 2) return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, R, 2>);
+  }
+  return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, R, 1>);
+}
+
 template <int EPI, int G>
-void* pick_pairs_kernel(int R) {
-  if (R == 4) return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, 4>);
-  if (R == 2) return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, 2>);
-  return reinterpret_cast<void*>(&gemv_pairs_kernel<EPI, G, 1>);
+void* pick_pairs_kernel_r(int R, int npl) {
+  if (R == 4) return pick_pairs_kernel_n<EPI, G, 4>(npl);
+  if (R == 2) return pick_pairs_kernel_n<EPI, G, 2>(npl);
+  return pick_pairs_kernel_n<EPI, G, 1>(npl);
 }
 
 template <int EPI>
-void* pick_pairs_kernel(int G, int R) {
-  if (G == 32) return pick_pairs_kernel<EPI, 32>(R);
-  if (G == 16) return pick_pairs_kernel<EPI, 16>(R);
-  return pick_pairs_kernel<EPI, 8>(R);
+void* pick_pairs_kernel(int G, int R, int npl) {
+  if (G == 32) return pick_pairs_kernel_r<EPI, 32>(R, npl);
+  if (G == 16) return pick_pairs_kernel_r<EPI, 16>(R, npl);
+  return pick_pairs_kernel_r<EPI, 8>(R, npl);
+}
+
+template <int EPI, int G>
+void* pick_dma_kernel_r(int R) {
+  if (R == 4) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 4>);
+  if (R == 2) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 2>);
+  return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 1>);
+}
+
+template <int EPI>
+void* pick_dma_kernel(int G, int R) {
+  if (G == 32) return pick_dma_kernel_r<EPI, 32>(R);
+  if (G == 16) return pick_dma_kernel_r<EPI, 16>(R);
+  return pick_dma_kernel_r<EPI, 8>(R);
 }
 
 }  // namespace
 
+// Tuning knobs, read once per process: EF_HIP_GEMV_SHAPE="G,R" (G in {8,16,32}, R in {1,2,4}) forces
+// the lane-group size and rows per group of the cols % 64 == 0 kernels; EF_HIP_GEMV_PATH=dma|regs
+// forces the LDS-DMA or the register-fetch kernel.
+const ShapeOverride& shape_override() {
+  static const ShapeOverride ov = [] {
+    ShapeOverride o;
+    const char* e = std::getenv("EF_HIP_GEMV_SHAPE");
+    int g = 0, r = 0;
+    if (e != nullptr && std::sscanf(e, "%d,%d", &g, &r) == 2 && (g == 8 || g == 16 || g == 32) &&
+        (r == 1 || r == 2 || r == 4)) {
+      o.G = g;
+      o.R = r;
+    }
+    const char* pth = std::getenv("EF_HIP_GEMV_PATH");
+    if (pth != nullptr) o.path = std::strcmp(pth, "dma") == 0 ? 1 : (std::strcmp(pth, "regs") == 0 ? 2 : 0);
+    return o;
+  }();
+  return ov;
+}
+
+bool mfma_gemv_disabled() { return shape_override().path != 0; }
+
 int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
-                size_t ldy, hipStream_t stream) {
+                size_t ldy, hipStream_t stream, void* ws, size_t ws_bytes) {
   EFH_CHECK(n_jobs >= 1 && n_jobs <= kMaxJobs, "gemv: 1..4 jobs per launch");
   EFH_CHECK(batch >= 1 && batch <= 65535, "gemv: batch must be in [1, 65535]");
   EFH_CHECK(epi >= kEpiStore && epi <= kEpiSwiglu, "gemv: unknown epilogue");
@@ -357,6 +635,8 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     EFH_CHECK(g.W->qtype == EF_QTYPE_Q4_0 || g.W->qtype == EF_QTYPE_Q8_0, "gemv: weights must be Q4_0 or Q8_0");
     EFH_CHECK(g.W->cols == K, "gemv: all jobs of one launch need the same cols");
     EFH_CHECK(g.W->rows >= 1 && g.W->rows <= (1u << 24), "gemv: rows must be in [1, 2^24]");
+    // buffer resources address a matrix with 32-bit byte offsets
+    EFH_CHECK(g.W->rows * g.W->row_bytes < (1ull << 32) - (1ull << 20), "gemv: a matrix must be under 4 GiB");
     if (epi == kEpiSwiglu) {
       EFH_CHECK(g.W2 && g.W2->qtype == g.W->qtype && g.W2->rows == g.W->rows && g.W2->cols == K,
                 "gemv: swiglu needs gate and up of the same type and shape");
@@ -368,6 +648,9 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
       EFH_CHECK((jobs[j].ldy ? jobs[j].ldy : ldy) >= jobs[j].W->rows, "gemv: ldy smaller than rows");
     }
   }
+  bool taken = false;
+  EFH_RC(launch_gemv_mfma(jobs, n_jobs, epi, norm_w, eps, batch, ldx, ldy, ws, ws_bytes, stream, &taken));
+  if (taken) return EF_HIP_OK;
   Args a{};
   a.n_jobs = n_jobs;
   a.K = static_cast<int>(K);
@@ -375,7 +658,32 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   a.eps = eps;
   const bool fast = K % 64 == 0;
   const int np = static_cast<int>(K / 64);
-  const int G = np >= 32 ? 32 : (np >= 16 ? 16 : 8);
+  int G = np >= 32 ? 32 : (np >= 16 ? 16 : 8);
+  const int nmat = epi == kEpiSwiglu ? 2 : 1;
+  // LDS of the DMA path for R rows per lane group: x slots + block sums, raw x (+ raw norm
+  // weights), then per wave and matrix the wave's RW rows.
+  auto dma_layout = [&](int g, int r, Args* out) -> size_t {
+    const size_t rw = static_cast<size_t>(kWave / g) * r;
+    size_t wstride = 0;
+    for (int j = 0; j < n_jobs; ++j) wstride = std::max(wstride, (rw * jobs[j].W->row_bytes + 15) & ~size_t(15));
+    size_t off = ((static_cast<size_t>(np) * kSlot + K / 32) * sizeof(float) + 15) & ~size_t(15);
+    const size_t raw_x = off;
+    off += K * 4;
+    const size_t raw_nw = off;
+    if (norm_w != nullptr) off += K * 4;
+    const size_t w_off = off;
+    off += static_cast<size_t>(kWaves) * nmat * wstride;
+    if (out != nullptr) {
+      out->raw_x_off = static_cast<uint32_t>(raw_x);
+      out->raw_nw_off = static_cast<uint32_t>(raw_nw);
+      out->w_off = static_cast<uint32_t>(w_off);
+      out->w_stride = static_cast<uint32_t>(wstride);
+    }
+    return off;
+  };
+  constexpr size_t kDmaLdsTarget = 80 * 1024;  // two workgroups per CU
+  const ShapeOverride& ov = shape_override();
+  bool use_dma = fast && ov.path != 2 && dma_layout(G, 1, nullptr) <= kDmaLdsTarget;
   // rows per tile: 4 waves x (64/G) groups x R rows; R as large as keeps >= 2 tiles per CU
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
   int R = 1;
@@ -384,12 +692,27 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
       const size_t per_tile = static_cast<size_t>(kWaves * (kWave / G) * cand);
       size_t tiles = 0;
       for (int j = 0; j < n_jobs; ++j) tiles += (jobs[j].W->rows + per_tile - 1) / per_tile;
-      if (tiles * static_cast<size_t>(batch) >= static_cast<size_t>(2 * cus)) {
+      if (tiles * static_cast<size_t>(batch) >= static_cast<size_t>(2 * cus) &&
+          (!use_dma || dma_layout(G, cand, nullptr) <= kDmaLdsTarget)) {
         R = cand;
         break;
       }
     }
   }
+  if (fast && ov.G > 0) {
+    G = ov.G;
+    R = ov.R;
+    if (ov.path == 1) use_dma = true;
+  }
+  size_t dma_lds = 0;
+  if (use_dma) {
+    dma_lds = dma_layout(G, R, &a);
+    const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
+    if (dma_lds > lim) use_dma = false;
+  }
+  // pairs per lane and chunk of the register path: all of a row's pairs when they fit in four
+  int npl = (np + G - 1) / G;
+  npl = npl >= 3 ? 4 : npl;
   int tiles = 0;
   for (int j = 0; j < n_jobs; ++j) {
     JobDev& d = a.job[j];
@@ -408,12 +731,17 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     tiles += (d.rows + d.rows_per_tile - 1) / d.rows_per_tile;
   }
   const int nslot = static_cast<int>((K + 63) / 64);
-  const size_t lds_bytes = (static_cast<size_t>(nslot) * kSlot + K / 32) * sizeof(float);
+  size_t lds_bytes = (static_cast<size_t>(nslot) * kSlot + K / 32) * sizeof(float);
   void* fn = nullptr;
-  if (fast) {
-    fn = epi == kEpiStore ? pick_pairs_kernel<kEpiStore>(G, R)
-                          : (epi == kEpiResidual ? pick_pairs_kernel<kEpiResidual>(G, R)
-                                                 : pick_pairs_kernel<kEpiSwiglu>(G, R));
+  if (fast && use_dma) {
+    fn = epi == kEpiStore ? pick_dma_kernel<kEpiStore>(G, R)
+                          : (epi == kEpiResidual ? pick_dma_kernel<kEpiResidual>(G, R)
+                                                 : pick_dma_kernel<kEpiSwiglu>(G, R));
+    lds_bytes = dma_lds;
+  } else if (fast) {
+    fn = epi == kEpiStore ? pick_pairs_kernel<kEpiStore>(G, R, npl)
+                          : (epi == kEpiResidual ? pick_pairs_kernel<kEpiResidual>(G, R, npl)
+                                                 : pick_pairs_kernel<kEpiSwiglu>(G, R, npl));
   } else {
     fn = epi == kEpiStore ? reinterpret_cast<void*>(&gemv_generic_kernel<kEpiStore>)
                           : (epi == kEpiResidual ? reinterpret_cast<void*>(&gemv_generic_kernel<kEpiResidual>)

@@ -51,7 +51,24 @@ __global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long r
 // One (query head h, sequence b) per workgroup: RoPE on q and on the new k (half-split pairs,
 // src/kernels.cpp:133-146), the new k / v written into the cache at pos by the first head of each
 // KV group, then causal attention over positions 0..pos (positions < pos from the cache, pos from
-// registers, so no head waits on another).
+// LDS, so no head waits on another).  K and V rows are staged through LDS in chunks of kAttnChunk
+// positions with coalesced float4 loads.  Scores use four lanes per position: lane s of a
+// quad accumulates the dot_f32 partials 2s and 2s+1 (kern::dot_f32's eight partials, i % 8), and
+// two shuffles finish the reference's pairwise tree exactly.  P.V keeps the reference's order: one
+// thread per output dimension accumulates positions in increasing order.
+constexpr int kAttnChunk = kAttnThreads / 4;
+
+__device__ __forceinline__ void stage_rows(float* dst, const float* cache, long kvd, const float* cur, int pos,
+                                           int c0, int n, int hd) {
+  // rows c0 .. c0+n-1 (n <= kAttnChunk) of one KV head, row `pos` from `cur`
+  const int q = hd / 4;  // float4 per row (hd % 4 == 0)
+  for (int idx = threadIdx.x; idx < n * q; idx += blockDim.x) {
+    const int r = idx / q, c = idx - r * q, tp = c0 + r;
+    const float* src = tp == pos ? cur : cache + static_cast<long>(tp) * kvd;
+    reinterpret_cast<float4*>(dst + r * hd)[c] = reinterpret_cast<const float4*>(src)[c];
+  }
+}
+
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   const int h = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
@@ -59,15 +76,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   const int g = h / (a.H / a.KV), kvd = a.KV * hd;
   float* qs = sm;              // [hd]
   float* kn = sm + hd;         // [hd] roped new k
-  float* sc = sm + 2 * hd;     // [n_pos] scores / probabilities
-  double* red = reinterpret_cast<double*>(sm + 2 * hd + ((a.max_seq + 1) & ~1));
+  float* vn = sm + 2 * hd;     // [hd] new v
+  float* rows = sm + 3 * hd;   // [kAttnChunk][hd] staged K or V rows
+  float* sc = rows + kAttnChunk * hd;  // [n_pos] scores / probabilities
+  double* red = reinterpret_cast<double*>(sc + ((a.max_seq + 1) & ~1));
   const float* cr = a.cos_t + static_cast<long>(pos) * half;
   const float* sr = a.sin_t + static_cast<long>(pos) * half;
   const float* q = a.q + static_cast<long>(b) * a.ldq + h * hd;
   const float* k_new = a.knew + static_cast<long>(b) * kvd + g * hd;
   const float* v_new = a.vnew + static_cast<long>(b) * kvd + g * hd;
-  float* kc = a.kcache + (static_cast<long>(b) * a.max_seq) * kvd;  // this layer, this sequence
-  float* vc = a.vcache + (static_cast<long>(b) * a.max_seq) * kvd;
+  const float* kc = a.kcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;  // this layer, sequence, head
+  const float* vc = a.vcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;
   const int t = threadIdx.x;
   if (t < half) {
     const float qa = q[t], qb = q[t + half], ka = k_new[t], kb = k_new[t + half];
@@ -76,26 +95,39 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     kn[t] = ka * cr[t] - kb * sr[t];
     kn[t + half] = kb * cr[t] + ka * sr[t];
   }
+  for (int i = t; i < hd; i += blockDim.x) vn[i] = v_new[i];
   __syncthreads();
   if (h % (a.H / a.KV) == 0) {  // the group's first head publishes k / v at pos for later steps
+    float* kw = a.kcache + (static_cast<long>(b) * a.max_seq + pos) * kvd + g * hd;
+    float* vw = a.vcache + (static_cast<long>(b) * a.max_seq + pos) * kvd + g * hd;
     for (int i = t; i < hd; i += blockDim.x) {
-      kc[static_cast<long>(pos) * kvd + g * hd + i] = kn[i];
-      vc[static_cast<long>(pos) * kvd + g * hd + i] = v_new[i];
+      kw[i] = kn[i];
+      vw[i] = vn[i];
     }
   }
-  // scores: kern::dot_f32 order (8 partial sums, pairwise), times the 1/sqrt(hd) scale
-  for (int tp = t; tp < n_pos; tp += blockDim.x) {
-    const float* kt = tp == pos ? kn : kc + static_cast<long>(tp) * kvd + g * hd;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int i = 0;
-    for (; i + 8 <= hd; i += 8) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] += qs[i + k] * kt[i + k];
+  // scores
+  const int quad = t >> 2, sub = t & 3;
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    stage_rows(rows, kc, kvd, kn, pos, c0, n, hd);
+    __syncthreads();
+    if (quad < n) {
+      const float* kt = rows + quad * hd;
+      float a0 = 0.0f, a1 = 0.0f;
+      int i = 0;
+      for (; i + 8 <= hd; i += 8) {
+        a0 += qs[i + 2 * sub] * kt[i + 2 * sub];
+        a1 += qs[i + 2 * sub + 1] * kt[i + 2 * sub + 1];
+      }
+      if (sub == 0)
+        for (; i < hd; ++i) a0 += qs[i] * kt[i];  // dot_f32's tail joins partial 0
+      float s = a0 + a1;                           // (acc[2s] + acc[2s+1])
+      s = s + __shfl_xor(s, 1, kWave);             // (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
+      s = s + __shfl_xor(s, 2, kWave);             // the two halves, low half first on lane 0
+      if (sub == 0) sc[c0 + quad] = s * a.scale;
     }
-    for (; i < hd; ++i) acc[0] += qs[i] * kt[i];
-    sc[tp] = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) * a.scale;
+    __syncthreads();
   }
-  __syncthreads();
   // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
   float mx = -INFINITY;
   for (int tp = t; tp < n_pos; tp += blockDim.x) mx = fmaxf(mx, sc[tp]);
@@ -118,16 +150,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) tot += red[w];
   const float inv = static_cast<float>(1.0 / tot);
   // out[d] = sum_t p_t v_t[d], positions in order
-  float* out = a.ctx + static_cast<long>(b) * a.ldq + h * hd;
-  for (int d = t; d < hd; d += blockDim.x) {
-    float o = 0.0f;
-    for (int tp = 0; tp < n_pos; ++tp) {
-      const float p = sc[tp] * inv;
-      const float v = tp == pos ? v_new[d] : vc[static_cast<long>(tp) * kvd + g * hd + d];
-      o += p * v;
+  float o = 0.0f;
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    stage_rows(rows, vc, kvd, vn, pos, c0, n, hd);
+    __syncthreads();
+    if (t < hd) {
+      for (int r = 0; r < n; ++r) {
+        const float p = sc[c0 + r] * inv;
+        o += p * rows[r * hd + t];
+      }
     }
-    out[d] = o;
+    __syncthreads();
   }
+  if (t < hd) a.ctx[static_cast<long>(b) * a.ldq + h * hd + t] = o;
 }
 
 // out[b] = w * (x[b] * rsqrt(mean(x[b]^2) + eps)) (kern::rmsnorm).
@@ -176,7 +212,7 @@ int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld,
 }
 
 size_t attention_lds_bytes(int hd, int max_seq) {
-  return (2 * static_cast<size_t>(hd) + ((max_seq + 1) & ~1)) * sizeof(float) + 4 * sizeof(double);
+  return ((3 + static_cast<size_t>(kAttnChunk)) * hd + ((max_seq + 1) & ~1)) * sizeof(float) + 4 * sizeof(double);
 }
 
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {

@@ -11,6 +11,21 @@ constexpr size_t kRngStateBytes = 2560;  // std::mt19937_64 state (312 words + i
 size_t sample_workspace_stride(int vocab);
 int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t s);
 int launch_argmax(const float* x, int n, long ld, int batch, int32_t* out, hipStream_t s);
+
+// Device-resident step state of the decode engine, advanced by the kernel that picks the token.
+struct StepArgs {
+  int32_t* next;        // [batch] picked ids
+  int32_t* hist;        // [batch][hist_ld] token history (prompt + generated)
+  long hist_ld;
+  int32_t* hist_len;    // [batch]
+  int32_t* out;         // [batch][out_ld] generated ids
+  long out_ld;
+  const int32_t* n_prompt;
+  int32_t* pos;         // current position (shared by the batch)
+  uint32_t* counter;    // zero between steps
+};
+// argmax per sequence, then the step bookkeeping (pos advances once for the batch).
+int launch_argmax_finish(const float* x, int n, long ld, int batch, const StepArgs& f, hipStream_t s);
 // ws: batch * sample_workspace_stride(vocab) bytes of device memory.
 int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_hip_sampler_config& cfg,
                   const int32_t* hist, const int32_t* hist_len, long hist_ld, void* rng, int32_t* out, void* ws,

@@ -84,15 +84,37 @@ __device__ __forceinline__ uint64_t make_key(float v, uint32_t id) {
 __device__ __forceinline__ uint32_t key_id(uint64_t k) { return 0xFFFFFFFFu - static_cast<uint32_t>(k); }
 
 // First maximum (strict >, scan order) of x[0..n): returns the index.  NaN never replaces the
-// running best; a NaN at index 0 is the answer, as in the sequential scan.
+// running best; a NaN at index 0 is the answer, as in the sequential scan (kern::argmax,
+// src/kernels.cpp:107-115).  Each thread scans its elements in increasing index order (float4
+// loads through a buffer resource, all issued before the compares); the merge keeps the larger
+// value and, on ties, the lower index, which is the sequential scan's answer.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxUnroll = 8;
+
+__device__ __forceinline__ void take(float v, int i, float& bv, int& bi) {
+  if (v == v && (bi == 0x7FFFFFFF || v > bv)) {
+    bv = v;
+    bi = i;
+  }
+}
+
 __device__ int block_argmax(const float* x, int n, float* s_val, int* s_idx) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(x, static_cast<uint32_t>(n) * 4u);
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = x[i];
-    if (v == v && (bi == 0x7FFFFFFF || v > bv)) {  // scanning upwards: equal values keep the lower index
-      bv = v;
-      bi = i;
+  const int step = blockDim.x * 4;
+  for (int base = 0; base < n; base += step * kArgmaxUnroll) {
+    float4 v[kArgmaxUnroll];
+#pragma unroll
+    for (int j = 0; j < kArgmaxUnroll; ++j)
+      v[j] = buf_f4(r, static_cast<uint32_t>(base + j * step + threadIdx.x * 4) * 4u);
+#pragma unroll
+    for (int j = 0; j < kArgmaxUnroll; ++j) {
+      const int i = base + j * step + threadIdx.x * 4;
+      if (i < n) take(v[j].x, i, bv, bi);
+      if (i + 1 < n) take(v[j].y, i + 1, bv, bi);
+      if (i + 2 < n) take(v[j].z, i + 2, bv, bi);
+      if (i + 3 < n) take(v[j].w, i + 3, bv, bi);
     }
   }
   for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -122,16 +144,40 @@ __device__ int block_argmax(const float* x, int n, float* s_val, int* s_idx) {
     s_idx[0] = (x0 != x0 || i == 0x7FFFFFFF) ? 0 : i;
   }
   __syncthreads();
-  const int r = s_idx[0];
+  const int res = s_idx[0];
   __syncthreads();
-  return r;
+  return res;
 }
 
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* x, int n, long ld, int32_t* out) {
-  __shared__ float s_val[kThreads / kWave];
-  __shared__ int s_idx[kThreads / kWave];
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, int n, long ld, int32_t* out) {
+  __shared__ float s_val[kArgmaxThreads / kWave];
+  __shared__ int s_idx[kArgmaxThreads / kWave];
   const int r = block_argmax(x + blockIdx.x * ld, n, s_val, s_idx);
   if (threadIdx.x == 0) out[blockIdx.x] = r;
+}
+
+// Greedy pick fused with the step bookkeeping of the decode engine (one workgroup per sequence):
+// the token becomes the input at p + 1, joins the history, lands in the output list at
+// p - (n_prompt - 1); the last workgroup to finish advances the shared position (every workgroup
+// has read it before it counts itself in) and re-arms the counter for the next step.
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_finish_kernel(const float* x, int n, long ld, StepArgs f) {
+  __shared__ float s_val[kArgmaxThreads / kWave];
+  __shared__ int s_idx[kArgmaxThreads / kWave];
+  const int b = blockIdx.x;
+  const int p = *f.pos;
+  const int tok = block_argmax(x + b * ld, n, s_val, s_idx);
+  if (threadIdx.x == 0) {
+    f.next[b] = tok;
+    const int k = p - (*f.n_prompt - 1);
+    if (p + 1 < f.hist_ld) f.hist[b * f.hist_ld + p + 1] = tok;
+    f.hist_len[b] = p + 2 < f.hist_ld ? p + 2 : static_cast<int32_t>(f.hist_ld);
+    if (k >= 0 && k < f.out_ld) f.out[b * f.out_ld + k] = tok;
+    __threadfence();
+    if (atomicAdd(f.counter, 1u) == gridDim.x - 1) {
+      *f.pos = p + 1;
+      atomicExch(f.counter, 0u);
+    }
+  }
 }
 
 // ---- bitonic sorts (descending) --------------------------------------------------------------------------
@@ -429,7 +475,15 @@ int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t
 }
 
 int launch_argmax(const float* x, int n, long ld, int batch, int32_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(kThreads), 0, s, x, n, ld, out);
+  EFH_CHECK(n >= 1 && static_cast<size_t>(n) * 4 < (1ull << 32), "argmax: n must be in [1, 2^30)");
+  hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, x, n, ld, out);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_argmax_finish(const float* x, int n, long ld, int batch, const StepArgs& f, hipStream_t s) {
+  EFH_CHECK(n >= 1 && static_cast<size_t>(n) * 4 < (1ull << 32), "argmax: n must be in [1, 2^30)");
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, x, n, ld, f);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }

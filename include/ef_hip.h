@@ -154,7 +154,8 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
 /* ---- decode engine ----------------------------------------------------------------------------
  * Transformer::forward (src/model.cpp:184-276) on the device for `batch` independent sequences
  * that share weights, with an FP32 KV cache [L][batch][max_seq][KV*hd] and a per-step HIP graph.
- * Weights are registered handles; norms and the BF16 embedding are device arrays. */
+ * Weights are registered handles; norms and the BF16 embedding are device arrays.  Limits: hd a
+ * multiple of 4 up to 256, max_seq up to 12000 (attention keeps scores and staged rows in LDS). */
 typedef struct {
   size_t D, F, H, KV, hd, V, L, max_pos;
   float eps, rope_theta;
