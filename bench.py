@@ -224,7 +224,7 @@ def main() -> int:
                    "device": dev, **extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_pairs_kernel<swiglu> (gate+up Q4_0 5632x2048, B=1)",
+                     "kernel": "gemv_dma_kernel<swiglu> (gate+up Q4_0 5632x2048, B=1, fused RMSNorm + SwiGLU)",
                      "avg_us": round(avg_ms * 1e3, 3), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }

@@ -379,8 +379,9 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
   void* ws = nullptr;
   size_t ws_bytes = 0;
   if (batch > 1) {
-    ws_bytes = gemv_mfma_workspace_bytes(batch, ldx, true, true);
-    EFH_HIP(hipMalloc(&ws, ws_bytes));
+    const GemvJob j0{W[0], epi == kEpiSwiglu ? W2[0] : nullptr, x, y};
+    ws_bytes = gemv_mfma_workspace_bytes(&j0, 1, epi, batch, ldx);
+    if (ws_bytes > 0) EFH_HIP(hipMalloc(&ws, ws_bytes));
   }
   EFH_HIP(hipEventRecord(e0, s));
   for (int i = 0; i < launches && rc == EF_HIP_OK; ++i) {

@@ -256,13 +256,30 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
     return cleanup_fail(fail(EF_HIP_ENOMEM, "engine sampler workspace"));
   e->allocs.push_back(ws);
   e->sample_ws = ws;
-  if (B > 1) {
-    e->gemv_ws_bytes = gemv_mfma_workspace_bytes(B, std::max(c.D, c.F), true, true);
-    void* gw = nullptr;
-    if (hipMalloc(&gw, e->gemv_ws_bytes) != hipSuccess)
-      return cleanup_fail(fail(EF_HIP_ENOMEM, "engine GEMV workspace"));
-    e->allocs.push_back(gw);
-    e->gemv_ws = gw;
+  if (B > 1) {  // the largest workspace any of the step's batched GEMVs plans for
+    size_t need = 0;
+    for (size_t l = 0; l < c.L; ++l) {
+      const ef_hip_layer& w = e->layers[l];
+      const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, c.D, c.D},
+                              {w.wk, nullptr, e->x, e->knew, c.D, kvd},
+                              {w.wv, nullptr, e->x, e->vnew, c.D, kvd}};
+      const GemvJob o{w.wo, nullptr, e->ctx, e->x, c.D, c.D};
+      const GemvJob gu{w.w_gate, w.w_up, e->x, e->act, c.D, c.F};
+      const GemvJob dn{w.w_down, nullptr, e->act, e->x, c.F, c.D};
+      need = std::max({need, gemv_mfma_workspace_bytes(qkv, 3, kEpiStore, B, c.D),
+                       gemv_mfma_workspace_bytes(&o, 1, kEpiResidual, B, c.D),
+                       gemv_mfma_workspace_bytes(&gu, 1, kEpiSwiglu, B, c.D),
+                       gemv_mfma_workspace_bytes(&dn, 1, kEpiResidual, B, c.F)});
+    }
+    const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, c.D, c.V};
+    need = std::max(need, gemv_mfma_workspace_bytes(&lm, 1, kEpiStore, B, c.D));
+    if (need > 0) {
+      void* gw = nullptr;
+      if (hipMalloc(&gw, need) != hipSuccess) return cleanup_fail(fail(EF_HIP_ENOMEM, "engine GEMV workspace"));
+      e->allocs.push_back(gw);
+      e->gemv_ws = gw;
+      e->gemv_ws_bytes = need;
+    }
   }
   if (hipHostMalloc(reinterpret_cast<void**>(&e->stage), (B * S + 8) * sizeof(int32_t), hipHostMallocDefault) !=
       hipSuccess)

@@ -28,9 +28,10 @@ const ShapeOverride& shape_override();
 bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU kernels
 
 // Matrix-core path for batches of 2 or more sequences (gemv_mfma.hip).  Sets *taken when it enqueued
-// the launches; otherwise the caller uses the vector-ALU kernels.  ws (>= gemv_mfma_workspace_bytes)
-// holds the prepared activation fragments; without it the launch allocates stream-ordered memory.
-size_t gemv_mfma_workspace_bytes(int batch, size_t K, bool q4, bool q8);
+// the launches; otherwise the caller uses the vector-ALU kernels.  ws (>= gemv_mfma_workspace_bytes
+// for the same launch) holds the prepared activation fragments and the split-K partial sums;
+// without it the launch allocates stream-ordered memory.  0 when the launch does not take this path.
+size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx);
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 

@@ -65,6 +65,8 @@ struct MArgs {
   const uint8_t* t8;
   const float* post;    // [B] 2^e_s
   uint32_t row_stride, w_stride;  // LDS: weight rows rs bytes apart, w_stride bytes per matrix
+  int ksplit, pairs_per_split;    // split-K: workgroups per row group and block pairs each
+  float* part;          // [group][split][B][rows of the group][matrices] partial sums (ksplit > 1)
 };
 
 struct PrepArgs {
@@ -282,30 +284,34 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
   const int K = a.K, B = a.B, nb = K >> 5, np = K >> 6;
-  const int tile = blockIdx.x;
+  const int S = a.ksplit, tile = blockIdx.x / S, ks = blockIdx.x % S;
   const MJob jb = find_mjob(a, tile);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x & (kWave - 1);
   const int row0 = (tile - jb.tile_begin) * ROWS;
   const uint32_t rb = static_cast<uint32_t>(jb.row_bytes), rs = a.row_stride;
+  const bool q4 = jb.qtype == EF_QTYPE_Q4_0;
+  const uint32_t pb = q4 ? 36u : 68u;  // bytes per block pair
+  // this workgroup's block pairs [p0, p1): multiples of 4 pairs, so their bytes are 16-byte units
+  const int p0 = ks * a.pairs_per_split, p1 = min(np, p0 + a.pairs_per_split);
 
-  // 1. wave w fetches rows w, w + 8, ... of the workgroup (rows past the end read as zeros)
+  // 1. wave w fetches the split's bytes of rows w, w + 8, ... (rows past the end read as zeros)
   {
     const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * rb;
     const __amdgpu_buffer_rsrc_t r1 = make_rsrc(jb.W, mat_bytes);
     const __amdgpu_buffer_rsrc_t r2 = make_rsrc(EPI == kEpiSwiglu ? jb.W2 : jb.W, mat_bytes);
+    const uint32_t bytes = static_cast<uint32_t>(p1 - p0) * pb;
 #pragma unroll
     for (int r = 0; r < ROWS / kWavesM; ++r) {
       const int jr = wave + kWavesM * r;
-      const uint32_t src = static_cast<uint32_t>(row0 + jr) * rb;
-      dma_copy<kNonTemporal>(r1, src, lb + jr * rs, rb, lane);
-      if (EPI == kEpiSwiglu) dma_copy<kNonTemporal>(r2, src, lb + a.w_stride + jr * rs, rb, lane);
+      const uint32_t src = static_cast<uint32_t>(row0 + jr) * rb + static_cast<uint32_t>(p0) * pb;
+      dma_copy<kNonTemporal>(r1, src, lb + jr * rs, bytes, lane);
+      if (EPI == kEpiSwiglu) dma_copy<kNonTemporal>(r2, src, lb + a.w_stride + jr * rs, bytes, lane);
     }
   }
 
   // 2. this wave's block pairs m = wave, wave + 8, ...; the A fragments of the next pair are
   //    loaded while the current pair's products run
   const int j = lane & 15, g = lane >> 4;
-  const bool q4 = jb.qtype == EF_QTYPE_Q4_0;
   const uint8_t* tab = (q4 ? a.t4 : a.t8) + static_cast<size_t>(lane) * 16;
   const size_t tstride = static_cast<size_t>(nb) * kWave * 16;  // bytes per sequence tile
   float acc[NT][RT][NM][2];
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
     for (int r = 0; r < RT; ++r) {
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt) {
-        const PairOps o = pair_ops(lb + mt * a.w_stride + (r * kTileRows + j) * rs, q4, m, g);
+        const PairOps o = pair_ops(lb + mt * a.w_stride + (r * kTileRows + j) * rs, q4, m - p0, g);
         f4v D[NT][2];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -349,15 +355,15 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
       }
     }
   };
-  if (wave < np) load_a(A[0], wave);
+  if (p0 + wave < p1) load_a(A[0], p0 + wave);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // weight rows (and the first fragments) landed
   __syncthreads();
-  for (int m = wave; m < np; m += 2 * kWavesM) {
+  for (int m = p0 + wave; m < p1; m += 2 * kWavesM) {
     const int m1 = m + kWavesM;
-    if (m1 < np) load_a(A[1], m1);
+    if (m1 < p1) load_a(A[1], m1);
     compute(A[0], m);
-    if (m1 < np) {
-      if (m1 + kWavesM < np) load_a(A[0], m1 + kWavesM);
+    if (m1 < p1) {
+      if (m1 + kWavesM < p1) load_a(A[0], m1 + kWavesM);
       compute(A[1], m1);
     }
   }
@@ -377,20 +383,19 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
       }
   __syncthreads();
   constexpr int wstep = NT * RT * NM * kWave * 2;  // floats per wave
-  for (int o = threadIdx.x; o < ROWS * B; o += kT) {
-    const int sq = o / ROWS, jr = o % ROWS, row = row0 + jr;
-    if (row >= jb.rows) continue;
+  // the workgroup's sums for output o = (sequence, row) of matrix mt, waves in order
+  auto wg_sum = [&](int o, int mt) {
+    const int sq = o / ROWS, jr = o % ROWS;
     const int t = sq / kSeqTile, s = sq % kSeqTile, r = jr / kTileRows, jj = jr % kTileRows;
     const int src = (jj + 16 * (s >> 1)) * 2 + (s & 1);  // lane holding D rows 4(l/16).., slot
-    float v[NM];
+    const float* p = red + (((t * RT + r) * NM + mt) * kWave) * 2 + src;
+    float sum = p[0];
 #pragma unroll
-    for (int mt = 0; mt < NM; ++mt) {
-      const float* p = red + (((t * RT + r) * NM + mt) * kWave) * 2 + src;
-      float sum = p[0];
-#pragma unroll
-      for (int w = 1; w < kWavesM; ++w) sum += p[w * wstep];  // waves in order
-      v[mt] = sum * a.post[sq];
-    }
+    for (int w = 1; w < kWavesM; ++w) sum += p[w * wstep];
+    return sum;
+  };
+  auto epilogue = [&](int o, const float (&v)[NM]) {
+    const int sq = o / ROWS, row = row0 + o % ROWS;
     float* y = jb.y + sq * jb.ldy + row;
     if (EPI == kEpiResidual) {
       *y = *y + v[0];
@@ -399,6 +404,63 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
     } else {
       *y = v[0];
     }
+  };
+  if (S == 1) {
+    for (int o = threadIdx.x; o < ROWS * B; o += kT) {
+      if (row0 + o % ROWS >= jb.rows) continue;
+      float v[NM];
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) v[mt] = wg_sum(o, mt) * a.post[o / ROWS];
+      epilogue(o, v);
+    }
+    return;
+  }
+  // split-K: this split's sums go to the workspace; finalize_kernel adds the splits in index order
+  // and applies the epilogue (the kernel boundary makes every split visible, no fences needed).
+  const size_t gsz = static_cast<size_t>(B) * ROWS * NM;
+  float* mine = a.part + (static_cast<size_t>(tile) * S + ks) * gsz;
+  for (int o = threadIdx.x; o < ROWS * B; o += kT) {
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) mine[o * NM + mt] = wg_sum(o, mt);
+  }
+}
+
+struct FinArgs {
+  MJob job[kMaxJobsM];
+  int n_jobs, B, rows_wg, S, total;  // total = groups * rows_wg * B outputs
+  const float* part;
+  const float* post;
+};
+
+// One output (sequence, row) per thread: the splits' sums in index order, the scale, the epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void finalize_kernel(FinArgs a) {
+  constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.total) return;
+  const int per_group = a.rows_wg * a.B;
+  const int tile = idx / per_group, o = idx % per_group;
+  MJob jb = a.job[0];
+  for (int i = 1; i < a.n_jobs; ++i)
+    if (tile >= a.job[i].tile_begin) jb = a.job[i];
+  const int sq = o / a.rows_wg, row = (tile - jb.tile_begin) * a.rows_wg + o % a.rows_wg;
+  if (row >= jb.rows) return;
+  const size_t gsz = static_cast<size_t>(per_group) * NM;
+  const float* p = a.part + static_cast<size_t>(tile) * a.S * gsz + static_cast<size_t>(o) * NM;
+  float v[NM];
+#pragma unroll
+  for (int mt = 0; mt < NM; ++mt) {
+    float sum = p[mt];
+    for (int k = 1; k < a.S; ++k) sum += p[k * gsz + mt];
+    v[mt] = sum * a.post[sq];
+  }
+  float* y = jb.y + sq * jb.ldy + row;
+  if (EPI == kEpiResidual) {
+    *y = *y + v[0];
+  } else if (EPI == kEpiSwiglu) {
+    *y = silu_m(v[0]) * v[NM - 1];
+  } else {
+    *y = v[0];
   }
 }
 
@@ -427,62 +489,109 @@ static int tiles_for(int nseq) {
   return nt <= 1 ? 1 : (nt <= 2 ? 2 : (nt <= 4 ? 4 : 8));
 }
 
-size_t gemv_mfma_workspace_bytes(int batch, size_t K, bool q4, bool q8) {
-  const size_t tab = static_cast<size_t>(tiles_for(batch)) * (K / 32) * kWave * 16;
-  return (q4 ? tab : 0) + (q8 ? tab : 0) + kMaxTiles * kSeqTile * sizeof(float);
+namespace {
+
+// Shape decisions of one batched launch and the workspace they need.
+struct Plan {
+  bool ok = false;
+  bool q4 = false, q8 = false;
+  int nm = 1, NT = 1, RT = 1, groups = 0, S = 1, pps = 0, chunk = 0;
+  size_t max_rb = 0, tab = 0, part_off = 0, bytes = 0, lds = 0;
+  uint32_t row_stride = 0, w_stride = 0;
+};
+
+Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
+  Plan p;
+  if (mfma_gemv_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return p;
+  const size_t K = jobs[0].W->cols;
+  if (K % 256 != 0) return p;  // pairs come in 16-byte multiples of 4 for the LDS-DMA row copies
+  for (int j = 0; j < n_jobs; ++j) {
+    p.q4 = p.q4 || jobs[j].W->qtype == EF_QTYPE_Q4_0;
+    p.q8 = p.q8 || jobs[j].W->qtype == EF_QTYPE_Q8_0;
+    p.max_rb = std::max(p.max_rb, jobs[j].W->row_bytes);
+    if (jobs[j].x != jobs[0].x || (jobs[j].ldx ? jobs[j].ldx : ldx) != (jobs[0].ldx ? jobs[0].ldx : ldx))
+      return p;  // one activation matrix per launch
+  }
+  const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
+  if (reinterpret_cast<uintptr_t>(jobs[0].x) % 16 != 0 || xld % 4 != 0) return p;
+  p.nm = epi == kEpiSwiglu ? 2 : 1;
+  p.chunk = std::min(batch, kMaxTiles * kSeqTile);
+  p.NT = tiles_for(batch);
+  // Two row tiles halve the fragment re-reads of large batches; SwiGLU already applies every
+  // fragment to two matrices (and a second row tile would not fit in registers).
+  p.RT = p.NT >= 4 && p.nm == 1 ? 2 : 1;
+  const int rows_wg = p.RT * kTileRows;
+  for (int j = 0; j < n_jobs; ++j) p.groups += static_cast<int>((jobs[j].W->rows + rows_wg - 1) / rows_wg);
+  // Every workgroup streams the activation fragments of its K range through its CU's L2 port
+  // (B x K x 4 bytes for the whole range).  Split K (one extra, tiny finalize launch) only when
+  // that exceeds 512 KB; splits are multiples of 4 block pairs, at least 8 (one per wave).
+  const int np = static_cast<int>(K / 64);
+  const size_t frag_bytes = static_cast<size_t>(p.chunk) * K * 4;
+  int S = static_cast<int>((frag_bytes + (512u << 10) - 1) / (512u << 10));
+  S = std::max(1, std::min({S, np / 8, 8}));
+  int pps = (np + S - 1) / S;
+  pps = (pps + 3) / 4 * 4;
+  p.S = (np + pps - 1) / pps;
+  p.pps = pps;
+  const size_t pb = p.q8 ? 68 : 36;
+  const size_t split_bytes = std::min<size_t>(static_cast<size_t>(pps) * pb, p.max_rb);
+  const size_t units = split_bytes / 16 + ((split_bytes / 16) % 2 == 0 ? 1 : 2);  // odd: distinct banks
+  p.row_stride = static_cast<uint32_t>(units * 16);
+  p.w_stride = static_cast<uint32_t>(rows_wg * p.row_stride);
+  p.lds = std::max<size_t>(static_cast<size_t>(p.nm) * p.w_stride,
+                           static_cast<size_t>(kWavesM) * p.NT * p.RT * p.nm * kWave * 2 * 4);
+  const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
+  if (p.lds > lim) return p;
+  // Layout: the A tables, the scales, the split-K partial sums.
+  p.tab = static_cast<size_t>(p.NT) * (K / 32) * kWave * 16;
+  size_t off = (p.q4 ? p.tab : 0) + (p.q8 ? p.tab : 0) + kMaxTiles * kSeqTile * sizeof(float);
+  off = (off + 255) & ~size_t(255);
+  p.part_off = off;
+  if (p.S > 1) off += static_cast<size_t>(p.groups) * p.S * p.chunk * rows_wg * p.nm * sizeof(float);
+  p.bytes = off;
+  p.ok = true;
+  return p;
+}
+
+}  // namespace
+
+size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
+  const Plan p = plan_mfma(jobs, n_jobs, epi, batch, ldx);
+  return p.ok ? p.bytes : 0;
 }
 
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken) {
   *taken = false;
-  if (mfma_gemv_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return EF_HIP_OK;
-  const size_t K = jobs[0].W->cols;
-  if (K % 256 != 0) return EF_HIP_OK;  // row bytes a multiple of 16 for the LDS-DMA row copies
-  bool any4 = false, any8 = false;
-  size_t max_rb = 0;
-  for (int j = 0; j < n_jobs; ++j) {
-    any4 = any4 || jobs[j].W->qtype == EF_QTYPE_Q4_0;
-    any8 = any8 || jobs[j].W->qtype == EF_QTYPE_Q8_0;
-    max_rb = std::max(max_rb, jobs[j].W->row_bytes);
-    if (jobs[j].x != jobs[0].x || (jobs[j].ldx ? jobs[j].ldx : ldx) != (jobs[0].ldx ? jobs[0].ldx : ldx))
-      return EF_HIP_OK;  // one activation matrix per launch
-  }
-  const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
-  if (reinterpret_cast<uintptr_t>(jobs[0].x) % 16 != 0 || xld % 4 != 0) return EF_HIP_OK;
+  const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, ldx);
+  if (!pl.ok) return EF_HIP_OK;
   if (norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 != 0) return EF_HIP_OK;
-  const int nm = epi == kEpiSwiglu ? 2 : 1;
-  const int max_chunk = kMaxTiles * kSeqTile;
-  const int NT = tiles_for(batch);
-  // Two row tiles halve the fragment re-reads of large batches; SwiGLU already applies every
-  // fragment to two matrices (and a second row tile would not fit in registers).
-  const int RT = NT >= 4 && nm == 1 ? 2 : 1;
-  // LDS: weight rows an odd number of 16-byte units apart; the cross-wave partial sums reuse it
-  MArgs a{};
-  const size_t units = max_rb / 16 + ((max_rb / 16) % 2 == 0 ? 1 : 2);
-  a.row_stride = static_cast<uint32_t>(units * 16);
-  a.w_stride = static_cast<uint32_t>(RT * kTileRows * a.row_stride);
-  const size_t lds = std::max<size_t>(static_cast<size_t>(nm) * a.w_stride,
-                                      static_cast<size_t>(kWavesM) * NT * RT * nm * kWave * 2 * 4);
-  const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
-  if (lds > lim) return EF_HIP_OK;
+  const size_t K = jobs[0].W->cols;
+  const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
   // workspace: the caller's, else a stream-ordered allocation freed after the launches
-  const size_t need = gemv_mfma_workspace_bytes(batch, K, any4, any8);
   void* buf = ws;
   bool own = false;
-  if (buf == nullptr || ws_bytes < need) {
-    EFH_HIP(hipMallocAsync(&buf, need, stream));
+  if (buf == nullptr || ws_bytes < pl.bytes) {
+    EFH_HIP(hipMallocAsync(&buf, pl.bytes, stream));
     own = true;
   }
   uint8_t* base = static_cast<uint8_t*>(buf);
-  const size_t tab = static_cast<size_t>(NT) * (K / 32) * kWave * 16;
-  uint8_t* t4 = any4 ? base : nullptr;
-  uint8_t* t8 = any8 ? base + (any4 ? tab : 0) : nullptr;
-  float* post = reinterpret_cast<float*>(base + (any4 ? tab : 0) + (any8 ? tab : 0));
-  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(RT, NT)
-                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(RT, NT) : pick_mfma<kEpiSwiglu>(RT, NT));
+  uint8_t* t4 = pl.q4 ? base : nullptr;
+  uint8_t* t8 = pl.q8 ? base + (pl.q4 ? pl.tab : 0) : nullptr;
+  float* post = reinterpret_cast<float*>(base + (pl.q4 ? pl.tab : 0) + (pl.q8 ? pl.tab : 0));
   int rc = EF_HIP_OK;
-  for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += max_chunk) {
-    const int nb = std::min(max_chunk, batch - b0);
+  MArgs a{};
+  a.row_stride = pl.row_stride;
+  a.w_stride = pl.w_stride;
+  a.ksplit = pl.S;
+  a.pairs_per_split = pl.pps;
+  a.part = reinterpret_cast<float*>(base + pl.part_off);
+  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(pl.RT, pl.NT)
+                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(pl.RT, pl.NT)
+                                                     : pick_mfma<kEpiSwiglu>(pl.RT, pl.NT));
+  const int rows_wg = pl.RT * kTileRows;
+  for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += pl.chunk) {
+    const int nb = std::min(pl.chunk, batch - b0);
     PrepArgs p{};
     p.x = jobs[0].x + b0 * xld;
     p.ldx = static_cast<long>(xld);
@@ -493,11 +602,11 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
     p.t4 = t4;
     p.t8 = t8;
     p.post = post;
-    hipLaunchKernelGGL(xfrag_kernel, dim3(kPrepSplit, NT), dim3(kTP), 0, stream, p);  // tiles past B get zeros
+    hipLaunchKernelGGL(xfrag_kernel, dim3(kPrepSplit, pl.NT), dim3(kTP), 0, stream, p);  // tiles past B get zeros
     a.n_jobs = n_jobs;
     a.K = static_cast<int>(K);
     a.B = nb;
-    a.n_tiles = NT;
+    a.n_tiles = pl.NT;
     a.t4 = t4;
     a.t8 = t8;
     a.post = post;
@@ -513,11 +622,31 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
       d.row_bytes = static_cast<int>(jobs[j].W->row_bytes);
       d.ldy = static_cast<long>(yld);
       d.tile_begin = tiles;
-      tiles += (d.rows + RT * kTileRows - 1) / (RT * kTileRows);
+      tiles += (d.rows + rows_wg - 1) / rows_wg;
     }
     void* params[] = {&a};
-    const hipError_t e = hipLaunchKernel(fn, dim3(tiles), dim3(kT), params, lds, stream);
-    if (e != hipSuccess) rc = fail_hip(e, "gemv_mfma_kernel");
+    hipError_t e = hipLaunchKernel(fn, dim3(tiles * pl.S), dim3(kT), params, pl.lds, stream);
+    if (e != hipSuccess) {
+      rc = fail_hip(e, "gemv_mfma_kernel");
+      break;
+    }
+    if (pl.S > 1) {
+      FinArgs f{};
+      for (int j = 0; j < n_jobs; ++j) f.job[j] = a.job[j];
+      f.n_jobs = n_jobs;
+      f.B = nb;
+      f.rows_wg = rows_wg;
+      f.S = pl.S;
+      f.total = tiles * rows_wg * nb;
+      f.part = a.part;
+      f.post = post;
+      void* fin = epi == kEpiStore ? reinterpret_cast<void*>(&finalize_kernel<kEpiStore>)
+                                   : (epi == kEpiResidual ? reinterpret_cast<void*>(&finalize_kernel<kEpiResidual>)
+                                                          : reinterpret_cast<void*>(&finalize_kernel<kEpiSwiglu>));
+      void* fparams[] = {&f};
+      e = hipLaunchKernel(fin, dim3((f.total + 255) / 256), dim3(256), fparams, 0, stream);
+      if (e != hipSuccess) rc = fail_hip(e, "finalize_kernel");
+    }
   }
   if (own) {
     const hipError_t e = hipFreeAsync(buf, stream);

@@ -1,0 +1,100 @@
+"""GPU parity of the batched (2+ sequences) packed GEMV on the matrix cores (C-ABI calls).
+
+Every sequence of a batch must meet the single-vector gates:
+|gpu - exact| <= 1e-5 * sum|w x| per row (tests/test_qinfer.cpp:95) and max |gpu - cpu fp32| <= 1e-4
+against the oracle's AVX2 kernel (src/qkernels.cpp:131-180) on that sequence alone.  Shapes cover
+batches that are not a multiple of the 8-sequence tile, more than 64 sequences (several launches),
+row counts that leave a partial workgroup, Q8_0, a K split (K = 5632 at B = 64) and mixed-type
+launches; epilogues and the fused RMSNorm are checked against the oracle's separate operations.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 1e-4
+REL_TOL = 1e-5
+
+
+def _batch_x(seed, batch, cols):
+    return np.stack([D.activations_with_outliers(seed + b, cols) for b in range(batch)]).astype(np.float32)
+
+
+@pytest.mark.parametrize("qtype,rows,cols,batch", [
+    (O.Q4_0, 512, 2048, 5),      # one partial sequence tile
+    (O.Q8_0, 300, 2048, 16),     # Q8_0, rows leave a partial workgroup
+    (O.Q4_0, 2048, 5632, 64),    # K split across workgroups
+    (O.Q4_0, 37, 256, 70),       # two launches (64 + 6 sequences), tiny K
+    (O.Q8_0, 64, 512, 2),
+])
+def test_batched_gemv_each_sequence_meets_the_gates(hip, qtype, rows, cols, batch):
+    print(f"[case] batched gemv qtype={qtype} {rows}x{cols} B={batch}", flush=True)
+    packed = D.random_rows(qtype, rows, cols, seed=rows + cols + batch)
+    X = _batch_x(1000 + batch, batch, cols)
+    W = hip.Weight(qtype, rows, cols, host=packed)
+    dx = hip.DeviceArray.from_host(X)
+    dy = hip.DeviceArray((batch, rows))
+    hip.matvec(W, dx, dy, batch=batch)
+    got = dy.numpy()
+    w64 = D.dequant_exact(qtype, packed, cols)
+    for b in range(batch):
+        assert D.rel_dot_error(w64, X[b], got[b]).max() < REL_TOL, b
+        cpu = O.matvec(qtype, packed.reshape(-1), X[b], backend=O.AVX2)
+        assert np.abs(got[b] - cpu).max() <= ABS_TOL + 1e-5 * np.abs(cpu).max(), b
+    hip.matvec(W, dx, dy, batch=batch)
+    assert np.array_equal(dy.numpy().view(np.uint32), got.view(np.uint32))  # reproducible bits
+
+
+def test_batched_swiglu_and_residual_chain(hip):
+    """Transformer::forward's FFN chain (src/model.cpp:249-262) for 64 sequences at once."""
+    B, D_, F = 64, 2048, 5632
+    X = np.stack([D.normal(40 + b, D_) for b in range(B)]).astype(np.float32)
+    nw = (1.0 + 0.1 * D.normal(41, D_)).astype(np.float32)
+    g = O.quantize(O.Q4_0, D.normal(42, (F, D_), 0.02))
+    u = O.quantize(O.Q4_0, D.normal(43, (F, D_), 0.02))
+    dn = O.quantize(O.Q4_0, D.normal(44, (D_, F), 0.02))
+    G, U, Dn = (hip.Weight(O.Q4_0, F, D_, host=g), hip.Weight(O.Q4_0, F, D_, host=u),
+                hip.Weight(O.Q4_0, D_, F, host=dn))
+    dx = hip.DeviceArray.from_host(X)
+    dnw = hip.DeviceArray.from_host(nw)
+    dact = hip.DeviceArray((B, F))
+    hip.matvec_swiglu(G, U, dx, dact, norm_w=dnw, eps=1e-5, batch=B)
+    hip.matvec_residual(Dn, dact, dx, batch=B)  # K = 5632 at B = 64: split-K with a finalize pass
+    got_act, got = dact.numpy(), dx.numpy()
+    L = O.lib()
+    for b in range(0, B, 9):
+        h = np.empty(D_, np.float32)
+        L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), D_, 1e-5)
+        gate, up = O.matvec_jobs([(O.Q4_0, g, h), (O.Q4_0, u, h)])
+        act = np.empty_like(gate)
+        L.efo_swiglu(O.ptr(act, O._f32p), O.ptr(gate, O._f32p), O.ptr(up, O._f32p), F)
+        assert np.abs(got_act[b] - act).max() <= ABS_TOL, b
+        ref = X[b] + O.matvec(O.Q4_0, dn.reshape(-1), got_act[b])
+        assert np.abs(got[b] - ref).max() <= ABS_TOL, b
+
+
+def test_batched_mixed_type_jobs_with_norm(hip):
+    """q/k/v with k, v stored Q8_0 in one launch for 8 sequences, input RMSNorm fused."""
+    B, cols = 8, 2048
+    X = np.stack([D.normal(60 + b, cols) for b in range(B)]).astype(np.float32)
+    nw = (1.0 + 0.05 * D.normal(61, cols)).astype(np.float32)
+    shapes = [(O.Q4_0, 2048), (O.Q8_0, 256), (O.Q8_0, 256)]
+    keep, ws, outs = [], [], []
+    for i, (qt, rows) in enumerate(shapes):
+        packed = O.quantize(qt, D.normal(70 + i, (rows, cols), 0.02))
+        keep.append(packed)
+        ws.append(hip.Weight(qt, rows, cols, host=packed))
+        outs.append(hip.DeviceArray((B, 2048)))  # one output stride for the launch (the C-ABI's ldy)
+    dx = hip.DeviceArray.from_host(X)
+    hip.matvec_jobs_rmsnorm([(ws[i], dx, outs[i]) for i in range(3)], hip.DeviceArray.from_host(nw), 1e-5, batch=B,
+                            ldx=cols, ldy=2048)
+    L = O.lib()
+    for b in range(B):
+        h = np.empty(cols, np.float32)
+        L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), cols, 1e-5)
+        for i, (qt, rows) in enumerate(shapes):
+            cpu = O.matvec(qt, keep[i].reshape(-1), h)
+            assert np.abs(outs[i].numpy()[b, :rows] - cpu).max() <= ABS_TOL, (b, i)
