@@ -23,6 +23,7 @@ struct GemvJob {
 struct ShapeOverride {
   int G = 0, R = 0;  // 0: the launcher's own choice
   int path = 0;      // 0 auto, 1 LDS-DMA kernel, 2 register-fetch kernel
+  int waves = 0;     // waves per workgroup of the LDS-DMA kernel (0: the launcher's choice)
 };
 const ShapeOverride& shape_override();
 bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU kernels

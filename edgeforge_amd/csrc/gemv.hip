@@ -406,10 +406,11 @@ __device__ __forceinline__ void dma_body(const float* lds_x, const float* lds_xs
   }
 }
 
-template <int EPI, int G, int R>
-__global__ __launch_bounds__(kThreads) void gemv_dma_kernel(Args a) {
+template <int EPI, int G, int R, int NW>
+__global__ __launch_bounds__(NW * kWave) void gemv_dma_kernel(Args a) {
+  constexpr int NT = NW * kWave;
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  __shared__ double red[kWaves];
+  __shared__ double red[NW];
   constexpr int RW = (kWave / G) * R;
   constexpr int RR = EPI == kEpiSwiglu ? 2 * R : R;
   const int K = a.K, np = K >> 6;
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void gemv_dma_kernel(Args a) {
     dma_span<kNonTemporal>(make_rsrc(jb.W, mat_bytes), src, wl, (region + 15u) & ~15u, lane);
     if (EPI == kEpiSwiglu)
       dma_span<kNonTemporal>(make_rsrc(jb.W2, mat_bytes), src, wl + a.w_stride, (region + 15u) & ~15u, lane);
-    const uint32_t xq = static_cast<uint32_t>(K);  // bytes of x per wave (a quarter of 4K)
+    const uint32_t xq = static_cast<uint32_t>(K) * 4u / NW;  // bytes of x per wave (a multiple of 16)
     const float* xb = jb.x + b * jb.ldx;
     dma_span<0>(make_rsrc(xb, static_cast<uint32_t>(K) * 4u), wave * xq, lb + a.raw_x_off + wave * xq, xq, lane);
     if (a.norm_w != nullptr)
@@ -448,14 +449,16 @@ __global__ __launch_bounds__(kThreads) void gemv_dma_kernel(Args a) {
     float inv = 1.0f;
     if (a.norm_w != nullptr) {
       double ss = 0.0;
-      for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) ss += sq_d(*reinterpret_cast<const float4*>(raw_x + i));
+      for (int i = threadIdx.x * 4; i < K; i += NT * 4) ss += sq_d(*reinterpret_cast<const float4*>(raw_x + i));
       ss = wave_sum_d(ss);
       if (lane == 0) red[wave] = ss;
       __syncthreads();
-      const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+      double tot = 0.0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) tot += red[w];  // waves in order
       inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)));
     }
-    for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) {
+    for (int i = threadIdx.x * 4; i < K; i += NT * 4) {
       float4 v = *reinterpret_cast<const float4*>(raw_x + i);
       if (a.norm_w != nullptr) v = norm4(v, *reinterpret_cast<const float4*>(raw_nw + i), inv);
       store_x4(v, i, lds_x, lds_xs);
@@ -584,25 +587,31 @@ void* pick_pairs_kernel(int G, int R, int npl) {
   return pick_pairs_kernel_r<EPI, 8>(R, npl);
 }
 
-template <int EPI, int G>
+template <int EPI, int G, int NW>
 void* pick_dma_kernel_r(int R) {
-  if (R == 4) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 4>);
-  if (R == 2) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 2>);
-  return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 1>);
+  if (R == 4) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 4, NW>);
+  if (R == 2) return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 2, NW>);
+  return reinterpret_cast<void*>(&gemv_dma_kernel<EPI, G, 1, NW>);
+}
+
+template <int EPI, int NW>
+void* pick_dma_kernel_g(int G, int R) {
+  if (G == 32) return pick_dma_kernel_r<EPI, 32, NW>(R);
+  if (G == 16) return pick_dma_kernel_r<EPI, 16, NW>(R);
+  return pick_dma_kernel_r<EPI, 8, NW>(R);
 }
 
 template <int EPI>
-void* pick_dma_kernel(int G, int R) {
-  if (G == 32) return pick_dma_kernel_r<EPI, 32>(R);
-  if (G == 16) return pick_dma_kernel_r<EPI, 16>(R);
-  return pick_dma_kernel_r<EPI, 8>(R);
+void* pick_dma_kernel(int G, int R, int nw) {
+  return nw == 8 ? pick_dma_kernel_g<EPI, 8>(G, R) : pick_dma_kernel_g<EPI, 4>(G, R);
 }
 
 }  // namespace
 
 // Tuning knobs, read once per process: EF_HIP_GEMV_SHAPE="G,R" (G in {8,16,32}, R in {1,2,4}) forces
 // the lane-group size and rows per group of the cols % 64 == 0 kernels; EF_HIP_GEMV_PATH=dma|regs
-// forces the LDS-DMA or the register-fetch kernel.
+// forces the LDS-DMA or the register-fetch kernel; EF_HIP_GEMV_WAVES=4|8 sets the DMA kernel's waves
+// per workgroup.
 const ShapeOverride& shape_override() {
   static const ShapeOverride ov = [] {
     ShapeOverride o;
@@ -613,6 +622,8 @@ const ShapeOverride& shape_override() {
       o.G = g;
       o.R = r;
     }
+    const char* wv = std::getenv("EF_HIP_GEMV_WAVES");
+    if (wv != nullptr && (std::atoi(wv) == 4 || std::atoi(wv) == 8)) o.waves = std::atoi(wv);
     const char* pth = std::getenv("EF_HIP_GEMV_PATH");
     if (pth != nullptr) o.path = std::strcmp(pth, "dma") == 0 ? 1 : (std::strcmp(pth, "regs") == 0 ? 2 : 0);
     return o;
@@ -662,7 +673,7 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   const int nmat = epi == kEpiSwiglu ? 2 : 1;
   // LDS of the DMA path for R rows per lane group: x slots + block sums, raw x (+ raw norm
   // weights), then per wave and matrix the wave's RW rows.
-  auto dma_layout = [&](int g, int r, Args* out) -> size_t {
+  auto dma_layout = [&](int g, int r, int nw, Args* out) -> size_t {
     const size_t rw = static_cast<size_t>(kWave / g) * r;
     size_t wstride = 0;
     for (int j = 0; j < n_jobs; ++j) wstride = std::max(wstride, (rw * jobs[j].W->row_bytes + 15) & ~size_t(15));
@@ -672,7 +683,7 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     const size_t raw_nw = off;
     if (norm_w != nullptr) off += K * 4;
     const size_t w_off = off;
-    off += static_cast<size_t>(kWaves) * nmat * wstride;
+    off += static_cast<size_t>(nw) * nmat * wstride;
     if (out != nullptr) {
       out->raw_x_off = static_cast<uint32_t>(raw_x);
       out->raw_nw_off = static_cast<uint32_t>(raw_nw);
@@ -683,17 +694,22 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   };
   constexpr size_t kDmaLdsTarget = 80 * 1024;  // two workgroups per CU
   const ShapeOverride& ov = shape_override();
-  bool use_dma = fast && ov.path != 2 && dma_layout(G, 1, nullptr) <= kDmaLdsTarget;
-  // rows per tile: 4 waves x (64/G) groups x R rows; R as large as keeps >= 2 tiles per CU
+  // Waves per workgroup of the DMA kernel.  Eight waves spread the per-workgroup staging over
+  // twice the rows but measured slower on MI355X (gate/up 5632x2048: 8.99 us against 8.30 us at
+  // four), so four is the default and eight stays selectable.
+  int nw = ov.waves > 0 ? ov.waves : 4;
+  bool use_dma = fast && ov.path != 2 && dma_layout(G, 1, nw, nullptr) <= kDmaLdsTarget;
+  if (!use_dma) nw = kWaves;
+  // rows per tile: nw waves x (64/G) groups x R rows; R as large as keeps >= 2 tiles per CU
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
   int R = 1;
   if (fast) {
     for (int cand : {4, 2}) {
-      const size_t per_tile = static_cast<size_t>(kWaves * (kWave / G) * cand);
+      const size_t per_tile = static_cast<size_t>(nw * (kWave / G) * cand);
       size_t tiles = 0;
       for (int j = 0; j < n_jobs; ++j) tiles += (jobs[j].W->rows + per_tile - 1) / per_tile;
       if (tiles * static_cast<size_t>(batch) >= static_cast<size_t>(2 * cus) &&
-          (!use_dma || dma_layout(G, cand, nullptr) <= kDmaLdsTarget)) {
+          (!use_dma || dma_layout(G, cand, nw, nullptr) <= kDmaLdsTarget)) {
         R = cand;
         break;
       }
@@ -706,10 +722,11 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   }
   size_t dma_lds = 0;
   if (use_dma) {
-    dma_lds = dma_layout(G, R, &a);
+    dma_lds = dma_layout(G, R, nw, &a);
     const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
     if (dma_lds > lim) use_dma = false;
   }
+  if (!use_dma) nw = kWaves;
   // pairs per lane and chunk of the register path: all of a row's pairs when they fit in four
   int npl = (np + G - 1) / G;
   npl = npl >= 3 ? 4 : npl;
@@ -726,7 +743,7 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     d.row_bytes = static_cast<int>(W->row_bytes);
     d.ldx = static_cast<long>(jobs[j].ldx ? jobs[j].ldx : ldx);
     d.ldy = static_cast<long>(jobs[j].ldy ? jobs[j].ldy : ldy);
-    d.rows_per_tile = fast ? kWaves * (kWave / G) * R : kWaves;
+    d.rows_per_tile = fast ? nw * (kWave / G) * R : kWaves;
     d.tile_begin = tiles;
     tiles += (d.rows + d.rows_per_tile - 1) / d.rows_per_tile;
   }
@@ -734,9 +751,9 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   size_t lds_bytes = (static_cast<size_t>(nslot) * kSlot + K / 32) * sizeof(float);
   void* fn = nullptr;
   if (fast && use_dma) {
-    fn = epi == kEpiStore ? pick_dma_kernel<kEpiStore>(G, R)
-                          : (epi == kEpiResidual ? pick_dma_kernel<kEpiResidual>(G, R)
-                                                 : pick_dma_kernel<kEpiSwiglu>(G, R));
+    fn = epi == kEpiStore ? pick_dma_kernel<kEpiStore>(G, R, nw)
+                          : (epi == kEpiResidual ? pick_dma_kernel<kEpiResidual>(G, R, nw)
+                                                 : pick_dma_kernel<kEpiSwiglu>(G, R, nw));
     lds_bytes = dma_lds;
   } else if (fast) {
     fn = epi == kEpiStore ? pick_pairs_kernel<kEpiStore>(G, R, npl)
@@ -748,7 +765,7 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
                                                  : reinterpret_cast<void*>(&gemv_generic_kernel<kEpiSwiglu>));
   }
   void* params[] = {&a};
-  EFH_HIP(hipLaunchKernel(fn, dim3(tiles, batch), dim3(kThreads), params, lds_bytes, stream));
+  EFH_HIP(hipLaunchKernel(fn, dim3(tiles, batch), dim3(nw * kWave), params, lds_bytes, stream));
   return EF_HIP_OK;
 }
 
