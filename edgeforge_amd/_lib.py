@@ -49,6 +49,12 @@ class ef_hip_layer(C.Structure):
                [("attn_norm_dev", _P), ("ffn_norm_dev", _P)]
 
 
+class ef_hip_efq_tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("rule", C.c_char_p), ("qtype", C.c_int), ("ndim", C.c_int),
+                ("rows", _sz), ("cols", _sz), ("offset", C.c_uint64), ("bytes", C.c_uint64),
+                ("rel_rmse", C.c_double), ("max_abs_err", C.c_double), ("host_data", _P)]
+
+
 # name -> (restype, argtypes); every entry point declared in include/ef_hip.h
 SIGNATURES = {
     "ef_hip_init": (C.c_int, [C.c_int]),
@@ -99,6 +105,27 @@ SIGNATURES = {
     "ef_hip_engine_hidden": (C.c_int, [_P, C.POINTER(_P)]),
     "ef_hip_engine_generate": (C.c_int, [_P, _i32p, _sz, _sz, C.POINTER(ef_hip_sampler_config), _P, _i32p,
                                          C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ef_hip_efq_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "ef_hip_efq_parse": (C.c_int, [_P, _sz, C.POINTER(_P)]),
+    "ef_hip_efq_close": (C.c_int, [_P]),
+    "ef_hip_efq_config": (C.c_int, [_P, C.POINTER(ef_hip_model_config), C.POINTER(C.c_int),
+                                    C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "ef_hip_efq_tensor_count": (C.c_int, [_P, C.POINTER(_sz)]),
+    "ef_hip_efq_tensor_info": (C.c_int, [_P, _sz, C.POINTER(ef_hip_efq_tensor)]),
+    "ef_hip_efq_find": (C.c_int, [_P, C.c_char_p, C.POINTER(_sz)]),
+    "ef_hip_efq_bytes_per_token": (C.c_int, [_P, _u64p]),
+    "ef_hip_efq_policy": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                    C.POINTER(_sz), C.c_char_p, _sz]),
+    "ef_hip_model_load_efq": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "ef_hip_model_upload": (C.c_int, [_P, C.POINTER(_P)]),
+    "ef_hip_model_free": (C.c_int, [_P]),
+    "ef_hip_model_config_get": (C.c_int, [_P, C.POINTER(ef_hip_model_config), C.POINTER(C.c_int),
+                                          C.POINTER(C.c_int64)]),
+    "ef_hip_model_description": (C.c_int, [_P, C.c_char_p, _sz]),
+    "ef_hip_model_bytes_per_token": (C.c_int, [_P, _u64p]),
+    "ef_hip_model_layer": (C.c_int, [_P, _sz, C.POINTER(ef_hip_layer)]),
+    "ef_hip_model_tensors": (C.c_int, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)]),
+    "ef_hip_model_engine_create": (C.c_int, [_P, _sz, C.c_int, C.POINTER(_P)]),
 }
 
 _lib = None

@@ -12,6 +12,7 @@
 // One step per layer: [rmsnorm + q/k/v GEMV] -> [RoPE + attention, cache write] -> [o GEMV +
 // residual] -> [rmsnorm + gate/up GEMV + SwiGLU] -> [down GEMV + residual]; then [final rmsnorm +
 // lm_head GEMV] and the token pick (argmax or the sampler) when logits are needed.
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <map>
@@ -50,6 +51,7 @@ struct ef_hip_engine_s {
   std::map<int, hipGraphExec_t> graphs;
   ef_hip_sampler_config scfg{};
   void* rng = nullptr;
+  std::atomic<int>* owner_refs = nullptr;  // live-engine count of the device model it was made from
 };
 
 namespace efh {
@@ -70,7 +72,9 @@ int dev_alloc(ef_hip_engine e, T** p, size_t count) {
   return EF_HIP_OK;
 }
 
-int check_matrix(ef_hip_weight w, size_t rows, size_t cols, bool packed, const char* what) {
+// Every storage type runs through the GEMVs (Q4_0 / Q8_0 packed, F32 / F16 / BF16 dense), as
+// kern::matvec_rows dispatches all five (src/qkernels.cpp:213-269).
+int check_matrix(ef_hip_weight w, size_t rows, size_t cols, const char* what) {
   int rc = check_weight(w);
   if (rc != EF_HIP_OK) return fail(rc, std::string(what) + ": bad weight handle");
   if (w->rows != rows || w->cols != cols) {
@@ -78,8 +82,10 @@ int check_matrix(ef_hip_weight w, size_t rows, size_t cols, bool packed, const c
                                    std::to_string(w->cols) + ", config needs " + std::to_string(rows) + "x" +
                                    std::to_string(cols));
   }
-  if (packed && w->qtype != EF_QTYPE_Q4_0 && w->qtype != EF_QTYPE_Q8_0)
-    return fail(EF_HIP_EINVAL, std::string(what) + ": the decode GEMVs need Q4_0 or Q8_0 weights");
+  if (!is_dense_qtype(w->qtype) && cols % 32 != 0)
+    return fail(EF_HIP_EINVAL, std::string(what) + ": Q4_0 / Q8_0 need cols % 32 == 0");
+  if (is_dense_qtype(w->qtype) && cols > kMaxDenseCols)
+    return fail(EF_HIP_EINVAL, std::string(what) + ": F32 / F16 / BF16 matrices need cols <= 16320");
   return EF_HIP_OK;
 }
 
@@ -182,6 +188,8 @@ int run_step(ef_hip_engine e, int mode) {
 }
 
 }  // namespace
+void engine_set_owner(ef_hip_engine e, std::atomic<int>* refs) { e->owner_refs = refs; }
+
 }  // namespace efh
 
 using namespace efh;
@@ -206,18 +214,18 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   const size_t kvd = c.KV * c.hd;
   for (size_t l = 0; l < c.L; ++l) {
     const ef_hip_layer& w = layers[l];
-    EFH_RC(check_matrix(w.wq, c.D, c.D, true, "q_proj"));
-    EFH_RC(check_matrix(w.wk, kvd, c.D, true, "k_proj"));
-    EFH_RC(check_matrix(w.wv, kvd, c.D, true, "v_proj"));
-    EFH_RC(check_matrix(w.wo, c.D, c.D, true, "o_proj"));
-    EFH_RC(check_matrix(w.w_gate, c.F, c.D, true, "gate_proj"));
-    EFH_RC(check_matrix(w.w_up, c.F, c.D, true, "up_proj"));
-    EFH_RC(check_matrix(w.w_down, c.D, c.F, true, "down_proj"));
+    EFH_RC(check_matrix(w.wq, c.D, c.D, "q_proj"));
+    EFH_RC(check_matrix(w.wk, kvd, c.D, "k_proj"));
+    EFH_RC(check_matrix(w.wv, kvd, c.D, "v_proj"));
+    EFH_RC(check_matrix(w.wo, c.D, c.D, "o_proj"));
+    EFH_RC(check_matrix(w.w_gate, c.F, c.D, "gate_proj"));
+    EFH_RC(check_matrix(w.w_up, c.F, c.D, "up_proj"));
+    EFH_RC(check_matrix(w.w_down, c.D, c.F, "down_proj"));
     EFH_CHECK(w.w_gate->qtype == w.w_up->qtype, "gate_proj and up_proj must share a storage type");
     EFH_CHECK(w.attn_norm_dev && w.ffn_norm_dev, "engine_create: null norm weights");
   }
-  EFH_RC(check_matrix(lm_head, c.V, c.D, true, "lm_head"));
-  EFH_RC(check_matrix(embed, c.V, c.D, false, "embed_tokens"));
+  EFH_RC(check_matrix(lm_head, c.V, c.D, "lm_head"));
+  EFH_RC(check_matrix(embed, c.V, c.D, "embed_tokens"));
 
   auto* e = new ef_hip_engine_s;
   e->c = c;
@@ -321,6 +329,7 @@ int ef_hip_engine_destroy(ef_hip_engine e) {
   for (void* p : e->allocs) (void)hipFree(p);
   if (e->stage) (void)hipHostFree(e->stage);
   (void)hipStreamDestroy(e->stream);
+  if (e->owner_refs != nullptr) e->owner_refs->fetch_sub(1);
   delete e;
   return EF_HIP_OK;
 }

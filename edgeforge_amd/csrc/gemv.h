@@ -36,6 +36,15 @@ size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int b
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 
+// F32 / F16 / BF16 weights (gemv_dense.hip): same jobs, epilogues and fused RMSNorm, any cols up to
+// kMaxDenseCols; all jobs of one launch share the type.  launch_gemv routes these types here.
+constexpr size_t kMaxDenseCols = 16320;
+bool is_dense_qtype(int qtype);
+int launch_gemv_dense(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch,
+                      size_t ldx, size_t ldy, hipStream_t stream);
+
+// Any storage type.  Jobs of one launch share cols (and x); a launch that mixes packed and
+// unquantized matrices is split into one launch per kind.
 int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                 size_t ldy, hipStream_t stream, void* ws = nullptr, size_t ws_bytes = 0);
 

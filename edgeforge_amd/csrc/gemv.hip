@@ -638,6 +638,34 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   EFH_CHECK(n_jobs >= 1 && n_jobs <= kMaxJobs, "gemv: 1..4 jobs per launch");
   EFH_CHECK(batch >= 1 && batch <= 65535, "gemv: batch must be in [1, 65535]");
   EFH_CHECK(epi >= kEpiStore && epi <= kEpiSwiglu, "gemv: unknown epilogue");
+  int n_dense = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    EFH_CHECK(jobs[j].W && jobs[j].x && jobs[j].y, "gemv: null weight / x / y");
+    n_dense += is_dense_qtype(jobs[j].W->qtype) ? 1 : 0;
+  }
+  if (n_dense > 0) {
+    for (int j = 0; j < n_jobs; ++j)
+      EFH_CHECK(jobs[j].W->cols == jobs[0].W->cols, "gemv: all jobs of one launch need the same cols");
+    if (batch > 1) {
+      for (int j = 0; j < n_jobs; ++j) {
+        EFH_CHECK((jobs[j].ldx ? jobs[j].ldx : ldx) >= jobs[j].W->cols, "gemv: ldx smaller than cols");
+        EFH_CHECK((jobs[j].ldy ? jobs[j].ldy : ldy) >= jobs[j].W->rows, "gemv: ldy smaller than rows");
+      }
+    }
+    // one launch per unquantized type, then one for the packed jobs
+    GemvJob group[kMaxJobs];
+    for (int qt : {EF_QTYPE_F32, EF_QTYPE_F16, EF_QTYPE_BF16}) {
+      int n = 0;
+      for (int j = 0; j < n_jobs; ++j)
+        if (jobs[j].W->qtype == qt) group[n++] = jobs[j];
+      if (n > 0) EFH_RC(launch_gemv_dense(group, n, epi, norm_w, eps, batch, ldx, ldy, stream));
+    }
+    int n = 0;
+    for (int j = 0; j < n_jobs; ++j)
+      if (!is_dense_qtype(jobs[j].W->qtype)) group[n++] = jobs[j];
+    if (n == 0) return EF_HIP_OK;
+    return launch_gemv(group, n, epi, norm_w, eps, batch, ldx, ldy, stream, ws, ws_bytes);
+  }
   const size_t K = jobs[0].W ? jobs[0].W->cols : 0;
   EFH_CHECK(K >= 32 && K % 32 == 0 && K <= kMaxCols, "gemv: cols must be a multiple of 32 in [32, 14336]");
   for (int j = 0; j < n_jobs; ++j) {

@@ -506,6 +506,7 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   const size_t K = jobs[0].W->cols;
   if (K % 256 != 0) return p;  // pairs come in 16-byte multiples of 4 for the LDS-DMA row copies
   for (int j = 0; j < n_jobs; ++j) {
+    if (jobs[j].W->qtype != EF_QTYPE_Q4_0 && jobs[j].W->qtype != EF_QTYPE_Q8_0) return Plan{};
     p.q4 = p.q4 || jobs[j].W->qtype == EF_QTYPE_Q4_0;
     p.q8 = p.q8 || jobs[j].W->qtype == EF_QTYPE_Q8_0;
     p.max_rb = std::max(p.max_rb, jobs[j].W->row_bytes);

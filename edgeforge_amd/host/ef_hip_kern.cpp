@@ -93,17 +93,11 @@ ef_hip_weight weight_of(const WeightView& W) {
   return h;
 }
 
-bool packed(const WeightView& W) { return W.type == QType::Q4_0 || W.type == QType::Q8_0; }
-
 // Runs a group of same-width jobs with device x / y, staging host pointers.
 void run_jobs_locked(const kern::MatvecJob* jobs, std::size_t n) {
   std::vector<ef_hip_job> dj(n);
   std::size_t xfloats = 0, yfloats = 0;
   for (std::size_t j = 0; j < n; ++j) {
-    if (!packed(*jobs[j].W)) {
-      record("ef::hip::matvec: the GPU GEMV reads Q4_0 / Q8_0 weights, got another storage type");
-      return;
-    }
     if (!is_device(jobs[j].x)) xfloats += jobs[j].W->cols;
     if (!is_device(jobs[j].y)) yfloats += jobs[j].W->rows;
   }

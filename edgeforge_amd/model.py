@@ -121,9 +121,15 @@ class DeviceModel:
 class Engine:
     """ef_hip_engine: Transformer::forward on the device for `batch` sequences."""
 
-    def __init__(self, model: DeviceModel, max_seq: int, batch: int = 1):
+    def __init__(self, model, max_seq: int, batch: int = 1):
+        """model: a DeviceModel, or a device model handle holder with .h (qfile.EfqModel)."""
         self.model, self.max_seq, self.batch = model, max_seq, batch
         cfg = model.cfg
+        if not isinstance(model, DeviceModel):
+            h = C.c_void_p()
+            EL.call("ef_hip_model_engine_create", model.h, max_seq, batch, C.byref(h))
+            self.h = h.value
+            return
         layers = (EL.ef_hip_layer * cfg.L)()
         for l in range(cfg.L):
             layers[l] = EL.ef_hip_layer(*[model.weights[(l, n)].handle for n in LAYER_MATS],

@@ -72,11 +72,13 @@ int ef_hip_weight_release(ef_hip_weight w);
 int ef_hip_weight_info(ef_hip_weight w, int* qtype, size_t* rows, size_t* cols, const void** dev_bytes);
 int ef_hip_row_bytes(int qtype, size_t cols, size_t* out); /* src/quant.cpp:136-149 */
 
-/* ---- packed GEMV -----------------------------------------------------------------------------
+/* ---- GEMV ------------------------------------------------------------------------------------
  * y[b][r] = sum_c W[r][c] * x[b][c] for b < batch, r < rows (FP32 activations, FP32 result).
  * Replaces kern::matvec (include/ef/qkernels.h:66, src/qkernels.cpp:275-278) and, with batch > 1,
  * the loop over independent sequences the reference would run.  ldx / ldy are the row strides
- * (in floats) of x and y.  Q4_0 / Q8_0 read the 18 / 34-byte blocks in place.  Results agree with
+ * (in floats) of x and y.  All five storage types, as kern::matvec_rows (src/qkernels.cpp:213-269):
+ * Q4_0 / Q8_0 read the 18 / 34-byte blocks in place (cols % 32 == 0, cols <= 14336); F32 / F16 /
+ * BF16 rows take any cols up to 16320.  Results agree with
  * the reference's FP32 kernels to the rounding of a different summation order (the dot products
  * are reproducible: the same inputs give the same bits on every call). */
 int ef_hip_matvec(ef_hip_weight W, const float* x_dev, float* y_dev, int batch, size_t ldx, size_t ldy, void* stream);
@@ -185,6 +187,60 @@ int ef_hip_engine_hidden(ef_hip_engine e, const float** hidden_dev); /* final-no
 int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n_prompt, size_t n,
                            const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
                            double* prefill_s, double* decode_s);
+
+/* ---- .efq model files -------------------------------------------------------------------------
+ * ef::QuantFile (include/ef/qfile.h:95-124).  ef_hip_efq_open maps a file and validates it as
+ * QuantFile::open / parse_efq do (src/qfile.cpp:125-243): magic, version, header length, strict
+ * JSON header, config.json fields (src/model_config.cpp:72-131), per-tensor type / shape / bytes /
+ * 64-byte alignment / bounds / overlap, exactly the tensors the config needs, and every tensor's
+ * type re-derived from the header's quantization policy.  ef_hip_efq_parse does the same over a
+ * caller's buffer (parse_efq; the buffer must outlive the handle).  Host-only: neither needs a GPU
+ * or ef_hip_init.  A rejected file gives EF_HIP_EINVAL and the reader's message (the reference's
+ * wording: "bad magic", "past the end", "64-byte aligned", "header says", "policy gives", ...). */
+typedef struct ef_hip_efq_s* ef_hip_efq;
+typedef struct {
+  const char* name;        /* valid while the handle lives */
+  const char* rule;        /* policy rule that chose the type: layers, lm_head, embed, norm, override, fallback-bf16 */
+  int qtype;
+  int ndim;                /* 1 (norms) or 2 */
+  size_t rows, cols;       /* a 1-D tensor has rows = 1 */
+  uint64_t offset, bytes;  /* absolute file offset and size */
+  double rel_rmse, max_abs_err;
+  const void* host_data;   /* the tensor's bytes in the mapping */
+} ef_hip_efq_tensor;
+int ef_hip_efq_open(const char* path, ef_hip_efq* out);            /* QuantFile::open, qfile.h:98 */
+int ef_hip_efq_parse(const void* bytes, size_t size, ef_hip_efq* out); /* parse_efq, qfile.h:133 */
+int ef_hip_efq_close(ef_hip_efq f);
+int ef_hip_efq_config(ef_hip_efq f, ef_hip_model_config* cfg, int* tie_word_embeddings, int64_t* bos_token_id,
+                      int64_t* eos_token_id);                      /* QuantFile::config, qfile.h:103 */
+int ef_hip_efq_tensor_count(ef_hip_efq f, size_t* n);              /* QuantFile::tensors, qfile.h:105 */
+int ef_hip_efq_tensor_info(ef_hip_efq f, size_t i, ef_hip_efq_tensor* out);
+int ef_hip_efq_find(ef_hip_efq f, const char* name, size_t* index); /* QuantFile::find / at, qfile.h:106 */
+int ef_hip_efq_bytes_per_token(ef_hip_efq f, uint64_t* out);        /* QuantFile::bytes_per_token, qfile.h:112 */
+/* QuantFile::policy, qfile.h:104 (layers / lm_head / embed types, override count, policy name). */
+int ef_hip_efq_policy(ef_hip_efq f, int* layers, int* lm_head, int* embed, size_t* n_overrides, char* name,
+                      size_t name_cap);
+
+/* ---- a model from an .efq file on the device ------------------------------------------------
+ * Model::load_efq (src/model.cpp:66-111): every tensor of the file copied once into one device
+ * arena in the file's own layout (64-byte aligned tensors), matrices as weight handles over it,
+ * norms as FP32 device arrays, the embedding as the lm_head when tie_word_embeddings is set.
+ * ef_hip_model_upload takes an open file (which may be closed afterwards).  Engines made by
+ * ef_hip_model_engine_create use the model's weights: destroy them before ef_hip_model_free
+ * (which otherwise returns EF_HIP_ESTATE). */
+typedef struct ef_hip_model_s* ef_hip_model;
+int ef_hip_model_load_efq(const char* path, ef_hip_model* out);
+int ef_hip_model_upload(ef_hip_efq f, ef_hip_model* out);
+int ef_hip_model_free(ef_hip_model m);
+int ef_hip_model_config_get(ef_hip_model m, ef_hip_model_config* cfg, int* tie_word_embeddings,
+                            int64_t* eos_token_id);                 /* Model::config, model.h:54 */
+int ef_hip_model_description(ef_hip_model m, char* buf, size_t cap); /* Model::description, model.h:65 */
+int ef_hip_model_bytes_per_token(ef_hip_model m, uint64_t* out);    /* model.h:63 */
+int ef_hip_model_layer(ef_hip_model m, size_t l, ef_hip_layer* out); /* Model::layer, model.h:58 */
+int ef_hip_model_tensors(ef_hip_model m, ef_hip_weight* embed, ef_hip_weight* lm_head,
+                         const float** final_norm_dev);             /* model.h:55-57 */
+/* Transformer(model, max_seq) (include/ef/model.h:101, src/model.cpp:153) for `batch` sequences. */
+int ef_hip_model_engine_create(ef_hip_model m, size_t max_seq, int batch, ef_hip_engine* out);
 
 #ifdef __cplusplus
 }

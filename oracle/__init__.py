@@ -178,6 +178,8 @@ def ref():
         _sig(R, "ref_engine_close", None, _P)
         _sig(R, "ref_engine_bytes_per_token", C.c_uint64, _P)
         _sig(R, "ref_engine_forward", C.c_int, _P, C.c_int32, _sz, C.c_int, _f32p)
+        _sig(R, "ref_efq_parse", C.c_long, _P, _sz, C.c_char_p, _sz)
+        _sig(R, "ref_model_load_efq", C.c_long, C.c_char_p, C.POINTER(C.c_uint64), C.c_char_p, _sz)
         _REF = R
     return _REF
 

@@ -18,11 +18,41 @@ MATS = [("wq", "self_attn.q_proj"), ("wk", "self_attn.k_proj"), ("wv", "self_att
         ("wo", "self_attn.o_proj"), ("w_gate", "mlp.gate_proj"), ("w_up", "mlp.up_proj"), ("w_down", "mlp.down_proj")]
 
 
-def write_efq(path: str, cfg, tensors: dict, layer_type: int = 4, lm_type: int = 3, embed_type: int = 2) -> None:
+def _glob(p: str, s: str) -> bool:
+    """'*' matches any run of characters (include/ef/qfile.h:45-47), by recursion on the pattern."""
+    if not p:
+        return not s
+    if p[0] == "*":
+        return any(_glob(p[1:], s[i:]) for i in range(len(s) + 1))
+    return bool(s) and s[0] == p[0] and _glob(p[1:], s[1:])
+
+
+def _rule(name: str, cols: int, layer_type: int, lm_type: int, embed_type: int, overrides) -> tuple:
+    """(type, rule) the reader re-derives for a tensor (src/qfile.cpp:66-78)."""
+    if "norm" in name:
+        return 0, "norm"
+    t, r = layer_type, "layers"
+    if name == "model.embed_tokens.weight":
+        t, r = embed_type, "embed"
+    if name == "lm_head.weight":
+        t, r = lm_type, "lm_head"
+    for pat, ot in overrides:
+        if _glob(pat, name):
+            t, r = ot, "override"
+    if t in (3, 4) and cols % 32:
+        t, r = 2, "fallback-bf16"
+    return t, r
+
+
+def write_efq(path: str, cfg, tensors: dict, layer_type: int = 4, lm_type: int = 3, embed_type: int = 2,
+              overrides=None, policy: str = "custom", tied: bool = False, extra_config: dict | None = None) -> None:
     """tensors: 'embed', 'lm_head' -> (qtype, bytes[rows, row_bytes]); (l, mat) -> same;
-    (l, 'attn') / (l, 'ffn') / 'final' -> float32 [D].  cfg: D, F, H, KV, hd, V, L, max_pos, eps, rope_theta."""
+    (l, 'attn') / (l, 'ffn') / 'final' -> float32 [D].  cfg: D, F, H, KV, hd, V, L, max_pos, eps, rope_theta.
+    overrides: [(pattern, qtype)] written into the policy (None: one exact-name override per layer
+    matrix whose type differs from layer_type).  tied: no lm_head tensor, tie_word_embeddings true."""
     order = [("model.embed_tokens.weight", "embed", [cfg.V, cfg.D])]
-    overrides = []
+    auto = overrides is None
+    overrides = [] if auto else list(overrides)
     for l in range(cfg.L):
         p = f"model.layers.{l}."
         for key, nm in MATS:
@@ -31,22 +61,22 @@ def write_efq(path: str, cfg, tensors: dict, layer_type: int = 4, lm_type: int =
                           "w_down": (cfg.D, cfg.F)}[key]
             name = p + nm + ".weight"
             order.append((name, (l, key), [rows, cols]))
-            if tensors[(l, key)][0] != layer_type:
-                overrides.append({"pattern": name, "type": TYPE_NAMES[tensors[(l, key)][0]]})
+            if auto and tensors[(l, key)][0] != layer_type:
+                overrides.append((name, tensors[(l, key)][0]))
         order.append((p + "input_layernorm.weight", (l, "attn"), [cfg.D]))
         order.append((p + "post_attention_layernorm.weight", (l, "ffn"), [cfg.D]))
     order.append(("model.norm.weight", "final", [cfg.D]))
-    order.append(("lm_head.weight", "lm_head", [cfg.V, cfg.D]))
+    if not tied:
+        order.append(("lm_head.weight", "lm_head", [cfg.V, cfg.D]))
 
     blobs, entries = [], []
     for name, key, shape in order:
         v = tensors[key]
         if isinstance(v, tuple):
             qt, data = v
-            rule = "embed" if key == "embed" else ("lm_head" if key == "lm_head" else
-                                                   ("override" if qt != layer_type else "layers"))
         else:
-            qt, data, rule = 0, np.ascontiguousarray(v, np.float32), "norm"
+            qt, data = 0, np.ascontiguousarray(v, np.float32)
+        _, rule = _rule(name, shape[-1], layer_type, lm_type, embed_type, overrides)
         raw = np.ascontiguousarray(data).view(np.uint8).reshape(-1).tobytes()
         blobs.append(raw)
         entries.append({"name": name, "type": TYPE_NAMES[qt], "rule": rule, "shape": shape, "bytes": len(raw)})
@@ -54,9 +84,11 @@ def write_efq(path: str, cfg, tensors: dict, layer_type: int = 4, lm_type: int =
               "hidden_size": cfg.D, "intermediate_size": cfg.F, "num_hidden_layers": cfg.L,
               "num_attention_heads": cfg.H, "num_key_value_heads": cfg.KV, "vocab_size": cfg.V,
               "max_position_embeddings": cfg.max_pos, "rms_norm_eps": float(cfg.eps),
-              "rope_theta": float(cfg.rope_theta), "tie_word_embeddings": False, "head_dim": cfg.hd}
+              "rope_theta": float(cfg.rope_theta), "tie_word_embeddings": bool(tied), "head_dim": cfg.hd}
+    config.update(extra_config or {})
     quant = {"layers": TYPE_NAMES[layer_type], "lm_head": TYPE_NAMES[lm_type], "embed": TYPE_NAMES[embed_type],
-             "norms": "F32", "block": 32, "scale": "F16", "policy": "custom", "overrides": overrides}
+             "norms": "F32", "block": 32, "scale": "F16", "policy": policy,
+             "overrides": [{"pattern": p_, "type": TYPE_NAMES[t_]} for p_, t_ in overrides]}
 
     def header(offsets):
         for e, off in zip(entries, offsets):

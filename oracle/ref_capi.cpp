@@ -183,4 +183,42 @@ int ref_engine_forward(void* ve, std::int32_t token, std::size_t pos, int comput
   }
 }
 
+// ---- .efq reader (src/qfile.cpp:125-243, src/model.cpp:66-111): accept / reject with the message
+namespace {
+int put_msg(const std::string& m, char* err, std::size_t cap) {
+  if (err != nullptr && cap > 0) {
+    const std::size_t n = std::min(m.size(), cap - 1);
+    std::memcpy(err, m.data(), n);
+    err[n] = '\0';
+  }
+  return -1;
+}
+}  // namespace
+
+// parse_efq over a buffer: the tensor count, or -1 with the exception text in err.
+long ref_efq_parse(const std::uint8_t* buf, std::size_t n, char* err, std::size_t cap) {
+  try {
+    return static_cast<long>(parse_efq(buf, n).tensors.size());
+  } catch (const Error& e) {
+    return put_msg(e.what(), err, cap);
+  }
+}
+
+// Model::load_efq: bytes per token and the description, or -1 with the message.
+long ref_model_load_efq(const char* path, std::uint64_t* bytes_per_token, char* desc, std::size_t cap) {
+  try {
+    const Model m = Model::load_efq(path);
+    if (bytes_per_token) *bytes_per_token = m.weight_bytes_per_token();
+    if (desc != nullptr && cap > 0) {
+      const std::string& d = m.description();
+      const std::size_t k = std::min(d.size(), cap - 1);
+      std::memcpy(desc, d.data(), k);
+      desc[k] = '\0';
+    }
+    return 0;
+  } catch (const Error& e) {
+    return put_msg(e.what(), desc, cap);
+  }
+}
+
 }  // extern "C"

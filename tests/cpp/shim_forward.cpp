@@ -175,16 +175,31 @@ int main() {
   }
   check(threw, "empty vocabulary throws ef::Error (src/sampler.cpp:14)");
 
-  // noexcept GEMV failures are sticky and surface as ef::Error
+  // every storage type goes through the GPU GEMV: the BF16 embedding as a matrix (tied lm_head)
+  std::vector<float> ye(d.V);
+  ef::hip::matvec(ye.data(), emb, x.data());
+  ef::hip::throw_if_error();
+  double bf_err = 0.0;
+  for (std::size_t r = 0; r < d.V; ++r) {
+    const float want = efo_dot_bf16_avx2(reinterpret_cast<const std::uint16_t*>(embed.data()) + r * d.D, x.data(), d.D);
+    bf_err = std::max(bf_err, std::fabs(static_cast<double>(ye[r]) - want));
+  }
+  check(bf_err <= 1e-4, "BF16 matvec within 1e-4 of dot_bf16_avx2");
+
+  // noexcept GEMV failures are sticky and surface as ef::Error: a Q4_0 row longer than the GPU
+  // kernels take (14336 columns)
+  const std::size_t wide = 14368;
+  std::vector<std::uint8_t> wb(wide / 32 * 18, 0x88);
+  std::vector<float> xw(wide, 1.0f);
   float y1 = 0.0f;
-  ef::hip::matvec(&y1, emb, x.data());  // BF16 is not a packed GPU format
+  ef::hip::matvec(&y1, WeightView{QType::Q4_0, wb.data(), 1, wide}, xw.data());
   threw = false;
   try {
     ef::hip::throw_if_error();
   } catch (const ef::Error& e) {
-    threw = std::string(e.what()).find("Q4_0 / Q8_0") != std::string::npos;
+    threw = std::string(e.what()).find("cols must be") != std::string::npos;
   }
-  check(threw, "unsupported weight type -> sticky error -> ef::Error");
+  check(threw, "rejected launch -> sticky error -> ef::Error");
   efo_sampler_destroy(os);
   efo_transformer_destroy(ot);
   std::printf(fails ? "FAILED (%d)\n" : "OK\n", fails);
