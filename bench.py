@@ -95,15 +95,52 @@ def profile_plain(H, L, model, key, qtype, block, batch: int, launches: int = 40
 
 def cpu_baseline(model, prompt, n: int = 32):
     """The reference CPU path (oracle: AVX2 + persistent thread pool, src/qkernels.cpp:131-297,
-    src/threadpool.cpp) on this host, same weights, the reference protocol: (n-1)/decode_s."""
+    src/threadpool.cpp) on this host, same weights, the reference protocol: (n-1)/decode_s, at the
+    default thread count and at one thread (the ladder's first row, src/bench_decode.cpp:73-81)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle as O  # noqa: F401  (checker / baseline only)
     from oracle.model import OracleModel, cpu_threads
     om = OracleModel(model)
     threads = cpu_threads()
-    om.run_once(prompt[:4], 2, threads=threads)  # warm-up (src/bench_decode.cpp:90-95)
-    _, _, pre, dec = om.run_once(prompt, n, threads=threads)
-    return (n - 1) / dec, threads, pre
+    out = {}
+    for t in (threads, 1):
+        om.run_once(prompt[:4], 2, threads=t)  # warm-up (src/bench_decode.cpp:90-95)
+        _, _, pre, dec = om.run_once(prompt, n, threads=t)
+        out[t] = (n - 1) / dec
+    return out[threads], threads, out[1]
+
+
+def cpu_topology() -> tuple[int, int]:
+    """(physical cores, logical CPUs) of this process's affinity set, from /proc/cpuinfo."""
+    try:
+        allowed = os.sched_getaffinity(0)
+    except AttributeError:
+        allowed = set(range(os.cpu_count() or 1))
+    cores, cpu, phys = set(), None, "0"
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                cpu = int(v)
+            elif k == "physical id":
+                phys = v
+            elif k == "core id" and cpu in allowed:
+                cores.add((phys, v))
+    except OSError:
+        pass
+    return (len(cores) or len(allowed)), len(allowed)
+
+
+def membench(L) -> dict:
+    """Achievable HBM read bandwidth (the reference's membench on the GPU): 1 GiB, 3 passes per
+    run, 1 warm-up + 5 timed runs, checksum-verified."""
+    o = L.ef_hip_membench_options(1 << 30, 5, 3, 1)
+    r = L.ef_hip_membench_result()
+    L.call("ef_hip_membench", C.byref(o), C.byref(r))
+    if not r.checksum_ok:
+        raise RuntimeError("membench checksum mismatch")
+    return {"median_gbs": round(r.median_gbps, 1), "best_gbs": round(r.best_gbps, 1), "bytes": r.buffer_bytes}
 
 
 def cpu_model_name() -> str:
@@ -190,6 +227,9 @@ def main() -> int:
     extra["q4_0_5632x2048_b64_us"] = round(q4b_ms * 1e3, 2)
     lm_ms, lm_bytes = profile_plain(H, L, model, "lm_head", L.Q8_0, 34, batch=1)
     extra["lm_head_q8_0_b1_gbs"] = round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1)
+    mb = membench(L)
+    extra["membench_gbs"] = mb["median_gbs"]
+    log(f"[bench] membench (1 GiB read, checksum ok): median {mb['median_gbs']} GB/s, best {mb['best_gbs']} GB/s")
     traffic = None
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_gate_up_b1_traffic.json")
     if os.path.exists(tpath):
@@ -198,11 +238,15 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         t1 = time.time()
-        cpu_tps, threads, _ = cpu_baseline(model, prompt)
-        log(f"[bench] CPU baseline: {cpu_tps:.2f} tok/s on {threads} threads ({time.time() - t1:.1f}s)")
+        cpu_tps, threads, cpu1 = cpu_baseline(model, prompt)
+        phys, logical = cpu_topology()
+        log(f"[bench] CPU baseline: {cpu_tps:.2f} tok/s on {threads} threads, {cpu1:.2f} tok/s on 1 thread "
+            f"({time.time() - t1:.1f}s); {cpu_model_name()}, {phys} physical / {logical} logical CPUs")
         cpu = {"value": round(cpu_tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "value_1_thread": round(cpu1, 3), "physical_cores": phys, "logical_cpus": logical,
+               "cpu_model": cpu_model_name(),
                "sample": "one sequence, 23-token prompt + 32 greedy steps (tok/s = 31/decode_s), full config-5 "
-                         f"weights, oracle AVX2 + thread pool, {cpu_model_name()}"}
+                         "weights, oracle AVX2 + thread pool; the same run on 1 thread as value_1_thread"}
 
     out = {
         "metric": "decode tok/s at TinyLlama-1.1B shapes B=1/64; Q4_0 matvec GB/s % of HBM peak",
@@ -224,6 +268,8 @@ def main() -> int:
                    "device": dev, **extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "achievable_gbs": mb["median_gbs"],
+                     "frac_of_achievable": round(achieved / mb["median_gbs"], 4),
                      "kernel": "gemv_dma_kernel<swiglu> (gate+up Q4_0 5632x2048, B=1, fused RMSNorm + SwiGLU)",
                      "avg_us": round(avg_ms * 1e3, 3), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,

@@ -55,6 +55,16 @@ class ef_hip_efq_tensor(C.Structure):
                 ("rel_rmse", C.c_double), ("max_abs_err", C.c_double), ("host_data", _P)]
 
 
+class ef_hip_membench_options(C.Structure):
+    _fields_ = [("buffer_bytes", C.c_uint64), ("runs", C.c_int), ("passes", C.c_int), ("warmup_runs", C.c_int)]
+
+
+class ef_hip_membench_result(C.Structure):
+    _fields_ = [("buffer_bytes", C.c_uint64), ("passes", C.c_int), ("bytes_per_run", C.c_uint64),
+                ("best_gbps", C.c_double), ("median_gbps", C.c_double), ("worst_gbps", C.c_double),
+                ("checksum", C.c_uint64), ("expected_checksum", C.c_uint64), ("checksum_ok", C.c_int)]
+
+
 # name -> (restype, argtypes); every entry point declared in include/ef_hip.h
 SIGNATURES = {
     "ef_hip_init": (C.c_int, [C.c_int]),
@@ -105,6 +115,8 @@ SIGNATURES = {
     "ef_hip_engine_hidden": (C.c_int, [_P, C.POINTER(_P)]),
     "ef_hip_engine_generate": (C.c_int, [_P, _i32p, _sz, _sz, C.POINTER(ef_hip_sampler_config), _P, _i32p,
                                          C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ef_hip_membench": (C.c_int, [C.POINTER(ef_hip_membench_options), C.POINTER(ef_hip_membench_result)]),
+    "ef_hip_membench_expected_pass_sum": (C.c_uint64, [C.c_uint64]),
     "ef_hip_efq_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "ef_hip_efq_parse": (C.c_int, [_P, _sz, C.POINTER(_P)]),
     "ef_hip_efq_close": (C.c_int, [_P]),

@@ -153,6 +153,25 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
                           const float* x_dev, const float* norm_w_dev, float eps, float* y_dev, int batch,
                           int launches, void* stream, float* avg_ms);
 
+/* Achievable HBM read bandwidth (membench, include/ef/membench.h:21-54, src/membench.cpp): sums a
+ * buffer of pattern words w[i] = i * 0x9E3779B97F4A7C15 + 0x0123456789ABCDEF `passes` times per run
+ * on every CU and checks the sum against the closed form; decimal GB/s of the timed runs.  The
+ * buffer is rounded down to a whole sweep of the grid (buffer_bytes in the result). */
+typedef struct {
+  uint64_t buffer_bytes; /* default in the reference: 1 GiB */
+  int runs, passes, warmup_runs;
+} ef_hip_membench_options;
+typedef struct {
+  uint64_t buffer_bytes;
+  int passes;
+  uint64_t bytes_per_run;
+  double best_gbps, median_gbps, worst_gbps;
+  uint64_t checksum, expected_checksum;
+  int checksum_ok; /* every run, warm-up included, matched */
+} ef_hip_membench_result;
+int ef_hip_membench(const ef_hip_membench_options* options, ef_hip_membench_result* result);
+uint64_t ef_hip_membench_expected_pass_sum(uint64_t words); /* membench.h:51 */
+
 /* ---- decode engine ----------------------------------------------------------------------------
  * Transformer::forward (src/model.cpp:184-276) on the device for `batch` independent sequences
  * that share weights, with an FP32 KV cache [L][batch][max_seq][KV*hd] and a per-step HIP graph.
