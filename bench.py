@@ -196,20 +196,23 @@ def main() -> int:
     # ---- B = 1 decode: W warm-up steps, then exactly K timed steps
     eng = Engine(model, max_seq=23 + max(K, W) + 1)
     eng.generate([prompt], W + 1)
-    toks, _, dec_s = eng.generate([prompt], K + 1)
+    toks, pre_s, dec_s = eng.generate([prompt], K + 1)
     eng.close()
     tps = K / dec_s
     log(f"[bench] B=1 decode: {K} steps in {dec_s * 1e3:.2f} ms -> {tps:.1f} tok/s "
         f"({tps * wbytes / 1e9:.1f} GB/s of weights)")
 
-    extra = {}
+    extra = {"prefill_b1_ms": round(pre_s * 1e3, 3), "prefill_b1_tok_s": round(len(prompt) / pre_s, 1)}
+    log(f"[bench] B=1 prefill (23 positions, batched, incl. the first pick): {pre_s * 1e3:.3f} ms")
     if args.batch64 > 0:
         B = args.batch64
         prompts = rng.integers(0, TINYLLAMA.V, size=(B, 23)).astype(np.int32)
         eng = Engine(model, max_seq=23 + max(K, W) + 1, batch=B)
         eng.generate(prompts, W + 1)
-        _, _, dec64 = eng.generate(prompts, K + 1)
+        _, pre64, dec64 = eng.generate(prompts, K + 1)
         eng.close()
+        extra["prefill_b64_ms"] = round(pre64 * 1e3, 3)
+        extra["prefill_b64_tok_s"] = round(B * prompts.shape[1] / pre64, 1)
         extra["b64_tok_s"] = round(B * K / dec64, 1)
         extra["b64_ms_per_step"] = round(dec64 / K * 1e3, 3)
         log(f"[bench] B={B} decode: {B * K / dec64:.1f} tok/s aggregate")

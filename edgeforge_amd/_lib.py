@@ -111,6 +111,7 @@ SIGNATURES = {
                                        C.c_int, C.POINTER(_P)]),
     "ef_hip_engine_destroy": (C.c_int, [_P]),
     "ef_hip_engine_forward": (C.c_int, [_P, _i32p, _sz, C.c_int]),
+    "ef_hip_engine_prefill": (C.c_int, [_P, _i32p, _sz, _sz, C.c_int]),
     "ef_hip_engine_logits": (C.c_int, [_P, C.POINTER(_P)]),
     "ef_hip_engine_hidden": (C.c_int, [_P, C.POINTER(_P)]),
     "ef_hip_engine_generate": (C.c_int, [_P, _i32p, _sz, _sz, C.POINTER(ef_hip_sampler_config), _P, _i32p,

@@ -12,9 +12,12 @@
 // One step per layer: [rmsnorm + q/k/v GEMV] -> [RoPE + attention, cache write] -> [o GEMV +
 // residual] -> [rmsnorm + gate/up GEMV + SwiGLU] -> [down GEMV + residual]; then [final rmsnorm +
 // lm_head GEMV] and the token pick (argmax or the sampler) when logits are needed.
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <vector>
 
@@ -26,7 +29,9 @@
 
 namespace {
 constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
-enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8 };
+enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16 };
+// Rows (sequences x positions) of one batched prefill launch; longer prompts go in chunks.
+constexpr size_t kPrefillRows = 4096;
 }  // namespace
 
 struct ef_hip_engine_s {
@@ -52,6 +57,12 @@ struct ef_hip_engine_s {
   ef_hip_sampler_config scfg{};
   void* rng = nullptr;
   std::atomic<int>* owner_refs = nullptr;  // live-engine count of the device model it was made from
+  // batched prefill: activations of `pf_rows` rows (sequence-major: row b * n + i) and the GEMV
+  // workspace for that many rows, allocated on first use
+  size_t pf_rows = 0;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_ctx = nullptr, *pf_act = nullptr;
+  void* pf_ws = nullptr;
+  size_t pf_ws_bytes = 0;
 };
 
 namespace efh {
@@ -90,10 +101,12 @@ int check_matrix(ef_hip_weight w, size_t rows, size_t cols, const char* what) {
 }
 
 
+int enqueue_tail(ef_hip_engine e, int mode);
+
 int enqueue_step(ef_hip_engine e, int mode) {
   const ef_hip_model_config& c = e->c;
   const int B = e->B;
-  const size_t D = c.D, F = c.F, V = c.V, kvd = e->kvd, S = e->max_seq;
+  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
   hipStream_t s = e->stream;
   EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s));
   AttnArgs a{};
@@ -126,6 +139,16 @@ int enqueue_step(ef_hip_engine e, int mode) {
     const GemvJob dn{w.w_down, nullptr, e->act, e->x, F, D};
     EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s, e->gemv_ws, e->gemv_ws_bytes));
   }
+  return enqueue_tail(e, mode);
+}
+
+// After the layers: final RMSNorm + lm_head, then the token pick and the step bookkeeping, or
+// only the position advance (a prompt position whose logits are not needed).
+int enqueue_tail(ef_hip_engine e, int mode) {
+  const ef_hip_model_config& c = e->c;
+  const int B = e->B;
+  const size_t D = c.D, V = c.V, S = e->max_seq;
+  hipStream_t s = e->stream;
   if (mode & kLogits) {
     const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, D, V};
     EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s, e->gemv_ws, e->gemv_ws_bytes));
@@ -147,6 +170,119 @@ int enqueue_step(ef_hip_engine e, int mode) {
   return EF_HIP_OK;
 }
 
+// Batched prefill of positions *pos .. *pos + n - 1 of every sequence (tokens already in the
+// history): every product runs once over all B * n rows (the matrix-core GEMV), RoPE + cache
+// writes for all rows, then causal attention per (head, row) over the cache; the last row of each
+// sequence becomes the decode state x, the position moves to the last prompt position and the
+// tail runs as for a decode step there.  Results equal the one-position-at-a-time path to the
+// GEMV's rounding.
+int enqueue_prefill(ef_hip_engine e, int n, int mode) {
+  const ef_hip_model_config& c = e->c;
+  const int B = e->B, R = B * n;
+  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
+  hipStream_t s = e->stream;
+  EFH_RC(launch_embed_rows(e->embed, e->hist, static_cast<long>(S), e->pos, n, R, e->pf_x, static_cast<long>(D), s));
+  PrefillArgs pa{};
+  pa.n = n;
+  AttnArgs& a = pa.a;
+  a.q = e->pf_q;
+  a.knew = e->pf_k;
+  a.vnew = e->pf_v;
+  a.cos_t = e->cos_t;
+  a.sin_t = e->sin_t;
+  a.pos_dev = e->pos;
+  a.ctx = e->pf_ctx;
+  a.ldq = static_cast<long>(D);
+  a.H = static_cast<int>(c.H);
+  a.KV = static_cast<int>(c.KV);
+  a.hd = static_cast<int>(c.hd);
+  a.max_seq = static_cast<int>(S);
+  a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.hd)));  // src/kernels.cpp:158
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = e->layers[l];
+    const GemvJob qkv[3] = {{w.wq, nullptr, e->pf_x, e->pf_q, D, D},
+                            {w.wk, nullptr, e->pf_x, e->pf_k, D, kvd},
+                            {w.wv, nullptr, e->pf_x, e->pf_v, D, kvd}};
+    EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, R, D, D, s, e->pf_ws, e->pf_ws_bytes));
+    a.kcache = e->kc + l * B * S * kvd;
+    a.vcache = e->vc + l * B * S * kvd;
+    EFH_RC(launch_prefill_attention(pa, R, s));
+    const GemvJob o{w.wo, nullptr, e->pf_ctx, e->pf_x, D, D};
+    EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, R, D, D, s, e->pf_ws, e->pf_ws_bytes));
+    const GemvJob gu{w.w_gate, w.w_up, e->pf_x, e->pf_act, D, F};
+    EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, R, D, F, s, e->pf_ws, e->pf_ws_bytes));
+    const GemvJob dn{w.w_down, nullptr, e->pf_act, e->pf_x, F, D};
+    EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, R, F, D, s, e->pf_ws, e->pf_ws_bytes));
+  }
+  if (n > 1) EFH_RC(launch_advance_by(e->pos, n - 1, s));
+  EFH_HIP(hipMemcpy2DAsync(e->x, D * sizeof(float), e->pf_x + (n - 1) * D, n * D * sizeof(float), D * sizeof(float),
+                           B, hipMemcpyDeviceToDevice, s));
+  return enqueue_tail(e, mode);
+}
+
+// Buffers and GEMV workspace for prefill launches of up to `rows` rows.
+int ensure_prefill(ef_hip_engine e, size_t rows) {
+  if (rows <= e->pf_rows) return EF_HIP_OK;
+  const ef_hip_model_config& c = e->c;
+  const size_t kvd = e->kvd;
+  float* bufs[6] = {};
+  const size_t sizes[6] = {rows * c.D, rows * c.D, rows * kvd, rows * kvd, rows * c.D, rows * c.F};
+  for (int i = 0; i < 6; ++i) {
+    if (hipMalloc(&bufs[i], sizes[i] * sizeof(float)) != hipSuccess) {
+      for (int k = 0; k < i; ++k) (void)hipFree(bufs[k]);
+      return fail(EF_HIP_ENOMEM, "engine prefill buffers");
+    }
+  }
+  size_t need = 0;
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = e->layers[l];
+    const GemvJob qkv[3] = {{w.wq, nullptr, bufs[0], bufs[1], c.D, c.D},
+                            {w.wk, nullptr, bufs[0], bufs[2], c.D, kvd},
+                            {w.wv, nullptr, bufs[0], bufs[3], c.D, kvd}};
+    const GemvJob o{w.wo, nullptr, bufs[4], bufs[0], c.D, c.D};
+    const GemvJob gu{w.w_gate, w.w_up, bufs[0], bufs[5], c.D, c.F};
+    const GemvJob dn{w.w_down, nullptr, bufs[5], bufs[0], c.F, c.D};
+    // every row count a launch may use (a last chunk is shorter): the plan depends on
+    // min(rows, 64) only, so 2 .. 64 and the full count cover all of them
+    const int top = static_cast<int>(std::min<size_t>(rows, 64));
+    for (int R = 2; R <= top + 1; ++R) {
+      const int r = R <= top ? R : static_cast<int>(rows);
+      need = std::max({need, gemv_mfma_workspace_bytes(qkv, 3, kEpiStore, r, c.D),
+                       gemv_mfma_workspace_bytes(&o, 1, kEpiResidual, r, c.D),
+                       gemv_mfma_workspace_bytes(&gu, 1, kEpiSwiglu, r, c.D),
+                       gemv_mfma_workspace_bytes(&dn, 1, kEpiResidual, r, c.F)});
+    }
+  }
+  void* ws = nullptr;
+  if (need > 0 && hipMalloc(&ws, need) != hipSuccess) {
+    for (float* b : bufs) (void)hipFree(b);
+    return fail(EF_HIP_ENOMEM, "engine prefill GEMV workspace");
+  }
+  // replace the old buffers (their graphs hold the old addresses)
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  for (auto it = e->graphs.begin(); it != e->graphs.end();) {
+    if (it->first & kPrefill) {
+      (void)hipGraphExecDestroy(it->second);
+      it = e->graphs.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  for (float* old : {e->pf_x, e->pf_q, e->pf_k, e->pf_v, e->pf_ctx, e->pf_act})
+    if (old) (void)hipFree(old);
+  if (e->pf_ws) (void)hipFree(e->pf_ws);
+  e->pf_x = bufs[0];
+  e->pf_q = bufs[1];
+  e->pf_k = bufs[2];
+  e->pf_v = bufs[3];
+  e->pf_ctx = bufs[4];
+  e->pf_act = bufs[5];
+  e->pf_ws = ws;
+  e->pf_ws_bytes = need;
+  e->pf_rows = rows;
+  return EF_HIP_OK;
+}
+
 int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
   auto it = e->graphs.find(mode);
   if (it != e->graphs.end()) {
@@ -154,7 +290,7 @@ int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
     return EF_HIP_OK;
   }
   EFH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-  const int rc = enqueue_step(e, mode);
+  const int rc = (mode & kPrefill) ? enqueue_prefill(e, mode >> 8, mode & 0xEF) : enqueue_step(e, mode);
   hipGraph_t g = nullptr;
   const hipError_t ec = hipStreamEndCapture(e->stream, &g);
   if (rc != EF_HIP_OK) {
@@ -185,6 +321,30 @@ int run_step(ef_hip_engine e, int mode) {
   EFH_RC(graph_for(e, mode, &g));
   EFH_HIP(hipGraphLaunch(g, e->stream));
   return EF_HIP_OK;
+}
+
+// Positions [*pos, *pos + n) of every sequence in chunks of at most kPrefillRows rows; `last_mode`
+// is the tail of the final chunk (earlier chunks only advance the position).  With instantiate
+// set, only builds the graphs (so a timed region launches nothing new).
+int run_prefill(ef_hip_engine e, size_t n, int last_mode, bool instantiate) {
+  size_t rows = kPrefillRows;
+  if (const char* v = std::getenv("EF_HIP_PREFILL_ROWS")) rows = std::max<long>(1, std::atol(v));  // test knob
+  const size_t chunk = std::max<size_t>(1, rows / static_cast<size_t>(e->B));
+  EFH_RC(ensure_prefill(e, static_cast<size_t>(e->B) * std::min(chunk, n)));
+  for (size_t done = 0; done < n;) {
+    const size_t k = std::min(chunk, n - done);
+    const int mode = kPrefill | (done + k == n ? last_mode : kAdvance) | static_cast<int>(k << 8);
+    hipGraphExec_t g;
+    EFH_RC(graph_for(e, mode, &g));
+    if (!instantiate) EFH_HIP(hipGraphLaunch(g, e->stream));
+    done += k;
+  }
+  return EF_HIP_OK;
+}
+
+bool batched_prefill_enabled() {
+  const char* v = std::getenv("EF_HIP_PREFILL");
+  return v == nullptr || std::strcmp(v, "serial") != 0;
 }
 
 }  // namespace
@@ -327,6 +487,9 @@ int ef_hip_engine_destroy(ef_hip_engine e) {
   (void)hipStreamSynchronize(e->stream);
   for (auto& kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
   for (void* p : e->allocs) (void)hipFree(p);
+  for (float* p : {e->pf_x, e->pf_q, e->pf_k, e->pf_v, e->pf_ctx, e->pf_act})
+    if (p) (void)hipFree(p);
+  if (e->pf_ws) (void)hipFree(e->pf_ws);
   if (e->stage) (void)hipHostFree(e->stage);
   (void)hipStreamDestroy(e->stream);
   if (e->owner_refs != nullptr) e->owner_refs->fetch_sub(1);
@@ -356,6 +519,34 @@ int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens, size_t pos, in
   EFH_RC(run_step(e, compute_logits ? kLogits : 0));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->cached = pos + 1;
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_prefill(ef_hip_engine e, const int32_t* tokens, size_t n, size_t pos, int compute_logits) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(tokens != nullptr && n >= 1, "engine_prefill: null tokens or n = 0");
+  for (size_t i = 0; i < n * static_cast<size_t>(e->B); ++i) {
+    if (tokens[i] < 0 || static_cast<size_t>(tokens[i]) >= e->c.V)
+      return fail(EF_HIP_EINVAL, "prefill: token id " + std::to_string(tokens[i]) + " is outside [0, " +
+                                     std::to_string(e->c.V) + ")");
+  }
+  if (pos + n > e->max_seq)
+    return fail(EF_HIP_EINVAL, "prefill: positions up to " + std::to_string(pos + n - 1) +
+                                   " exceed the KV-cache capacity " + std::to_string(e->max_seq));
+  if (pos > e->cached)
+    return fail(EF_HIP_EINVAL, "prefill: position " + std::to_string(pos) + " skips ahead of the " +
+                                   std::to_string(e->cached) + " cached tokens");
+  const size_t S = e->max_seq;
+  const int B = e->B;
+  EFH_HIP(hipStreamSynchronize(e->stream));  // the pinned staging buffer is reused below
+  for (size_t i = 0; i < n * static_cast<size_t>(B); ++i) e->stage[i] = tokens[i];
+  EFH_HIP(hipMemcpy2DAsync(e->hist + pos, S * 4, e->stage, n * 4, n * 4, B, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->stage[0] = static_cast<int32_t>(pos);
+  EFH_HIP(hipMemcpyAsync(e->pos, e->stage, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_RC(run_prefill(e, n, compute_logits ? kLogits : 0, false));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->cached = pos + n;
   return EF_HIP_OK;
 }
 
@@ -414,15 +605,26 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   EFH_HIP(hipMemcpyAsync(e->hist_len, e->stage, B * 4, hipMemcpyHostToDevice, e->stream));
   EFH_HIP(hipMemcpyAsync(e->pos, e->stage + B, 4, hipMemcpyHostToDevice, e->stream));
   EFH_HIP(hipMemcpyAsync(e->n_prompt, e->stage + B + 1, 4, hipMemcpyHostToDevice, e->stream));
-  // instantiate the graphs before the clock starts
-  hipGraphExec_t g_pre, g_dec;
-  EFH_RC(graph_for(e, kAdvance, &g_pre));
+  // The prompt: one batched prefill (every prompt position of every sequence through each
+  // product at once) or, with EF_HIP_PREFILL=serial, the reference's one position at a time
+  // (src/model.cpp:290).  Graphs are instantiated before the clock starts.
+  const bool batched = n_prompt >= 2 && batched_prefill_enabled();
+  hipGraphExec_t g_pre = nullptr, g_dec;
+  if (batched) {
+    EFH_RC(run_prefill(e, n_prompt, kLogits | pick, true));
+  } else {
+    EFH_RC(graph_for(e, kAdvance, &g_pre));
+  }
   EFH_RC(graph_for(e, kLogits | pick, &g_dec));
   EFH_HIP(hipStreamSynchronize(e->stream));
   using Clock = std::chrono::steady_clock;
   const auto t0 = Clock::now();
-  for (size_t p = 0; p + 1 < n_prompt; ++p) EFH_HIP(hipGraphLaunch(g_pre, e->stream));
-  EFH_HIP(hipGraphLaunch(g_dec, e->stream));  // last prompt position: logits and the first pick
+  if (batched) {
+    EFH_RC(run_prefill(e, n_prompt, kLogits | pick, false));  // ends with logits and the first pick
+  } else {
+    for (size_t p = 0; p + 1 < n_prompt; ++p) EFH_HIP(hipGraphLaunch(g_pre, e->stream));
+    EFH_HIP(hipGraphLaunch(g_dec, e->stream));  // last prompt position: logits and the first pick
+  }
   EFH_HIP(hipStreamSynchronize(e->stream));
   const auto t1 = Clock::now();
   for (size_t k = 1; k < n; ++k) EFH_HIP(hipGraphLaunch(g_dec, e->stream));

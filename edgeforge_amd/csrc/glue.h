@@ -20,6 +20,17 @@ struct AttnArgs {
   float scale;          // float(1 / sqrt(hd))
 };
 
+// Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of
+// sequence b; q / knew / vnew / ctx are [rows][...] with the strides of AttnArgs.
+struct PrefillArgs {
+  AttnArgs a;
+  int n;
+};
+int launch_prefill_attention(const PrefillArgs& a, int rows, hipStream_t s);  // RoPE + cache write, then attention
+int launch_embed_rows(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int n,
+                      int rows, float* out, long ldo, hipStream_t s);
+int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s);
+
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
                     float* out, long ldo, hipStream_t s);
 size_t attention_lds_bytes(int hd, int max_seq);

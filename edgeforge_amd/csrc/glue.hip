@@ -69,6 +69,76 @@ __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long 
   }
 }
 
+// Causal attention of one (query head, row) over positions 0 .. n_pos-1 of one KV head: scores in
+// kern::dot_f32's order, softmax_inplace, then p.v in position order (src/kernels.cpp:153-174).
+// qs (roped query) is in LDS; K and V rows come from the cache except position `cur`, which is
+// taken from kn / vn (the decode step's new row; cur = -1 when every row is in the cache).
+__device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, double* red, const float* kc,
+                                       const float* vc, long kvd, const float* kn, const float* vn, int cur,
+                                       int n_pos, int hd, float scale, float* out) {
+  const int t = threadIdx.x;
+  // scores
+  const int quad = t >> 2, sub = t & 3;
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    stage_rows(rows, kc, kvd, kn, cur, c0, n, hd);
+    __syncthreads();
+    if (quad < n) {
+      const float* kt = rows + quad * hd;
+      float a0 = 0.0f, a1 = 0.0f;
+      int i = 0;
+      for (; i + 8 <= hd; i += 8) {
+        a0 += qs[i + 2 * sub] * kt[i + 2 * sub];
+        a1 += qs[i + 2 * sub + 1] * kt[i + 2 * sub + 1];
+      }
+      if (sub == 0)
+        for (; i < hd; ++i) a0 += qs[i] * kt[i];  // dot_f32's tail joins partial 0
+      float s = a0 + a1;                           // (acc[2s] + acc[2s+1])
+      s = s + __shfl_xor(s, 1, kWave);             // (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
+      s = s + __shfl_xor(s, 2, kWave);             // the two halves, low half first on lane 0
+      if (sub == 0) sc[c0 + quad] = s * scale;
+    }
+    __syncthreads();
+  }
+  // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
+  float mx = -INFINITY;
+  for (int tp = t; tp < n_pos; tp += blockDim.x) mx = fmaxf(mx, sc[tp]);
+  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = mx;
+  __syncthreads();
+  mx = static_cast<float>(red[0]);
+  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) mx = fmaxf(mx, static_cast<float>(red[w]));
+  __syncthreads();
+  double s = 0.0;
+  for (int tp = t; tp < n_pos; tp += blockDim.x) {
+    const float e = expf(sc[tp] - mx);
+    sc[tp] = e;
+    s += static_cast<double>(e);
+  }
+  s = wave_sum_d(s);
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
+  __syncthreads();
+  double tot = 0.0;
+  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) tot += red[w];
+  const float inv = static_cast<float>(1.0 / tot);
+  // out[d] = sum_t p_t v_t[d], positions in order
+  float o = 0.0f;
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    stage_rows(rows, vc, kvd, vn, cur, c0, n, hd);
+    __syncthreads();
+    if (t < hd) {
+      for (int r = 0; r < n; ++r) {
+        const float p = sc[c0 + r] * inv;
+        o += p * rows[r * hd + t];
+      }
+    }
+    __syncthreads();
+  }
+  if (t < hd) out[t] = o;
+}
+
+
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   const int h = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
@@ -105,66 +175,72 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
       vw[i] = vn[i];
     }
   }
-  // scores
-  const int quad = t >> 2, sub = t & 3;
-  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
-    const int n = min(kAttnChunk, n_pos - c0);
-    stage_rows(rows, kc, kvd, kn, pos, c0, n, hd);
-    __syncthreads();
-    if (quad < n) {
-      const float* kt = rows + quad * hd;
-      float a0 = 0.0f, a1 = 0.0f;
-      int i = 0;
-      for (; i + 8 <= hd; i += 8) {
-        a0 += qs[i + 2 * sub] * kt[i + 2 * sub];
-        a1 += qs[i + 2 * sub + 1] * kt[i + 2 * sub + 1];
-      }
-      if (sub == 0)
-        for (; i < hd; ++i) a0 += qs[i] * kt[i];  // dot_f32's tail joins partial 0
-      float s = a0 + a1;                           // (acc[2s] + acc[2s+1])
-      s = s + __shfl_xor(s, 1, kWave);             // (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
-      s = s + __shfl_xor(s, 2, kWave);             // the two halves, low half first on lane 0
-      if (sub == 0) sc[c0 + quad] = s * a.scale;
-    }
-    __syncthreads();
-  }
-  // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
-  float mx = -INFINITY;
-  for (int tp = t; tp < n_pos; tp += blockDim.x) mx = fmaxf(mx, sc[tp]);
-  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  if ((t & (kWave - 1)) == 0) red[t / kWave] = mx;
-  __syncthreads();
-  mx = static_cast<float>(red[0]);
-  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) mx = fmaxf(mx, static_cast<float>(red[w]));
-  __syncthreads();
-  double s = 0.0;
-  for (int tp = t; tp < n_pos; tp += blockDim.x) {
-    const float e = expf(sc[tp] - mx);
-    sc[tp] = e;
-    s += static_cast<double>(e);
-  }
-  s = wave_sum_d(s);
-  if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
-  __syncthreads();
-  double tot = 0.0;
-  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) tot += red[w];
-  const float inv = static_cast<float>(1.0 / tot);
-  // out[d] = sum_t p_t v_t[d], positions in order
-  float o = 0.0f;
-  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
-    const int n = min(kAttnChunk, n_pos - c0);
-    stage_rows(rows, vc, kvd, vn, pos, c0, n, hd);
-    __syncthreads();
-    if (t < hd) {
-      for (int r = 0; r < n; ++r) {
-        const float p = sc[c0 + r] * inv;
-        o += p * rows[r * hd + t];
-      }
-    }
-    __syncthreads();
-  }
-  if (t < hd) a.ctx[static_cast<long>(b) * a.ldq + h * hd + t] = o;
+  attend(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
+         a.ctx + static_cast<long>(b) * a.ldq + h * hd);
 }
+
+// Prefill, step 1: every row r = (sequence b, chunk index i) at position p = *pos_dev + i gets RoPE
+// on each query head in place and on each key head, and its roped key and its value row are
+// written into the cache at p (the decode kernel's rotation, operation for operation).
+__global__ __launch_bounds__(kAttnThreads) void rope_store_kernel(PrefillArgs a) {
+  const int r = blockIdx.x, b = r / a.n, p = *a.a.pos_dev + r % a.n;
+  const int hd = a.a.hd, half = hd / 2, kvd = a.a.KV * hd;
+  const float* cr = a.a.cos_t + static_cast<long>(p) * half;
+  const float* sr = a.a.sin_t + static_cast<long>(p) * half;
+  float* q = const_cast<float*>(a.a.q) + static_cast<long>(r) * a.a.ldq;
+  for (int idx = threadIdx.x; idx < a.a.H * half; idx += blockDim.x) {
+    const int j = idx % half;
+    float* qh = q + (idx / half) * hd;
+    const float qa = qh[j], qb = qh[j + half];
+    qh[j] = qa * cr[j] - qb * sr[j];
+    qh[j + half] = qb * cr[j] + qa * sr[j];
+  }
+  const float* k = a.a.knew + static_cast<long>(r) * kvd;
+  const float* v = a.a.vnew + static_cast<long>(r) * kvd;
+  float* kw = a.a.kcache + (static_cast<long>(b) * a.a.max_seq + p) * kvd;
+  float* vw = a.a.vcache + (static_cast<long>(b) * a.a.max_seq + p) * kvd;
+  for (int idx = threadIdx.x; idx < a.a.KV * half; idx += blockDim.x) {
+    const int j = idx % half, o = (idx / half) * hd;
+    const float ka = k[o + j], kb = k[o + j + half];
+    kw[o + j] = ka * cr[j] - kb * sr[j];
+    kw[o + j + half] = kb * cr[j] + ka * sr[j];
+  }
+  for (int idx = threadIdx.x; idx < kvd; idx += blockDim.x) vw[idx] = v[idx];
+}
+
+// Prefill, step 2: one (query head, row) per workgroup over positions 0 .. p, all from the cache.
+__global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(PrefillArgs a) {
+  extern __shared__ float sm[];
+  const int h = blockIdx.x, r = blockIdx.y, b = r / a.n, p = *a.a.pos_dev + r % a.n;
+  const int hd = a.a.hd, g = h / (a.a.H / a.a.KV), kvd = a.a.KV * hd;
+  float* qs = sm;
+  float* rows = sm + 3 * hd;
+  float* sc = rows + kAttnChunk * hd;
+  double* red = reinterpret_cast<double*>(sc + ((a.a.max_seq + 1) & ~1));
+  const float* q = a.a.q + static_cast<long>(r) * a.a.ldq + h * hd;
+  for (int i = threadIdx.x; i < hd; i += blockDim.x) qs[i] = q[i];
+  __syncthreads();
+  const float* kc = a.a.kcache + (static_cast<long>(b) * a.a.max_seq) * kvd + g * hd;
+  const float* vc = a.a.vcache + (static_cast<long>(b) * a.a.max_seq) * kvd + g * hd;
+  attend(qs, rows, sc, red, kc, vc, kvd, nullptr, nullptr, -1, p + 1, hd, a.a.scale,
+         a.a.ctx + static_cast<long>(r) * a.a.ldq + h * hd);
+}
+
+// x[r] = row hist[b][*pos_dev + i] of the embedding table for every prefill row r = (b, i).
+__global__ void embed_rows_kernel(const uint8_t* __restrict__ W, int qtype, long rows, long cols, long rb,
+                                  const int32_t* __restrict__ hist, long hist_ld, const int32_t* __restrict__ pos_dev,
+                                  int n, float* __restrict__ out, long ldo) {
+  const int r = blockIdx.y, b = r / n, p = *pos_dev + r % n;
+  const int32_t id = hist[b * hist_ld + p];
+  const bool ok = id >= 0 && id < rows;
+  const uint8_t* row = W + (ok ? id : 0) * rb;
+  for (long c = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols;
+       c += static_cast<long>(gridDim.x) * blockDim.x) {
+    out[r * ldo + c] = ok ? decode_elem(row, qtype, c) : __int_as_float(0x7FC00000);
+  }
+}
+
+__global__ void advance_by_kernel(int32_t* pos_dev, int n) { *pos_dev += n; }
 
 // out[b] = w * (x[b] * rsqrt(mean(x[b]^2) + eps)) (kern::rmsnorm).
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
@@ -213,6 +289,30 @@ int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld,
 
 size_t attention_lds_bytes(int hd, int max_seq) {
   return ((3 + static_cast<size_t>(kAttnChunk)) * hd + ((max_seq + 1) & ~1)) * sizeof(float) + 4 * sizeof(double);
+}
+
+int launch_prefill_attention(const PrefillArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(rope_store_kernel, dim3(rows), dim3(kAttnThreads), 0, s, a);
+  EFH_HIP(hipGetLastError());
+  const size_t lds = attention_lds_bytes(a.a.hd, a.a.max_seq);
+  hipLaunchKernelGGL(prefill_attention_kernel, dim3(a.a.H, rows), dim3(kAttnThreads), lds, s, a);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_embed_rows(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int n,
+                      int rows, float* out, long ldo, hipStream_t s) {
+  const unsigned gx = static_cast<unsigned>(std::min<size_t>((W->cols + 255) / 256, 16));
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(gx, rows), dim3(256), 0, s, W->dev, W->qtype, static_cast<long>(W->rows),
+                     static_cast<long>(W->cols), static_cast<long>(W->row_bytes), hist, hist_ld, pos_dev, n, out, ldo);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s) {
+  hipLaunchKernelGGL(advance_by_kernel, dim3(1), dim3(1), 0, s, pos_dev, n);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
 }
 
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {

@@ -144,6 +144,11 @@ class Engine:
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(self.batch))
         EL.call("ef_hip_engine_forward", self.h, t.ctypes.data_as(EL._i32p), pos, int(compute_logits))
 
+    def prefill(self, tokens, pos: int, compute_logits: bool = True) -> None:
+        """tokens [batch][n] at positions pos .. pos+n-1, all rows at once (ef_hip_engine_prefill)."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(self.batch, -1))
+        EL.call("ef_hip_engine_prefill", self.h, t.ctypes.data_as(EL._i32p), t.shape[1], pos, int(compute_logits))
+
     def _fetch(self, fn: str, n: int) -> np.ndarray:
         p = C.c_void_p()
         EL.call(fn, self.h, C.byref(p))

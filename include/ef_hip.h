@@ -196,12 +196,19 @@ int ef_hip_engine_destroy(ef_hip_engine e);
 /* One forward at position pos for all sequences: tokens[batch] (host).  Logits [batch][V] stay on
  * the device (ef_hip_engine_logits); compute_logits = 0 skips the lm_head, as prefill does. */
 int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens_host, size_t pos, int compute_logits);
+/* Positions pos .. pos+n-1 of every sequence at once: tokens[batch][n] (host).  Equivalent to n
+ * forward calls (src/model.cpp:290 feeds the prompt one position at a time), with every product
+ * run once over all batch * n rows on the matrix cores and causal attention over the cache; logits
+ * (compute_logits) and the hidden state are those of position pos+n-1. */
+int ef_hip_engine_prefill(ef_hip_engine e, const int32_t* tokens_host, size_t n, size_t pos, int compute_logits);
 int ef_hip_engine_logits(ef_hip_engine e, const float** logits_dev);
 int ef_hip_engine_hidden(ef_hip_engine e, const float** hidden_dev); /* final-norm output [batch][D] */
 /* The reference decode protocol (src/bench_decode.cpp:30-49, generate_greedy src/model.cpp:278-304)
  * run on the device: prompt [batch][n_prompt] one position at a time (logits only at the last),
  * then n tokens per sequence picked by argmax (cfg NULL or temperature <= 0) or by the sampler
- * (rng_dev as in ef_hip_sample; the history is the prompt plus the tokens picked so far).
+ * (rng_dev as in ef_hip_sample; the history is the prompt plus the tokens picked so far).  The
+ * prompt goes through ef_hip_engine_prefill's batched path (environment EF_HIP_PREFILL=serial
+ * selects the reference's one-position-at-a-time order instead).
  * tokens_out [batch][n] host.  Each step is one HIP graph launch; timings in seconds. */
 int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n_prompt, size_t n,
                            const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
