@@ -65,6 +65,18 @@ class ef_hip_membench_result(C.Structure):
                 ("checksum", C.c_uint64), ("expected_checksum", C.c_uint64), ("checksum_ok", C.c_int)]
 
 
+class ef_hip_reply_options(C.Structure):
+    _fields_ = [("max_new", _sz), ("eos_id", C.c_int32), ("eos_min_p", C.c_float), ("steps_per_check", C.c_int)]
+
+
+class ef_hip_reply_stats(C.Structure):
+    _fields_ = [("prompt_tokens", _sz), ("reused_tokens", _sz), ("prefill_tokens", _sz), ("generated", _sz),
+                ("steps", _sz), ("reason", C.c_int), ("prefill_s", C.c_double), ("decode_s", C.c_double),
+                ("eos_p_max", C.c_double), ("eos_p_max_step", _sz)]
+
+
+STOP_NONE, STOP_EOS, STOP_EOS_MIN_P, STOP_MAX_NEW, STOP_CONTEXT = 0, 1, 2, 5, 6
+
 # name -> (restype, argtypes); every entry point declared in include/ef_hip.h
 SIGNATURES = {
     "ef_hip_init": (C.c_int, [C.c_int]),
@@ -118,6 +130,10 @@ SIGNATURES = {
                                          C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ef_hip_membench": (C.c_int, [C.POINTER(ef_hip_membench_options), C.POINTER(ef_hip_membench_result)]),
     "ef_hip_membench_expected_pass_sum": (C.c_uint64, [C.c_uint64]),
+    "ef_hip_engine_reply": (C.c_int, [_P, _i32p, _sz, C.POINTER(ef_hip_sampler_config), _P,
+                                      C.POINTER(ef_hip_reply_options), _i32p, C.POINTER(C.c_double),
+                                      C.POINTER(ef_hip_reply_stats)]),
+    "ef_hip_engine_reset": (C.c_int, [_P]),
     "ef_hip_efq_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "ef_hip_efq_parse": (C.c_int, [_P, _sz, C.POINTER(_P)]),
     "ef_hip_efq_close": (C.c_int, [_P]),

@@ -29,7 +29,7 @@
 
 namespace {
 constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
-enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16 };
+enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32 };
 // Rows (sequences x positions) of one batched prefill launch; longer prompts go in chunks.
 constexpr size_t kPrefillRows = 4096;
 }  // namespace
@@ -63,6 +63,13 @@ struct ef_hip_engine_s {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_ctx = nullptr, *pf_act = nullptr;
   void* pf_ws = nullptr;
   size_t pf_ws_bytes = 0;
+  // chat turns (ef_hip_engine_reply): the token ids whose K / V the cache holds, P(EOS) per
+  // sequence and per generated token, and a copy of the RNG states taken before each window of steps
+  std::vector<int32_t> chat_ids;
+  int eos_id = -1;
+  double* eos_cur = nullptr;  // [B]
+  double* eos_out = nullptr;  // [B][max_seq]
+  void* rng_snap = nullptr;
 };
 
 namespace efh {
@@ -159,10 +166,13 @@ int enqueue_tail(ef_hip_engine e, int mode) {
                  e->n_prompt, e->pos, e->step_counter};
       EFH_RC(launch_argmax_finish(e->logits, static_cast<int>(V), static_cast<long>(V), B, f, s));
     } else {
+      const bool eos = (mode & kEos) != 0;
       EFH_RC(launch_sample(e->logits, static_cast<int>(V), B, static_cast<long>(V), e->scfg, e->hist, e->hist_len,
-                           static_cast<long>(S), e->rng, e->next_tok, e->sample_ws, s));
+                           static_cast<long>(S), e->rng, e->next_tok, e->sample_ws, s, e->eos_id,
+                           eos ? e->eos_cur : nullptr));
       EFH_RC(launch_finish_step(e->next_tok, B, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens,
-                                static_cast<long>(S), e->n_prompt, e->pos, s));
+                                static_cast<long>(S), e->n_prompt, e->pos, s, eos ? e->eos_cur : nullptr,
+                                eos ? e->eos_out : nullptr));
     }
   } else if (mode & kAdvance) {
     EFH_RC(launch_advance(e->pos, s));
@@ -307,12 +317,27 @@ int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
   return EF_HIP_OK;
 }
 
-int drop_graph(ef_hip_engine e, int mode) {
-  auto it = e->graphs.find(mode);
-  if (it != e->graphs.end()) {
-    EFH_HIP(hipGraphExecDestroy(it->second));
-    e->graphs.erase(it);
+// Drops every cached graph whose mode has any of `bits` (their captured arguments are stale).
+int drop_graphs_with(ef_hip_engine e, int bits) {
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  for (auto it = e->graphs.begin(); it != e->graphs.end();) {
+    if (it->first & bits) {
+      EFH_HIP(hipGraphExecDestroy(it->second));
+      it = e->graphs.erase(it);
+    } else {
+      ++it;
+    }
   }
+  return EF_HIP_OK;
+}
+
+// Sampler settings and RNG states are captured into the graphs that sample.
+int set_sampler(ef_hip_engine e, const ef_hip_sampler_config& cfg, void* rng) {
+  const bool same = e->rng == rng && e->scfg.temperature == cfg.temperature && e->scfg.top_k == cfg.top_k &&
+                    e->scfg.top_p == cfg.top_p && e->scfg.repetition_penalty == cfg.repetition_penalty;
+  if (!same) EFH_RC(drop_graphs_with(e, kSample));
+  e->scfg = cfg;
+  e->rng = rng;
   return EF_HIP_OK;
 }
 
@@ -416,7 +441,8 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
       (rc = dev_alloc(e, &e->hist, B * S)) || (rc = dev_alloc(e, &e->hist_len, B)) ||
       (rc = dev_alloc(e, &e->next_tok, B)) || (rc = dev_alloc(e, &e->pos, 1)) ||
       (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S)) ||
-      (rc = dev_alloc(e, &e->step_counter, 1))) {
+      (rc = dev_alloc(e, &e->step_counter, 1)) || (rc = dev_alloc(e, &e->eos_cur, B)) ||
+      (rc = dev_alloc(e, &e->eos_out, B * S))) {
     return cleanup_fail(rc);
   }
   void* ws = nullptr;
@@ -586,11 +612,7 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   int pick = kGreedy;
   if (cfg != nullptr) {
     EFH_CHECK(cfg->temperature <= 0.0f || rng != nullptr, "generate: sampling needs rng states");
-    const bool same = e->rng == rng && e->scfg.temperature == cfg->temperature && e->scfg.top_k == cfg->top_k &&
-                      e->scfg.top_p == cfg->top_p && e->scfg.repetition_penalty == cfg->repetition_penalty;
-    if (!same) EFH_RC(drop_graph(e, kLogits | kSample));
-    e->scfg = *cfg;
-    e->rng = rng;
+    EFH_RC(set_sampler(e, *cfg, rng));
     pick = kSample;
   }
   // history <- prompt, hist_len <- n_prompt, position 0
@@ -633,8 +655,140 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   EFH_HIP(hipMemcpy2DAsync(tokens_out, n * 4, e->out_tokens, S * 4, n * 4, B, hipMemcpyDeviceToHost, e->stream));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->cached = n_prompt + n - 1;
+  e->chat_ids.clear();
   if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
   if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_reset(ef_hip_engine e) {
+  EFH_RC(check_engine(e));
+  e->chat_ids.clear();
+  e->cached = 0;
+  return EF_HIP_OK;
+}
+
+// The token-level loop of ChatSession::reply (src/chat.cpp:174-259): reuse of the cached prefix
+// (longest common prefix with the ids whose K / V the cache holds, at least the last prompt token
+// recomputed), batched prefill of the rest, then sample / P(EOS) / stop checks per step.  Steps
+// run on the device in windows of steps_per_check graph launches; the host then applies the
+// reference's stop checks to the window's tokens in order.  Steps launched past a stop only write
+// cache positions the next turn recomputes, and the RNG states are restored to the window's start
+// and advanced by the draws the reference makes (one per sampled step), so a conversation samples
+// the same ids as the reference's Sampler.
+int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids, size_t n_ids, const ef_hip_sampler_config* cfg,
+                        void* rng, const ef_hip_reply_options* o, int32_t* reply_out, double* eos_p_out,
+                        ef_hip_reply_stats* st) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(ids && cfg && o && reply_out, "engine_reply: null argument");
+  EFH_CHECK(e->B == 1, "engine_reply: a chat session is one sequence (engine batch 1)");
+  EFH_CHECK(n_ids >= 1, "engine_reply: empty prompt");
+  EFH_CHECK(o->max_new > 0, "chat: max_new must be > 0");
+  const size_t S = e->max_seq;
+  if (n_ids >= S)
+    return fail(EF_HIP_EINVAL, "message is too long for the " + std::to_string(S) + "-token context");
+  for (size_t i = 0; i < n_ids; ++i) {
+    if (ids[i] < 0 || static_cast<size_t>(ids[i]) >= e->c.V)
+      return fail(EF_HIP_EINVAL, "reply: token id " + std::to_string(ids[i]) + " out of range");
+  }
+  const bool sampled = cfg->temperature > 0.0f;
+  EFH_CHECK(!sampled || rng != nullptr, "engine_reply: sampling needs rng states");
+  EFH_RC(set_sampler(e, *cfg, rng));
+  if (e->eos_id != o->eos_id) {
+    EFH_RC(drop_graphs_with(e, kEos));
+    e->eos_id = o->eos_id;
+  }
+  if (sampled && e->rng_snap == nullptr) EFH_RC(dev_alloc(e, reinterpret_cast<uint8_t**>(&e->rng_snap), kRngStateBytes));
+  ef_hip_reply_stats r{};
+  r.prompt_tokens = n_ids;
+  size_t lcp = 0;
+  while (lcp < e->chat_ids.size() && lcp < n_ids && e->chat_ids[lcp] == ids[lcp]) ++lcp;
+  if (lcp == n_ids) --lcp;
+  lcp = std::min(lcp, e->cached);
+  r.reused_tokens = lcp;
+  r.prefill_tokens = n_ids - lcp;
+  // history <- ids, hist_len <- n_ids, n_prompt <- n_ids, position <- lcp
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  for (size_t i = 0; i < n_ids; ++i) e->stage[i] = ids[i];
+  EFH_HIP(hipMemcpyAsync(e->hist, e->stage, n_ids * 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->stage[0] = static_cast<int32_t>(n_ids);
+  e->stage[1] = static_cast<int32_t>(lcp);
+  EFH_HIP(hipMemcpyAsync(e->hist_len, e->stage, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(e->n_prompt, e->stage, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(e->pos, e->stage + 1, 4, hipMemcpyHostToDevice, e->stream));
+  const int mode = kLogits | kSample | kEos;
+  const size_t n_pre = n_ids - lcp;
+  const bool batched = n_pre >= 2 && batched_prefill_enabled();
+  hipGraphExec_t g_dec;
+  if (batched) EFH_RC(run_prefill(e, n_pre, mode, true));
+  EFH_RC(graph_for(e, mode, &g_dec));
+  const size_t max_new = std::min(o->max_new, S - n_ids);
+  const size_t window = static_cast<size_t>(std::max(1, o->steps_per_check));
+  std::vector<int32_t> toks(max_new);
+  std::vector<double> peos(max_new);
+  auto snapshot = [&]() -> int {
+    if (sampled) EFH_HIP(hipMemcpyAsync(e->rng_snap, rng, kRngStateBytes, hipMemcpyDeviceToDevice, e->stream));
+    return EF_HIP_OK;
+  };
+  using Clock = std::chrono::steady_clock;
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const auto t0 = Clock::now();
+  EFH_RC(snapshot());
+  if (batched) {
+    EFH_RC(run_prefill(e, n_pre, mode, false));  // ends with the first pick
+  } else {
+    for (size_t p = lcp; p + 1 < n_ids; ++p) EFH_RC(run_step(e, kAdvance));
+    EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+  }
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const auto t1 = Clock::now();
+  size_t picks = 1, w0 = 0, steps = 0, generated = 0, forwarded = 0;
+  int reason = 0;
+  while (reason == 0) {
+    const size_t w1 = std::min(max_new, w0 + window);
+    for (; picks < w1; ++picks) EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+    EFH_HIP(hipMemcpyAsync(toks.data() + w0, e->out_tokens + w0, (w1 - w0) * 4, hipMemcpyDeviceToHost, e->stream));
+    EFH_HIP(hipMemcpyAsync(peos.data() + w0, e->eos_out + w0, (w1 - w0) * 8, hipMemcpyDeviceToHost, e->stream));
+    EFH_HIP(hipStreamSynchronize(e->stream));
+    for (size_t k = w0; k < w1 && reason == 0; ++k) {  // src/chat.cpp:220-246
+      steps = k + 1;
+      if (peos[k] > r.eos_p_max) {
+        r.eos_p_max = peos[k];
+        r.eos_p_max_step = k;
+      }
+      if (toks[k] == o->eos_id) {
+        reason = EF_HIP_STOP_EOS;
+      } else if (o->eos_min_p > 0.0f && peos[k] >= static_cast<double>(o->eos_min_p)) {
+        reason = EF_HIP_STOP_EOS_MIN_P;
+      } else {
+        reply_out[generated++] = toks[k];
+        if (k + 1 == max_new) {
+          reason = max_new < o->max_new ? EF_HIP_STOP_CONTEXT : EF_HIP_STOP_MAX_NEW;
+        } else {
+          ++forwarded;
+        }
+      }
+    }
+    if (reason != 0 && sampled && steps < w1) {  // steps w0 .. steps-1 happened in the reference
+      EFH_HIP(hipMemcpyAsync(rng, e->rng_snap, kRngStateBytes, hipMemcpyDeviceToDevice, e->stream));
+      EFH_RC(launch_rng_discard(rng, 1, static_cast<int>(steps - w0), e->stream));
+    }
+    w0 = w1;
+    if (reason == 0) EFH_RC(snapshot());
+  }
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const auto t2 = Clock::now();
+  if (eos_p_out != nullptr) std::copy(peos.begin(), peos.begin() + steps, eos_p_out);
+  e->chat_ids.assign(ids, ids + n_ids);
+  e->chat_ids.insert(e->chat_ids.end(), reply_out, reply_out + forwarded);
+  e->cached = e->chat_ids.size();
+  r.generated = generated;
+  r.steps = steps;
+  r.reason = reason;
+  r.prefill_s = std::chrono::duration<double>(t1 - t0).count();
+  r.decode_s = std::chrono::duration<double>(t2 - t1).count();
+  if (st != nullptr) *st = r;
   return EF_HIP_OK;
 }
 

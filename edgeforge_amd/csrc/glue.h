@@ -36,8 +36,10 @@ int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld,
 size_t attention_lds_bytes(int hd, int max_seq);
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, int batch, float* out, hipStream_t s);
+// With out_eos: eos_p[b] is stored beside the picked token (the chat loop's per-step P(EOS)).
 int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_ld, int32_t* hist_len, int32_t* out,
-                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s);
+                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s,
+                       const double* eos_p = nullptr, double* out_eos = nullptr);
 int launch_advance(int32_t* pos_dev, hipStream_t s);
 
 }  // namespace efh

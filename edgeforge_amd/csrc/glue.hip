@@ -261,14 +261,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 // the history, lands in the output list at p - (n_prompt - 1), and the position advances.
 __global__ void finish_step_kernel(const int32_t* __restrict__ next, int batch, int32_t* hist, long hist_ld,
                                    int32_t* hist_len, int32_t* out, long out_ld, const int32_t* n_prompt_dev,
-                                   int32_t* pos_dev) {
+                                   int32_t* pos_dev, const double* eos_p, double* out_eos) {
   const int p = *pos_dev;
   const int k = p - (*n_prompt_dev - 1);
   for (int b = threadIdx.x; b < batch; b += blockDim.x) {
     const int32_t tok = next[b];
     if (p + 1 < hist_ld) hist[b * hist_ld + p + 1] = tok;
     hist_len[b] = p + 2 < hist_ld ? p + 2 : static_cast<int32_t>(hist_ld);
-    if (k >= 0 && k < out_ld) out[b * out_ld + k] = tok;
+    if (k >= 0 && k < out_ld) {
+      out[b * out_ld + k] = tok;
+      if (out_eos != nullptr) out_eos[b * out_ld + k] = eos_p[b];
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) *pos_dev = p + 1;
@@ -329,9 +332,10 @@ int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, in
 }
 
 int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_ld, int32_t* hist_len, int32_t* out,
-                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s) {
+                       long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s, const double* eos_p,
+                       double* out_eos) {
   hipLaunchKernelGGL(finish_step_kernel, dim3(1), dim3(256), 0, s, next, batch, hist, hist_ld, hist_len, out, out_ld,
-                     n_prompt_dev, pos_dev);
+                     n_prompt_dev, pos_dev, eos_p, out_eos);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }

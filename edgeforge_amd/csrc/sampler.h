@@ -27,8 +27,11 @@ struct StepArgs {
 // argmax per sequence, then the step bookkeeping (pos advances once for the batch).
 int launch_argmax_finish(const float* x, int n, long ld, int batch, const StepArgs& f, hipStream_t s);
 // ws: batch * sample_workspace_stride(vocab) bytes of device memory.
+// With eos_p: also P(eos_id) under softmax of the raw logits per sequence (prob_of, src/chat.cpp:35-42).
 int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_hip_sampler_config& cfg,
                   const int32_t* hist, const int32_t* hist_len, long hist_ld, void* rng, int32_t* out, void* ws,
-                  hipStream_t s);
+                  hipStream_t s, int eos_id = -1, double* eos_p = nullptr);
+// std::mt19937_64::discard(k) on every sequence's state.
+int launch_rng_discard(void* rng, int batch, int k, hipStream_t s);
 
 }  // namespace efh

@@ -68,6 +68,14 @@ __device__ double mt_uniform(MtState* s) {
   return r >= 1.0 ? 0x1.fffffffffffffp-1 : r;
 }
 
+// Advances every state by k draws (std::mt19937_64::discard).
+__global__ void rng_discard_kernel(uint8_t* states, int batch, int k) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  MtState* st = reinterpret_cast<MtState*>(states + static_cast<size_t>(b) * kRngStateBytes);
+  for (int i = 0; i < k; ++i) (void)mt_next(st);
+}
+
 __global__ void rng_seed_kernel(uint8_t* states, const uint64_t* seeds, int batch) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b < batch) mt_seed(reinterpret_cast<MtState*>(states + static_cast<size_t>(b) * kRngStateBytes), seeds[b]);
@@ -275,7 +283,34 @@ struct SampleArgs {
   uint8_t* ws;  // workspace base
   size_t ws_stride;
   int npow2;
+  int eos_id;     // with eos_p: P(eos_id) under softmax(logits) per sequence
+  double* eos_p;  // [batch] or null
 };
+
+// P(id) under softmax of the raw logits, in double (prob_of, src/chat.cpp:35-42): max, then the sum
+// of exp(l - max) over the vocabulary (per-thread partial sums combined in a fixed order; the
+// reference adds left to right, a difference in the last bits of a double).  Thread 0 returns it.
+__device__ double softmax_prob(const float* lg, int V, int id, double* red) {
+  const int t = threadIdx.x, nw = blockDim.x / kWave;
+  double m = -INFINITY;
+  for (int i = t; i < V; i += blockDim.x) m = fmax(m, static_cast<double>(lg[i]));
+  for (int o = kWave / 2; o > 0; o >>= 1) m = fmax(m, __shfl_xor(m, o, kWave));
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = m;
+  __syncthreads();
+  m = red[0];
+  for (int w = 1; w < nw; ++w) m = fmax(m, red[w]);
+  __syncthreads();
+  double s = 0.0;
+  for (int i = t; i < V; i += blockDim.x) s += exp(static_cast<double>(lg[i]) - m);
+  s = wave_sum_d(s);
+  if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
+  __syncthreads();
+  double tot = 0.0;
+  for (int w = 0; w < nw; ++w) tot += red[w];
+  __syncthreads();
+  if (id < 0 || id >= V) return 0.0;
+  return exp(static_cast<double>(lg[id]) - m) / tot;
+}
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ uint64_t s_keys[kChunk];  // 32 KB: top-k candidates / sort chunk
@@ -295,6 +330,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + ((V * 8 + 255) & ~255));  // [npow2]
   const float* lg = a.logits + b * a.ld;
 
+  if (a.eos_p != nullptr) {
+    __shared__ double s_red[kThreads / kWave];
+    const double pe = softmax_prob(lg, V, a.eos_id, s_red);
+    if (threadIdx.x == 0) a.eos_p[b] = pe;
+  }
   for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = lg[i];
   __syncthreads();
   // repetition penalty: each unique in-range history id once, in history order (src/sampler.cpp:16-24)
@@ -488,10 +528,19 @@ int launch_argmax_finish(const float* x, int n, long ld, int batch, const StepAr
   return EF_HIP_OK;
 }
 
+int launch_rng_discard(void* rng, int batch, int k, hipStream_t s) {
+  if (k <= 0) return EF_HIP_OK;
+  hipLaunchKernelGGL(rng_discard_kernel, dim3((batch + 63) / 64), dim3(64), 0, s, static_cast<uint8_t*>(rng), batch, k);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
 int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_hip_sampler_config& cfg,
                   const int32_t* hist, const int32_t* hist_len, long hist_ld, void* rng, int32_t* out, void* ws,
-                  hipStream_t s) {
+                  hipStream_t s, int eos_id, double* eos_p) {
   SampleArgs a{};
+  a.eos_id = eos_id;
+  a.eos_p = eos_p;
   a.logits = logits;
   a.ld = ld;
   a.vocab = vocab;

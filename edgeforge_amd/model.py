@@ -177,6 +177,26 @@ class Engine:
                out.ctypes.data_as(EL._i32p), C.byref(pre), C.byref(dec))
         return out, pre.value, dec.value
 
+    def reply(self, ids, max_new: int, sampler: dict | None = None, rng: H.RngStates | None = None,
+              eos_id: int = -1, eos_min_p: float = 0.0, steps_per_check: int = 8):
+        """ChatSession::reply at the token level (batch 1): (reply ids, P(EOS) per step, stats)."""
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        sampler = sampler or {}
+        cfg = EL.ef_hip_sampler_config(sampler.get("temperature", 0.0), sampler.get("top_k", 0),
+                                      sampler.get("top_p", 1.0), sampler.get("repetition_penalty", 1.0),
+                                      sampler.get("seed", 0))
+        opts = EL.ef_hip_reply_options(max_new, eos_id, eos_min_p, steps_per_check)
+        out = np.empty(max_new, np.int32)
+        peos = np.empty(max_new, np.float64)
+        st = EL.ef_hip_reply_stats()
+        EL.call("ef_hip_engine_reply", self.h, ids.ctypes.data_as(EL._i32p), ids.size, C.byref(cfg),
+               rng.buf.ptr if rng else None, C.byref(opts), out.ctypes.data_as(EL._i32p),
+               peos.ctypes.data_as(C.POINTER(C.c_double)), C.byref(st))
+        return out[:st.generated].copy(), peos[:st.steps].copy(), st
+
+    def reset(self) -> None:
+        EL.call("ef_hip_engine_reset", self.h)
+
     def close(self) -> None:
         if getattr(self, "h", None):
             EL.call("ef_hip_engine_destroy", self.h)

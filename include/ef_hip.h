@@ -214,6 +214,40 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n
                            const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
                            double* prefill_s, double* decode_s);
 
+/* ---- chat turns ----------------------------------------------------------------------------------
+ * The token-level loop of ef::ChatSession::reply (include/ef/chat.h:99-105, src/chat.cpp:174-259)
+ * on an engine of batch 1: ids is the rendered conversation (the tokenizer and chat template stay
+ * on the caller's side).  The longest common prefix with the ids whose K / V the engine holds is
+ * reused (at least the last id is recomputed), the rest is prefilled in one batched pass, then each
+ * step samples (cfg; greedy when temperature <= 0), records P(eos_id) under softmax of the raw
+ * logits (prob_of, src/chat.cpp:35-42, fused into the sampler kernel), and stops as the reference:
+ * the EOS id, P(EOS) >= eos_min_p (when > 0), or max_new / the context limit.  reply_out gets the
+ * generated ids (at most max_new), eos_p_out (optional) P(EOS) of every step.  Role-marker and
+ * repetition stops work on decoded text and stay with the caller.  Consecutive calls continue the
+ * conversation (the RNG states advance exactly as the reference's Sampler). */
+#define EF_HIP_STOP_NONE 0
+#define EF_HIP_STOP_EOS 1        /* StopReason order, include/ef/chat.h */
+#define EF_HIP_STOP_EOS_MIN_P 2
+#define EF_HIP_STOP_MAX_NEW 5
+#define EF_HIP_STOP_CONTEXT 6
+typedef struct {
+  size_t max_new;       /* ChatOptions::max_new */
+  int32_t eos_id;       /* Tokenizer::eos_id (-1: none) */
+  float eos_min_p;      /* StopConfig::eos_min_p (0: off) */
+  int steps_per_check;  /* decode steps launched between host checks (>= 1) */
+} ef_hip_reply_options;
+typedef struct {        /* TurnStats (include/ef/chat.h) */
+  size_t prompt_tokens, reused_tokens, prefill_tokens, generated, steps;
+  int reason;           /* EF_HIP_STOP_* */
+  double prefill_s, decode_s, eos_p_max;
+  size_t eos_p_max_step;
+} ef_hip_reply_stats;
+int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids_host, size_t n_ids, const ef_hip_sampler_config* cfg,
+                        void* rng_dev, const ef_hip_reply_options* options, int32_t* reply_out, double* eos_p_out,
+                        ef_hip_reply_stats* stats);
+/* ChatSession::reset (src/chat.cpp:143-148): forget the cached ids (the next turn prefills all). */
+int ef_hip_engine_reset(ef_hip_engine e);
+
 /* ---- .efq model files -------------------------------------------------------------------------
  * ef::QuantFile (include/ef/qfile.h:95-124).  ef_hip_efq_open maps a file and validates it as
  * QuantFile::open / parse_efq do (src/qfile.cpp:125-243): magic, version, header length, strict

@@ -131,3 +131,70 @@ class HostModel:
         t = {k: (self.weights[k].qtype, self._bytes[k]) for k in self._bytes}
         t.update(self._norms)
         return t
+
+
+def prob_of(logits: np.ndarray, token: int) -> float:
+    """P(token) under softmax(logits) in double, summed left to right (src/chat.cpp:35-42)."""
+    import math
+    if token < 0 or token >= logits.size:
+        return 0.0
+    l64 = logits.astype(np.float64)
+    m = -math.inf
+    for v in l64:
+        m = max(m, float(v))
+    s = 0.0
+    for v in l64:
+        s += math.exp(float(v) - m)
+    return math.exp(float(l64[token]) - m) / s
+
+
+STOP_EOS, STOP_EOS_MIN_P, STOP_MAX_NEW, STOP_CONTEXT = 1, 2, 5, 6
+
+
+class OracleChat:
+    """ChatSession::reply at the token level (src/chat.cpp:174-259) over the oracle's Transformer and
+    Sampler, TEST INFRASTRUCTURE ONLY: cached-prefix reuse (at least the last id recomputed),
+    prob_of(EOS) every step, and the EOS / EOS-probability / max-new / context stops in the
+    reference's order.  The Sampler (and its RNG) lives across turns, as ChatSession's does."""
+
+    def __init__(self, om: OracleModel, max_seq: int, sampler: dict, threads: int = 2):
+        self.t = om.transformer(max_seq, threads=threads)
+        self.s = O.Sampler(**sampler)
+        self.cached: list[int] = []
+        self.max_seq = max_seq
+
+    def reply(self, ids, max_new: int, eos_id: int = -1, eos_min_p: float = 0.0):
+        ids = [int(v) for v in ids]
+        lcp = 0
+        while lcp < len(self.cached) and lcp < len(ids) and self.cached[lcp] == ids[lcp]:
+            lcp += 1
+        if lcp == len(ids):
+            lcp -= 1
+        logits = None
+        for p in range(lcp, len(ids)):
+            logits = self.t.forward(ids[p], p, p + 1 == len(ids))
+        self.cached = list(ids)
+        limit = min(max_new, self.max_seq - len(ids))
+        history, gen, peos, reason = list(ids), [], [], 0
+        min_p = float(np.float32(eos_min_p))
+        for step in range(limit):
+            tok = self.s.sample(logits, history)
+            pe = prob_of(logits, eos_id)
+            peos.append(pe)
+            if tok == eos_id:
+                reason = STOP_EOS
+                break
+            if min_p > 0.0 and pe >= min_p:
+                reason = STOP_EOS_MIN_P
+                break
+            gen.append(tok)
+            history.append(tok)
+            if step + 1 == limit:
+                reason = STOP_CONTEXT if limit < max_new else STOP_MAX_NEW
+                break
+            logits = self.t.forward(tok, len(self.cached))
+            self.cached.append(tok)
+        return gen, peos, reason, lcp
+
+    def close(self):
+        self.t.close()
