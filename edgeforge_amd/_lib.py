@@ -77,6 +77,11 @@ class ef_hip_reply_stats(C.Structure):
 
 STOP_NONE, STOP_EOS, STOP_EOS_MIN_P, STOP_MAX_NEW, STOP_CONTEXT = 0, 1, 2, 5, 6
 
+
+class ef_hip_dist_stats(C.Structure):
+    _fields_ = [("n", _sz), ("top1", _sz), ("confident", _sz), ("confident_top1", _sz), ("nonfinite", _sz),
+                ("kl_sum", C.c_double), ("kl_max", C.c_double), ("kl_mean", C.c_double)]
+
 # name -> (restype, argtypes); every entry point declared in include/ef_hip.h
 SIGNATURES = {
     "ef_hip_init": (C.c_int, [C.c_int]),
@@ -134,6 +139,10 @@ SIGNATURES = {
                                       C.POINTER(ef_hip_reply_options), _i32p, C.POINTER(C.c_double),
                                       C.POINTER(ef_hip_reply_stats)]),
     "ef_hip_engine_reset": (C.c_int, [_P]),
+    "ef_hip_engine_score": (C.c_int, [_P, _i32p, _sz, _sz, C.POINTER(C.c_double), _P]),
+    "ef_hip_compare_dist": (C.c_int, [_P, _P, _sz, _sz, _sz, _sz, C.POINTER(C.c_double), C.POINTER(ef_hip_dist_stats),
+                                      _P]),
+    "ef_hip_neg_log_prob": (C.c_int, [_P, _sz, _sz, _sz, _P, _P, _P]),
     "ef_hip_efq_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "ef_hip_efq_parse": (C.c_int, [_P, _sz, C.POINTER(_P)]),
     "ef_hip_efq_close": (C.c_int, [_P]),

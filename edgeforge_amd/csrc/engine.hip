@@ -29,7 +29,7 @@
 
 namespace {
 constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
-enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32 };
+enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32, kAllLogits = 64 };
 // Rows (sequences x positions) of one batched prefill launch; longer prompts go in chunks.
 constexpr size_t kPrefillRows = 4096;
 }  // namespace
@@ -63,6 +63,8 @@ struct ef_hip_engine_s {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_ctx = nullptr, *pf_act = nullptr;
   void* pf_ws = nullptr;
   size_t pf_ws_bytes = 0;
+  float* pf_logits = nullptr;  // [pf_rows][V], teacher-forced scoring only (allocated on first use)
+  size_t pf_logit_rows = 0;
   // chat turns (ef_hip_engine_reply): the token ids whose K / V the cache holds, P(EOS) per
   // sequence and per generated token, and a copy of the RNG states taken before each window of steps
   std::vector<int32_t> chat_ids;
@@ -224,6 +226,10 @@ int enqueue_prefill(ef_hip_engine e, int n, int mode) {
     const GemvJob dn{w.w_down, nullptr, e->pf_act, e->pf_x, F, D};
     EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, R, F, D, s, e->pf_ws, e->pf_ws_bytes));
   }
+  if (mode & kAllLogits) {  // teacher-forced scoring: final RMSNorm + lm_head on every row
+    const GemvJob lm{e->lm_head, nullptr, e->pf_x, e->pf_logits, D, c.V};
+    return launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, R, D, c.V, s, e->pf_ws, e->pf_ws_bytes);
+  }
   if (n > 1) EFH_RC(launch_advance_by(e->pos, n - 1, s));
   EFH_HIP(hipMemcpy2DAsync(e->x, D * sizeof(float), e->pf_x + (n - 1) * D, n * D * sizeof(float), D * sizeof(float),
                            B, hipMemcpyDeviceToDevice, s));
@@ -257,10 +263,12 @@ int ensure_prefill(ef_hip_engine e, size_t rows) {
     const int top = static_cast<int>(std::min<size_t>(rows, 64));
     for (int R = 2; R <= top + 1; ++R) {
       const int r = R <= top ? R : static_cast<int>(rows);
+      const GemvJob lm{e->lm_head, nullptr, bufs[0], nullptr, c.D, c.V};
       need = std::max({need, gemv_mfma_workspace_bytes(qkv, 3, kEpiStore, r, c.D),
                        gemv_mfma_workspace_bytes(&o, 1, kEpiResidual, r, c.D),
                        gemv_mfma_workspace_bytes(&gu, 1, kEpiSwiglu, r, c.D),
-                       gemv_mfma_workspace_bytes(&dn, 1, kEpiResidual, r, c.F)});
+                       gemv_mfma_workspace_bytes(&dn, 1, kEpiResidual, r, c.F),
+                       gemv_mfma_workspace_bytes(&lm, 1, kEpiStore, r, c.D)});
     }
   }
   void* ws = nullptr;
@@ -374,6 +382,7 @@ bool batched_prefill_enabled() {
 
 }  // namespace
 void engine_set_owner(ef_hip_engine e, std::atomic<int>* refs) { e->owner_refs = refs; }
+int launch_nll(const float* logits, int V, long ld, const int32_t* targets, int n, double* nll, hipStream_t s);
 
 }  // namespace efh
 
@@ -516,6 +525,7 @@ int ef_hip_engine_destroy(ef_hip_engine e) {
   for (float* p : {e->pf_x, e->pf_q, e->pf_k, e->pf_v, e->pf_ctx, e->pf_act})
     if (p) (void)hipFree(p);
   if (e->pf_ws) (void)hipFree(e->pf_ws);
+  if (e->pf_logits) (void)hipFree(e->pf_logits);
   if (e->stage) (void)hipHostFree(e->stage);
   (void)hipStreamDestroy(e->stream);
   if (e->owner_refs != nullptr) e->owner_refs->fetch_sub(1);
@@ -666,6 +676,69 @@ int ef_hip_engine_reset(ef_hip_engine e) {
   e->chat_ids.clear();
   e->cached = 0;
   return EF_HIP_OK;
+}
+
+int ef_hip_engine_score(ef_hip_engine e, const int32_t* ids, size_t n, size_t first, double* nll_host,
+                        float* logits_dev) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(ids && nll_host, "engine_score: null argument");
+  EFH_CHECK(e->B == 1, "engine_score: scores one sequence (engine batch 1)");
+  EFH_CHECK(n >= 2 && first + 1 < n, "engine_score: need n >= 2 and first < n - 1");
+  EFH_CHECK(n - 1 <= e->max_seq, "engine_score: sequence longer than the KV cache");
+  for (size_t i = 0; i < n; ++i) {
+    if (ids[i] < 0 || static_cast<size_t>(ids[i]) >= e->c.V)
+      return fail(EF_HIP_EINVAL, "score: token id " + std::to_string(ids[i]) + " out of range");
+  }
+  const size_t V = e->c.V, m = n - 1;
+  size_t rows = 1024;  // [rows][V] logits per launch: 128 MB at V = 32000
+  if (const char* v = std::getenv("EF_HIP_PREFILL_ROWS"))  // test knob: smaller launches
+    rows = std::min<size_t>(rows, static_cast<size_t>(std::max<long>(1, std::atol(v))));
+  const size_t chunk = std::min(rows, m);
+  EFH_RC(ensure_prefill(e, chunk));
+  if (e->pf_logit_rows < chunk) {
+    if (e->pf_logits) (void)hipFree(e->pf_logits);
+    e->pf_logits = nullptr;
+    e->pf_logit_rows = 0;
+    EFH_RC(drop_graphs_with(e, kAllLogits));
+    EFH_HIP(hipMalloc(&e->pf_logits, chunk * V * sizeof(float)));
+    e->pf_logit_rows = chunk;
+  }
+  int32_t* targets = nullptr;
+  double* nll = nullptr;
+  EFH_HIP(hipMallocAsync(reinterpret_cast<void**>(&targets), n * sizeof(int32_t), e->stream));
+  EFH_HIP(hipMallocAsync(reinterpret_cast<void**>(&nll), n * sizeof(double), e->stream));
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  for (size_t i = 0; i < n; ++i) e->stage[i] = ids[i];
+  EFH_HIP(hipMemcpyAsync(e->hist, e->stage, n * 4, hipMemcpyHostToDevice, e->stream));
+  EFH_HIP(hipMemcpyAsync(targets, e->stage, n * 4, hipMemcpyHostToDevice, e->stream));
+  int rc = EF_HIP_OK;
+  for (size_t c0 = 0; c0 < m && rc == EF_HIP_OK; c0 += chunk) {
+    const size_t k = std::min(chunk, m - c0);
+    EFH_HIP(hipStreamSynchronize(e->stream));  // the pinned slot below is reused per chunk
+    e->stage[n] = static_cast<int32_t>(c0);
+    EFH_HIP(hipMemcpyAsync(e->pos, e->stage + n, 4, hipMemcpyHostToDevice, e->stream));
+    rc = run_step(e, kPrefill | kAllLogits | static_cast<int>(k << 8));
+    if (rc != EF_HIP_OK) break;
+    // rows of this chunk at positions >= first: targets are the next ids
+    const size_t lo = std::max(first, c0), hi = c0 + k;
+    if (lo < hi) {
+      rc = launch_nll(e->pf_logits + (lo - c0) * V, static_cast<int>(V), static_cast<long>(V), targets + lo + 1,
+                      static_cast<int>(hi - lo), nll + (lo - first), e->stream);
+      if (rc == EF_HIP_OK && logits_dev != nullptr &&
+          hipMemcpyAsync(logits_dev + (lo - first) * V, e->pf_logits + (lo - c0) * V, (hi - lo) * V * sizeof(float),
+                         hipMemcpyDeviceToDevice, e->stream) != hipSuccess)
+        rc = fail(EF_HIP_ERUNTIME, "score: logits copy");
+    }
+  }
+  if (rc == EF_HIP_OK &&
+      hipMemcpyAsync(nll_host, nll, (m - first) * sizeof(double), hipMemcpyDeviceToHost, e->stream) != hipSuccess)
+    rc = fail(EF_HIP_ERUNTIME, "score: nll copy");
+  (void)hipFreeAsync(targets, e->stream);
+  (void)hipFreeAsync(nll, e->stream);
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->cached = std::max(e->cached, m);
+  e->chat_ids.clear();
+  return rc;
 }
 
 // The token-level loop of ChatSession::reply (src/chat.cpp:174-259): reuse of the cached prefix

@@ -197,6 +197,15 @@ class Engine:
     def reset(self) -> None:
         EL.call("ef_hip_engine_reset", self.h)
 
+    def score(self, ids, first: int = 0, logits: H.DeviceArray | None = None) -> np.ndarray:
+        """Teacher-forced NLL of ids[p+1] at positions p in [first, n-1) (batch 1); logits, when given,
+        receives those positions' logits [(n-1-first)][V] on the device."""
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        nll = np.empty(ids.size - 1 - first, np.float64)
+        EL.call("ef_hip_engine_score", self.h, ids.ctypes.data_as(EL._i32p), ids.size, first,
+               nll.ctypes.data_as(C.POINTER(C.c_double)), logits.ptr if logits is not None else None)
+        return nll
+
     def close(self) -> None:
         if getattr(self, "h", None):
             EL.call("ef_hip_engine_destroy", self.h)

@@ -214,6 +214,20 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n
                            const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
                            double* prefill_s, double* decode_s);
 
+/* ---- quality of a quantized model (eval-quant, src/eval_quant.cpp) ---------------------------------
+ * compare_dist (src/eval_quant.cpp:48-96) over n positions of device logits: KL(P_ref || P_ours) in
+ * double, top-1 agreement, the reference confident (its top-1 probability >= 0.5), ours finite;
+ * kl_host (optional) gets each position's KL, agg the DistAgg totals in position order. */
+typedef struct {
+  size_t n, top1, confident, confident_top1, nonfinite;
+  double kl_sum, kl_max, kl_mean;
+} ef_hip_dist_stats;
+int ef_hip_compare_dist(const float* ref_dev, const float* ours_dev, size_t V, size_t n, size_t ld_ref, size_t ld_ours,
+                        double* kl_host, ef_hip_dist_stats* agg, void* stream);
+/* neg_log_prob (src/eval_quant.cpp:100-102): nll[p] = log_sum_exp(logits_p) - logits_p[target_p]. */
+int ef_hip_neg_log_prob(const float* logits_dev, size_t V, size_t n, size_t ld, const int32_t* targets_dev,
+                        double* nll_dev, void* stream);
+
 /* ---- chat turns ----------------------------------------------------------------------------------
  * The token-level loop of ef::ChatSession::reply (include/ef/chat.h:99-105, src/chat.cpp:174-259)
  * on an engine of batch 1: ids is the rendered conversation (the tokenizer and chat template stay
@@ -247,6 +261,13 @@ int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids_host, size_t n_ids, 
                         ef_hip_reply_stats* stats);
 /* ChatSession::reset (src/chat.cpp:143-148): forget the cached ids (the next turn prefills all). */
 int ef_hip_engine_reset(ef_hip_engine e);
+/* Teacher-forced scoring of one sequence (engine batch 1; eval-quant's text chunk loop,
+ * src/eval_quant.cpp:383-399): ids[0 .. n-2] at positions 0 .. n-2 in batched prefills with the
+ * logits of every position (the lm_head on the matrix cores), nll_host[p - first] =
+ * neg_log_prob(logits_p, ids[p+1]) for p in [first, n-1); logits_dev (optional) receives those
+ * positions' logits, [(n-1-first)][V]. */
+int ef_hip_engine_score(ef_hip_engine e, const int32_t* ids_host, size_t n, size_t first, double* nll_host,
+                        float* logits_dev);
 
 /* ---- .efq model files -------------------------------------------------------------------------
  * ef::QuantFile (include/ef/qfile.h:95-124).  ef_hip_efq_open maps a file and validates it as
