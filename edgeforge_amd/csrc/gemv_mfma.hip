@@ -277,13 +277,80 @@ __device__ __forceinline__ PairOps pair_ops(const uint8_t* row, bool q4, int m, 
   return o;
 }
 
+// Phase 3 of both batched kernels: the eight waves' partial sums combined in LDS in a fixed order
+// (the operand LDS is reused), the scale undone, then the epilogue (one K split) or the split's sums
+// to the workspace for finalize_kernel.
+template <int EPI, int RT, int NT>
+__device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb, uint8_t* lb,
+                                                  float (&acc)[NT][RT][EPI == kEpiSwiglu ? 2 : 1][2], int wave,
+                                                  int lane, int row0, int tile, int ks, int s0) {
+  constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
+  constexpr int ROWS = RT * kTileRows;
+  const int S = a.ksplit;
+  const int nloc = min(NT * kSeqTile, a.B - s0);  // this workgroup's sequences s0 .. s0 + nloc - 1
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lb);  // [wave][t][r][mt][lane][2]
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        float* p = red + ((((wave * NT + t) * RT + r) * NM + mt) * kWave + lane) * 2;
+        p[0] = acc[t][r][mt][0];
+        p[1] = acc[t][r][mt][1];
+      }
+  __syncthreads();
+  constexpr int wstep = NT * RT * NM * kWave * 2;  // floats per wave
+  // the workgroup's sums for output o = (sequence, row) of matrix mt, waves in order
+  auto wg_sum = [&](int o, int mt) {
+    const int sq = o / ROWS, jr = o % ROWS;
+    const int t = sq / kSeqTile, s = sq % kSeqTile, r = jr / kTileRows, jj = jr % kTileRows;
+    const int src = (jj + 16 * (s >> 1)) * 2 + (s & 1);  // lane holding D rows 4(l/16).., slot
+    const float* p = red + (((t * RT + r) * NM + mt) * kWave) * 2 + src;
+    float sum = p[0];
+#pragma unroll
+    for (int w = 1; w < kWavesM; ++w) sum += p[w * wstep];
+    return sum;
+  };
+  auto epilogue = [&](int o, const float (&v)[NM]) {
+    const int sq = s0 + o / ROWS, row = row0 + o % ROWS;
+    float* y = jb.y + sq * jb.ldy + row;
+    if (EPI == kEpiResidual) {
+      *y = *y + v[0];
+    } else if (EPI == kEpiSwiglu) {
+      *y = silu_m(v[0]) * v[NM - 1];
+    } else {
+      *y = v[0];
+    }
+  };
+  if (S == 1) {
+    for (int o = threadIdx.x; o < ROWS * nloc; o += kT) {
+      if (row0 + o % ROWS >= jb.rows) continue;
+      float v[NM];
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) v[mt] = wg_sum(o, mt) * a.post[s0 + o / ROWS];
+      epilogue(o, v);
+    }
+    return;
+  }
+  // split-K: this split's sums go to the workspace; finalize_kernel adds the splits in index order
+  // and applies the epilogue (the kernel boundary makes every split visible, no fences needed).
+  const size_t gsz = static_cast<size_t>(a.B) * ROWS * NM;
+  float* mine = a.part + (static_cast<size_t>(tile) * S + ks) * gsz + static_cast<size_t>(s0) * ROWS * NM;
+  for (int o = threadIdx.x; o < ROWS * nloc; o += kT) {
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) mine[o * NM + mt] = wg_sum(o, mt);
+  }
+}
+
 // RT row tiles of 16 rows per workgroup, NT sequence tiles of 8 sequences per launch.
 template <int EPI, int RT, int NT>
 __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lb[];
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
-  const int K = a.K, B = a.B, nb = K >> 5, np = K >> 6;
+  const int K = a.K, nb = K >> 5, np = K >> 6;
   const int S = a.ksplit, tile = blockIdx.x / S, ks = blockIdx.x % S;
   const MJob jb = find_mjob(a, tile);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x & (kWave - 1);
@@ -311,9 +378,10 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
 
   // 2. this wave's block pairs m = wave, wave + 8, ...; the A fragments of the next pair are
   //    loaded while the current pair's products run
-  const int j = lane & 15, g = lane >> 4;
-  const uint8_t* tab = (q4 ? a.t4 : a.t8) + static_cast<size_t>(lane) * 16;
+  // sequence tiles blockIdx.y * NT .. + NT - 1 of the launch (a grid row per group of tiles)
+  const int j = lane & 15, g = lane >> 4, s0 = blockIdx.y * NT * kSeqTile;
   const size_t tstride = static_cast<size_t>(nb) * kWave * 16;  // bytes per sequence tile
+  const uint8_t* tab = (q4 ? a.t4 : a.t8) + static_cast<size_t>(lane) * 16 + blockIdx.y * NT * tstride;
   float acc[NT][RT][NM][2];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -368,61 +436,7 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
     }
   }
 
-  // 3. combine the eight waves in order (the weight rows' LDS is reused), undo the scale, epilogue
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(lb);  // [wave][t][r][mt][lane][2]
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        float* p = red + ((((wave * NT + t) * RT + r) * NM + mt) * kWave + lane) * 2;
-        p[0] = acc[t][r][mt][0];
-        p[1] = acc[t][r][mt][1];
-      }
-  __syncthreads();
-  constexpr int wstep = NT * RT * NM * kWave * 2;  // floats per wave
-  // the workgroup's sums for output o = (sequence, row) of matrix mt, waves in order
-  auto wg_sum = [&](int o, int mt) {
-    const int sq = o / ROWS, jr = o % ROWS;
-    const int t = sq / kSeqTile, s = sq % kSeqTile, r = jr / kTileRows, jj = jr % kTileRows;
-    const int src = (jj + 16 * (s >> 1)) * 2 + (s & 1);  // lane holding D rows 4(l/16).., slot
-    const float* p = red + (((t * RT + r) * NM + mt) * kWave) * 2 + src;
-    float sum = p[0];
-#pragma unroll
-    for (int w = 1; w < kWavesM; ++w) sum += p[w * wstep];
-    return sum;
-  };
-  auto epilogue = [&](int o, const float (&v)[NM]) {
-    const int sq = o / ROWS, row = row0 + o % ROWS;
-    float* y = jb.y + sq * jb.ldy + row;
-    if (EPI == kEpiResidual) {
-      *y = *y + v[0];
-    } else if (EPI == kEpiSwiglu) {
-      *y = silu_m(v[0]) * v[NM - 1];
-    } else {
-      *y = v[0];
-    }
-  };
-  if (S == 1) {
-    for (int o = threadIdx.x; o < ROWS * B; o += kT) {
-      if (row0 + o % ROWS >= jb.rows) continue;
-      float v[NM];
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) v[mt] = wg_sum(o, mt) * a.post[o / ROWS];
-      epilogue(o, v);
-    }
-    return;
-  }
-  // split-K: this split's sums go to the workspace; finalize_kernel adds the splits in index order
-  // and applies the epilogue (the kernel boundary makes every split visible, no fences needed).
-  const size_t gsz = static_cast<size_t>(B) * ROWS * NM;
-  float* mine = a.part + (static_cast<size_t>(tile) * S + ks) * gsz;
-  for (int o = threadIdx.x; o < ROWS * B; o += kT) {
-#pragma unroll
-    for (int mt = 0; mt < NM; ++mt) mine[o * NM + mt] = wg_sum(o, mt);
-  }
+  combine_and_store<EPI, RT, NT>(a, jb, lb, acc, wave, lane, row0, tile, ks, s0);
 }
 
 struct FinArgs {
@@ -496,9 +510,24 @@ struct Plan {
   bool ok = false;
   bool q4 = false, q8 = false;
   int nm = 1, NT = 1, RT = 1, groups = 0, S = 1, pps = 0, chunk = 0;
+  int NTW = 1, SG = 1;  // sequence tiles per workgroup, and workgroup rows of the grid (NT = NTW * SG)
   size_t max_rb = 0, tab = 0, part_off = 0, bytes = 0, lds = 0;
   uint32_t row_stride = 0, w_stride = 0;
 };
+
+// LDS row stride for `pairs` block pairs per row: an odd number of 16-byte units, so the 16 rows a
+// B fragment reads fall in distinct banks.
+uint32_t odd_stride(size_t pairs, size_t pb, size_t max_rb) {
+  const size_t bytes = std::min<size_t>(pairs * pb, max_rb);
+  const size_t units = bytes / 16 + ((bytes / 16) % 2 == 0 ? 1 : 2);
+  return static_cast<uint32_t>(units * 16);
+}
+
+int groups_for(const GemvJob* jobs, int n_jobs, int rows_wg) {
+  int g = 0;
+  for (int j = 0; j < n_jobs; ++j) g += static_cast<int>((jobs[j].W->rows + rows_wg - 1) / rows_wg);
+  return g;
+}
 
 Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
   Plan p;
@@ -522,7 +551,7 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   // fragment to two matrices (and a second row tile would not fit in registers).
   p.RT = p.NT >= 4 && p.nm == 1 ? 2 : 1;
   const int rows_wg = p.RT * kTileRows;
-  for (int j = 0; j < n_jobs; ++j) p.groups += static_cast<int>((jobs[j].W->rows + rows_wg - 1) / rows_wg);
+  p.groups = groups_for(jobs, n_jobs, rows_wg);
   // Every workgroup streams the activation fragments of its K range through its CU's L2 port
   // (B x K x 4 bytes for the whole range).  Split K (one extra, tiny finalize launch) only when
   // that exceeds 512 KB; splits are multiples of 4 block pairs, at least 8 (one per wave).
@@ -534,13 +563,19 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   pps = (pps + 3) / 4 * 4;
   p.S = (np + pps - 1) / pps;
   p.pps = pps;
+  // Sequence groups: a workgroup takes NTW of the launch's NT sequence tiles, halving NTW (and the
+  // fragment bytes each workgroup streams) until every CU has a workgroup.  A workgroup's time is
+  // mostly its fragment stream, so small row counts (q / o at 64 sequences: 64 workgroups of 32
+  // rows) finish in a fraction of the time on 4x the CUs.
+  const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
+  p.NTW = p.NT;
+  while (p.NTW > 1 && static_cast<long>(p.groups) * p.S * (p.NT / p.NTW) < cus) p.NTW /= 2;
+  p.SG = p.NT / p.NTW;
   const size_t pb = p.q8 ? 68 : 36;
-  const size_t split_bytes = std::min<size_t>(static_cast<size_t>(pps) * pb, p.max_rb);
-  const size_t units = split_bytes / 16 + ((split_bytes / 16) % 2 == 0 ? 1 : 2);  // odd: distinct banks
-  p.row_stride = static_cast<uint32_t>(units * 16);
+  p.row_stride = odd_stride(static_cast<size_t>(pps), pb, p.max_rb);
   p.w_stride = static_cast<uint32_t>(rows_wg * p.row_stride);
   p.lds = std::max<size_t>(static_cast<size_t>(p.nm) * p.w_stride,
-                           static_cast<size_t>(kWavesM) * p.NT * p.RT * p.nm * kWave * 2 * 4);
+                           static_cast<size_t>(kWavesM) * p.NTW * p.RT * p.nm * kWave * 2 * 4);
   const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
   if (p.lds > lim) return p;
   // Layout: the A tables, the scales, the split-K partial sums.
@@ -587,9 +622,9 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
   a.ksplit = pl.S;
   a.pairs_per_split = pl.pps;
   a.part = reinterpret_cast<float*>(base + pl.part_off);
-  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(pl.RT, pl.NT)
-                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(pl.RT, pl.NT)
-                                                     : pick_mfma<kEpiSwiglu>(pl.RT, pl.NT));
+  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(pl.RT, pl.NTW)
+                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(pl.RT, pl.NTW)
+                                                     : pick_mfma<kEpiSwiglu>(pl.RT, pl.NTW));
   const int rows_wg = pl.RT * kTileRows;
   for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += pl.chunk) {
     const int nb = std::min(pl.chunk, batch - b0);
@@ -626,7 +661,9 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
       tiles += (d.rows + rows_wg - 1) / rows_wg;
     }
     void* params[] = {&a};
-    hipError_t e = hipLaunchKernel(fn, dim3(tiles * pl.S), dim3(kT), params, pl.lds, stream);
+    // the chunk's sequences cover ceil(nb / 8) tiles; grid rows past them would have no sequences
+    const int sg = std::min(pl.SG, (nb + pl.NTW * kSeqTile - 1) / (pl.NTW * kSeqTile));
+    hipError_t e = hipLaunchKernel(fn, dim3(tiles * pl.S, sg), dim3(kT), params, pl.lds, stream);
     if (e != hipSuccess) {
       rc = fail_hip(e, "gemv_mfma_kernel");
       break;
