@@ -381,6 +381,63 @@ __device__ __forceinline__ void dma_span(__amdgpu_buffer_rsrc_t r, uint32_t src_
   }
 }
 
+// LDS accesses the compiler does not see (inline assembly).  After an LDS-DMA load the compiler
+// makes every later LDS access of the same array wait for all outstanding vector-memory operations,
+// which would make the x staging wait for the weight rows it is meant to overlap; these helpers
+// wait only for their own LDS operation.
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  typedef const __attribute__((address_space(3))) void* lds_ptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)p));
+}
+typedef float f4n __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 lds_read4(const float* p) {
+  f4n v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void lds_write4(float* p, float4 v) {
+  const f4n w = {v.x, v.y, v.z, v.w};
+  asm volatile("ds_write_b128 %0, %1" : : "v"(lds_off(p)), "v"(w) : "memory");
+}
+__device__ __forceinline__ void lds_write1(float* p, float v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(lds_off(p)), "v"(v) : "memory");
+}
+// Workgroup barrier after this wave's LDS writes completed, without waiting for vector memory.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Waits until at most n of this wave's vector-memory operations are outstanding (n wave-uniform;
+// counts above 24 wait for all).  Operations retire in issue order, so issuing x before the weight
+// rows lets the x staging start while the rows are still in flight.
+__device__ __forceinline__ void wait_vmcnt_at_most(int n) {
+  switch (n) {
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
+
 template <int QT, int RR>
 __device__ __forceinline__ void lds_pair(const uint8_t* p, uint32_t (&d)[RR][PairOf<QT>::PD], int r) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
@@ -426,47 +483,58 @@ __global__ __launch_bounds__(NW * kWave) void gemv_dma_kernel(Args a) {
   const int wrow0 = (tile - jb.tile_begin) * jb.rows_per_tile + wave * RW;
   uint8_t* wl = lb + a.w_off + static_cast<uint32_t>(wave) * (EPI == kEpiSwiglu ? 2u : 1u) * a.w_stride;
 
-  // 1. every fetch of the workgroup, weights first (the largest latency)
+  // 1. every fetch of the workgroup: this wave's quarter of x (and of the norm weights), then its
+  //    weight rows; the staging below waits for x only, the dot products for the rows
+  int n_rows_ops;
   {
-    const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * rb;
-    const uint32_t region = static_cast<uint32_t>(RW) * rb;
-    const uint32_t src = static_cast<uint32_t>(wrow0) * rb;  // rows past the end read as zeros
-    dma_span<kNonTemporal>(make_rsrc(jb.W, mat_bytes), src, wl, (region + 15u) & ~15u, lane);
-    if (EPI == kEpiSwiglu)
-      dma_span<kNonTemporal>(make_rsrc(jb.W2, mat_bytes), src, wl + a.w_stride, (region + 15u) & ~15u, lane);
     const uint32_t xq = static_cast<uint32_t>(K) * 4u / NW;  // bytes of x per wave (a multiple of 16)
     const float* xb = jb.x + b * jb.ldx;
     dma_span<0>(make_rsrc(xb, static_cast<uint32_t>(K) * 4u), wave * xq, lb + a.raw_x_off + wave * xq, xq, lane);
     if (a.norm_w != nullptr)
       dma_span<0>(make_rsrc(a.norm_w, static_cast<uint32_t>(K) * 4u), wave * xq, lb + a.raw_nw_off + wave * xq, xq,
                   lane);
+    const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * rb;
+    const uint32_t region = (static_cast<uint32_t>(RW) * rb + 15u) & ~15u;
+    const uint32_t src = static_cast<uint32_t>(wrow0) * rb;  // rows past the end read as zeros
+    dma_span<kNonTemporal>(make_rsrc(jb.W, mat_bytes), src, wl, region, lane);
+    if (EPI == kEpiSwiglu) dma_span<kNonTemporal>(make_rsrc(jb.W2, mat_bytes), src, wl + a.w_stride, region, lane);
+    n_rows_ops = static_cast<int>((region + 1023u) / 1024u) * (EPI == kEpiSwiglu ? 2 : 1);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  wait_vmcnt_at_most(n_rows_ops);
+  // every wave's part of x is in LDS: a bare barrier (a __syncthreads fence would wait for the
+  // weight rows too)
+  asm volatile("s_barrier" ::: "memory");
 
-  // 2. normalise x into the padded slots (+ block sums)
+  // 2. normalise x into the padded slots (+ block sums), while the weight rows are in flight
   {
     float inv = 1.0f;
     if (a.norm_w != nullptr) {
       double ss = 0.0;
-      for (int i = threadIdx.x * 4; i < K; i += NT * 4) ss += sq_d(*reinterpret_cast<const float4*>(raw_x + i));
+      for (int i = threadIdx.x * 4; i < K; i += NT * 4) ss += sq_d(lds_read4(raw_x + i));
       ss = wave_sum_d(ss);
       if (lane == 0) red[wave] = ss;
-      __syncthreads();
+      lds_barrier();
       double tot = 0.0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) tot += red[w];  // waves in order
       inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)));
     }
     for (int i = threadIdx.x * 4; i < K; i += NT * 4) {
-      float4 v = *reinterpret_cast<const float4*>(raw_x + i);
-      if (a.norm_w != nullptr) v = norm4(v, *reinterpret_cast<const float4*>(raw_nw + i), inv);
-      store_x4(v, i, lds_x, lds_xs);
+      float4 v = lds_read4(raw_x + i);
+      if (a.norm_w != nullptr) v = norm4(v, lds_read4(raw_nw + i), inv);
+      lds_write4(lds_x + (i >> 6) * kSlot + (i & 63), v);
+      // K % 32 == 0: the 8 threads of a block are active together, xor partners stay in the group
+      float bs = (v.x + v.y) + (v.z + v.w);
+      bs += __shfl_xor(bs, 1, kWave);
+      bs += __shfl_xor(bs, 2, kWave);
+      bs += __shfl_xor(bs, 4, kWave);
+      if ((threadIdx.x & 7) == 0) lds_write1(lds_xs + (i >> 5), bs);
     }
     __syncthreads();
   }
 
-  // 3. dot products
+  // 3. dot products, once this wave's rows have landed (only this wave reads them)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const int grp = lane / G, t = lane % G;
   const int row0 = wrow0 + grp * R;
   const int nvalid = max(0, min(R, jb.rows - row0));
