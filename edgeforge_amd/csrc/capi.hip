@@ -285,10 +285,9 @@ int ef_hip_weight_release(ef_hip_weight w) {
   EFH_READY();
   EFH_RC(check_weight(w));
   w->magic = 0;
-  if (w->owned) {
-    EFH_HIP(hipStreamSynchronize(g_ctx.stream));
-    EFH_HIP(hipFree(const_cast<uint8_t*>(w->dev)));
-  }
+  if (w->owned || w->tiled != nullptr) EFH_HIP(hipStreamSynchronize(g_ctx.stream));
+  if (w->owned) EFH_HIP(hipFree(const_cast<uint8_t*>(w->dev)));
+  if (w->tiled != nullptr) EFH_HIP(hipFree(w->tiled));
   delete w;
   return EF_HIP_OK;
 }
@@ -375,10 +374,17 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
   EFH_HIP(hipEventCreate(&e1));
   int rc = EF_HIP_OK;
   const size_t ldx = W[0]->cols, ldy = W[0]->rows;
-  // batched launches get their activation workspace up front, as the decode engine does
+  // batched launches get their activation workspace and the matrices' tile-order copies up front,
+  // as the decode engine does
   void* ws = nullptr;
   size_t ws_bytes = 0;
   if (batch > 1) {
+    for (size_t i = 0; i < n_weights; ++i) {
+      for (const ef_hip_weight_s* w : {W[i], W2 ? W2[i] : nullptr}) {
+        if (w != nullptr && (w->qtype == EF_QTYPE_Q4_0 || w->qtype == EF_QTYPE_Q8_0) && w->cols % 32 == 0)
+          EFH_RC(ensure_tiled(w, s));
+      }
+    }
     const GemvJob j0{W[0], epi == kEpiSwiglu ? W2[0] : nullptr, x, y};
     ws_bytes = gemv_mfma_workspace_bytes(&j0, 1, epi, batch, ldx);
     if (ws_bytes > 0) EFH_HIP(hipMalloc(&ws, ws_bytes));

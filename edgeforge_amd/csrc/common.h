@@ -58,6 +58,9 @@ struct ef_hip_weight_s {
   const uint8_t* dev = nullptr;
   bool owned = false;
   uint32_t magic = 0;
+  // Copy of a Q4_0 / Q8_0 matrix in the batched GEMV's tile order (gemv_mfma.hip), made on the
+  // first batched use or at engine creation, freed with the handle.
+  mutable uint8_t* tiled = nullptr;
 };
 
 namespace efh {

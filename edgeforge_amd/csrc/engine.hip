@@ -420,6 +420,16 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   }
   EFH_RC(check_matrix(lm_head, c.V, c.D, "lm_head"));
   EFH_RC(check_matrix(embed, c.V, c.D, "embed_tokens"));
+  // Batched products (several sequences, or a prefill's positions) read packed matrices from a
+  // tile-order copy; make them now, before any graph is captured.
+  auto tile = [](ef_hip_weight w) {
+    return w->qtype == EF_QTYPE_Q4_0 || w->qtype == EF_QTYPE_Q8_0 ? ensure_tiled(w, ctx().stream) : EF_HIP_OK;
+  };
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = layers[l];
+    for (ef_hip_weight m : {w.wq, w.wk, w.wv, w.wo, w.w_gate, w.w_up, w.w_down}) EFH_RC(tile(m));
+  }
+  EFH_RC(tile(lm_head));
 
   auto* e = new ef_hip_engine_s;
   e->c = c;

@@ -33,6 +33,10 @@ bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU 
 // for the same launch) holds the prepared activation fragments and the split-K partial sums;
 // without it the launch allocates stream-ordered memory.  0 when the launch does not take this path.
 size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx);
+// The batched path reads Q4_0 / Q8_0 matrices from a tile-order copy (w->tiled, tiled_bytes(w)
+// bytes).  ensure_tiled makes it when missing (allocates; refused while `s` is capturing a graph).
+size_t tiled_bytes(const ef_hip_weight_s* w);
+int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s);
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 

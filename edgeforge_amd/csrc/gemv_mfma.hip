@@ -1,17 +1,18 @@
 // Packed Q4_0 / Q8_0 GEMV on the matrix cores for batches of sequences (2..64 per launch).
 //
-// Two kernels per launch:
+// Two kernels per launch (three with a K split):
 //  1. xfrag_kernel turns the activations [B][K] (optionally RMS-normalised, kern::rmsnorm order)
 //     into the A operands of v_mfma_f32_16x16x32_f16, in global memory, laid out exactly as a wave
-//     loads them: for each tile of 8 sequences and each 32-weight block, 64 lanes x 16 bytes (one
-//     coalesced 1 KB load).  A row i = 2s + p of a tile holds sequence s's hi (p = 0) or lo (p = 1)
-//     part: x' = x * 2^-e_s (a per-sequence power of two keeping |x'| < 2^15) split exactly into
-//     fp16 hi + lo (x' - hi - lo is below 2^-22 |x'|).  Columns follow the codes' k order below.
-//  2. gemv_mfma_kernel: a workgroup (8 waves) owns 16 or 32 rows (x2 matrices for SwiGLU); its
-//     rows' packed blocks are fetched with coalesced 1 KB LDS-DMA loads into LDS rows an odd number
-//     of 16-byte units apart (the 16 rows one B fragment reads fall in distinct banks).  The waves
-//     split the block pairs (pair m to wave m % 8).  Per pair, each matrix's codes are converted
-//     once into B operands and reused for every sequence tile:
+//     loads them: for each tile of 16 sequences, each 32-weight block and each part (hi, lo),
+//     64 lanes x 16 bytes (one coalesced 1 KB load).  Row i of a tile is sequence i: x' = x * 2^-e_s
+//     (a per-sequence power of two keeping |x'| < 2^15) split exactly into fp16 hi + lo
+//     (x' - hi - lo is below 2^-22 |x'|).  Columns follow the codes' k order below.
+//  2. gemv_mfma_kernel: a workgroup (8 waves) owns RT tiles of 16 rows (x2 matrices for SwiGLU),
+//     NS sequence tiles and a range of block pairs; its rows' packed blocks are fetched with
+//     coalesced 1 KB LDS-DMA loads into LDS rows an odd number of 16-byte units apart (the 16 rows
+//     one B fragment reads fall in distinct banks).  The waves split the block pairs (pair m to wave
+//     m % 8).  Per pair, each row tile's codes are converted once into B operands and reused for
+//     every sequence tile:
 //       B = the row's codes minus their bias as exact fp16, straight out of the packed bytes: one
 //           AND-OR of a Q4_0 dword with the fp16 pattern of 1024 yields two codes as 1024 + c
 //           ((q & 0x000F000F) | 0x64006400: codes 0 and 2 of the dword's low nibbles; the high
@@ -19,17 +20,28 @@
 //           1024 + 8 (resp. 1024 + 128) exactly.  Q8_0 codes are offset to unsigned (q ^ 0x80) and
 //           taken two per AND-OR the same way, minus 1024 + 128.  The A columns are permuted to
 //           match, and divided by 16 where the code is a scaled high nibble;
-//       D = A x B gives, for each sequence of the tile, hi and lo parts of sum_k (c_k - bias) x'_k;
-//           the block adds d * (D[2s][j] + D[2s+1][j]) to an FP32 accumulator.
-//     Partial sums of the eight waves are combined in LDS in a fixed order; the scale 2^e_s is
-//     undone and the epilogue (store / residual / SwiGLU) applied.
+//       D = A_hi x B, then D += A_lo x B on the matrix core (the accumulator input), so D holds
+//           sum_k (c_k - bias) x'_k of the block for 16 sequences x 16 rows, and the block adds
+//           d * D to an FP32 accumulator: one FMA per output and block, the only per-block VALU
+//           work besides the B conversion.
+//     The waves' partial sums are combined in LDS in a fixed order, one row tile at a time (the
+//     operand LDS is reused); the scale 2^e_s is undone and the epilogue (store / residual /
+//     SwiGLU) applied, or, with K split over workgroups, the split's sums go to a workspace.
+//  3. finalize_kernel (K split only) adds the splits in index order and applies the epilogue.
+// The planner sizes RT (rows per workgroup: every workgroup streams its sequences' A operands
+// through its CU, so more rows per workgroup mean fewer re-reads), NS and the K split to fill the
+// 256 CUs; measured aggregate L2 read bandwidth when every workgroup streams one shared table is
+// ~20-30 TB/s on MI355X.
 // (Codes as fp16 subnormals would save the add, but the matrix core does not sum products of
 // subnormal operands exactly: measured errors of thousands of ulps, biased; normal operands give
 // a few ulps, unbiased.)  Products are exact (fp16 x fp16 in FP32), so results match an FP32 dot
 // product to rounding; the order differs from the reference CPU kernels (src/qkernels.cpp:39-65,
 // 131-180) and is fixed for a given shape.  Single sequences use the vector-ALU kernels (gemv.hip),
 // which are faster when nothing amortises the activation preparation.
+#include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 
 #include "gemv.h"
 
@@ -41,31 +53,33 @@ constexpr int kWavesM = kT / kWave;
 constexpr int kTP = 1024;                       // prep workgroup
 constexpr int kWavesP = kTP / kWave;
 constexpr int kTileRows = 16;
-constexpr int kSeqTile = 8;                     // sequences per A operand (hi + lo rows)
-constexpr int kMaxTiles = 8;                    // sequence tiles per launch: 64 sequences
+constexpr int kSeqTile = 16;                    // sequences per A operand (one per row)
+constexpr int kMaxTiles = 4;                    // sequence tiles per launch: 64 sequences
 constexpr int kMaxJobsM = 4;
-constexpr int kPrepSplit = 4;                   // workgroups per sequence tile in xfrag_kernel
+constexpr int kPrepBlocks = kTP / kWave;        // blocks per xfrag workgroup: one per wave
+constexpr int kMaxBlocksPerWave = 8;            // K blocks per wave of one batched GEMV workgroup
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 struct MJob {
-  const uint8_t* W;
+  const uint8_t* W;     // tile-order copies (tile_layout_kernel)
   const uint8_t* W2;
   float* y;
-  int rows, qtype, row_bytes, tile_begin;
+  int rows, qtype, tile_begin;
+  uint32_t bytes;       // of each tile-order matrix
   long ldy;
 };
 
 struct MArgs {
   MJob job[kMaxJobsM];
   int n_jobs, K, B, n_tiles;
-  const uint8_t* t4;    // A tables (Q4_0 and Q8_0 column orders), [tile][block][64 lanes][16 bytes]
+  const uint8_t* t4;    // A tables (Q4_0 and Q8_0 column orders), [tile][block][hi, lo][64 lanes][16 bytes]
   const uint8_t* t8;
+  uint32_t tab_bytes;   // bytes of each table
   const float* post;    // [B] 2^e_s
-  uint32_t row_stride, w_stride;  // LDS: weight rows rs bytes apart, w_stride bytes per matrix
-  int ksplit, pairs_per_split;    // split-K: workgroups per row group and block pairs each
+  int ksplit, blocks_per_split;   // split-K: workgroups per row group and blocks each
   float* part;          // [group][split][B][rows of the group][matrices] partial sums (ksplit > 1)
 };
 
@@ -103,14 +117,18 @@ __device__ __forceinline__ float f16hi(uint32_t v) { return half_bits_to_float(v
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// (v & mask) | fp16(1024) pattern in both halves, minus (1024 + bias) in both halves: exact.
+// (v & mask) | fp16(1024) pattern in both halves, minus (1024 + bias) in both halves: exact.  The
+// mask comes in a scalar register and the pattern in a vector register, so that the AND-OR is one
+// v_and_or_b32 (its three-operand encoding takes no literal constants).
 __device__ __forceinline__ uint32_t codes2(uint32_t v, uint32_t mask, _Float16 minus) {
-  const uint32_t m = (v & mask) | 0x64006400u;
+  const uint32_t m = __builtin_amdgcn_readfirstlane(mask);
+  uint32_t pat = 0x64006400u, r;
+  asm("" : "+v"(pat));  // keep the pattern in a register
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(pat));
   h2 h;
-  __builtin_memcpy(&h, &m, 4);
+  __builtin_memcpy(&h, &r, 4);
   const h2 c = {minus, minus};
   h = h + c;
-  uint32_t r;
   __builtin_memcpy(&r, &h, 4);
   return r;
 }
@@ -137,27 +155,27 @@ __device__ __forceinline__ h8 q8_operand(uint32_t q0, uint32_t q1) {
 
 __device__ __forceinline__ float silu_m(float g) { return g / (1.0f + expf(-g)); }  // src/kernels.cpp:94
 
-// grid (kPrepSplit, tiles): every workgroup of a tile recomputes the tile's per-sequence factors
-// (a read of 8 x K floats from L2), then writes the fragments of its share of the blocks.
+// grid (ceil(nb / 16), tiles): workgroup (x, t) prepares sequences 16 t .. 16 t + 15 for blocks
+// 16 x .. 16 x + 15.  Every workgroup of a tile recomputes the tile's per-sequence factors (a read of
+// 16 x K floats, one wave per sequence), then each wave writes one block's fragments.
 __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
   __shared__ double s_ss[kWavesP];
   __shared__ float s_ax[kWavesP];
   __shared__ float s_aw[kWavesP];
   __shared__ float s_mul[kSeqTile], s_pre[kSeqTile];
+  static_assert(kWavesP == kSeqTile, "one wave per sequence of the tile");
   const int K = a.K, tile = blockIdx.y, nb = K >> 5;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const bool has_norm = a.norm_w != nullptr;
-  // 1. per-sequence sum of squares (double, kern::rmsnorm) and max |x|, and max |norm weight|.
-  //    Threads are sequence-major (128 per sequence), so each thread reduces one sequence and the
-  //    cross-lane reductions are one chain per wave rather than one per sequence.
+  // 1. per-sequence sum of squares (double, kern::rmsnorm) and max |x| (wave s reduces sequence
+  //    s), and max |norm weight| (every thread)
   {
-    constexpr int kPer = kTP / kSeqTile;  // threads per sequence: two waves
-    const int s = threadIdx.x / kPer, r = threadIdx.x % kPer, sq = tile * kSeqTile + s;
+    const int sq = tile * kSeqTile + wave;
     double ss = 0.0;
     float ax = 0.0f, aw = 0.0f;
     if (sq < a.B) {
       const float* xr = a.x + sq * a.ldx;
-      for (int k = r * 4; k < K; k += kPer * 4) {
+      for (int k = lane * 4; k < K; k += kWave * 4) {
         const float4 v = *reinterpret_cast<const float4*>(xr + k);
         ss += static_cast<double>(v.x) * static_cast<double>(v.x);
         ss += static_cast<double>(v.y) * static_cast<double>(v.y);
@@ -189,8 +207,8 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
     float aw = 0.0f;
     for (int w = 0; w < kWavesP; ++w) aw = fmaxf(aw, s_aw[w]);
     if (!has_norm) aw = 1.0f;
-    const double tot = s_ss[2 * s] + s_ss[2 * s + 1];  // the sequence's two waves
-    const float ax = fmaxf(s_ax[2 * s], s_ax[2 * s + 1]);
+    const double tot = s_ss[s];
+    const float ax = s_ax[s];
     const float inv = has_norm ? static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)))
                                : 1.0f;
     const float bound = ax * inv * aw * 1.0001f;  // >= max |w * (x * inv)|
@@ -201,14 +219,15 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
     if (blockIdx.x == 0 && sq < a.B) a.post[sq] = ldexpf(1.0f, e);
   }
   __syncthreads();
-  // 2. fragments: one (block, lane) per thread, 16 bytes each.  The 8 values of a Q4_0 fragment are
-  //    weights 4g..4g+3 and 4g+16..4g+19 of the block, of a Q8_0 fragment 8g..8g+7: two float4 each.
-  const int i = lane & 15, g = lane >> 4, s = i >> 1, part = i & 1, sq = tile * kSeqTile + s;
+  // 2. fragments: wave w writes block 16 x + w, lane l the 8 values of sequence l % 16 and k group
+  //    l / 16, hi and lo.  The 8 values of a Q4_0 fragment are weights 4g..4g+3 and 4g+16..4g+19
+  //    of the block, of a Q8_0 fragment 8g..8g+7: two float4 each.
+  const int kb = blockIdx.x * kPrepBlocks + wave;
+  if (kb >= nb) return;
+  const int i = lane & 15, g = lane >> 4, sq = tile * kSeqTile + i;
   const bool live = sq < a.B;
-  const float inv = s_mul[s], pre = s_pre[s];
+  const float inv = s_mul[i], pre = s_pre[i];
   const float* xr = a.x + (live ? sq : 0) * a.ldx;
-  const int per = (nb + kPrepSplit - 1) / kPrepSplit;
-  const int kb0 = blockIdx.x * per, kb1 = min(nb, kb0 + per);
   auto frag = [&](const int (&k0)[2], float (&out)[8]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -226,217 +245,290 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
       out[4 * h + 3] = v.w * pre;
     }
   };
-  auto split = [&](float xp) -> _Float16 {
-    const _Float16 hi = static_cast<_Float16>(xp);
-    return part == 0 ? hi : static_cast<_Float16>(xp - static_cast<float>(hi));
+  // hi and lo parts of the 8 values in slot order `ord`, slots with q16 set divided by 16
+  auto store = [&](uint8_t* table, const float (&xv)[8], const int (&ord)[8], const bool (&q16)[8]) {
+    h8 hi, lo;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float xp = xv[ord[u]];
+      const _Float16 h = static_cast<_Float16>(xp);
+      const _Float16 l = static_cast<_Float16>(xp - static_cast<float>(h));
+      const _Float16 q = static_cast<_Float16>(q16[u] ? 0.0625f : 1.0f);  // exact powers of two
+      hi[u] = h * q;
+      lo[u] = l * q;
+    }
+    uint8_t* f = table + ((static_cast<size_t>(tile) * nb + kb) * 2 * kWave + lane) * 16;
+    *reinterpret_cast<h8*>(f) = hi;
+    *reinterpret_cast<h8*>(f + kWave * 16) = lo;
   };
-  for (int kb = kb0 + wave; kb < kb1; kb += kWavesP) {
-    if (a.t4 != nullptr) {  // slots 0..7 = weights 4g + {0, 2, 16, 18, 1, 3, 17, 19}
-      const int k0[2] = {kb * 32 + 4 * g, kb * 32 + 16 + 4 * g};
-      float xv[8];
-      frag(k0, xv);
-      const _Float16 q = static_cast<_Float16>(0.0625f);  // pairs a code scaled by 16
-      const h8 f = {split(xv[0]), split(xv[2]), split(xv[4]) * q, split(xv[6]) * q,
-                    split(xv[1]), split(xv[3]), split(xv[5]) * q, split(xv[7]) * q};
-      *reinterpret_cast<h8*>(a.t4 + ((static_cast<size_t>(tile) * nb + kb) * kWave + lane) * 16) = f;
-    }
-    if (a.t8 != nullptr) {  // slots 0..7 = weights 8g + {0, 2, 1, 3, 4, 6, 5, 7}
-      const int k0[2] = {kb * 32 + 8 * g, kb * 32 + 8 * g + 4};
-      float xv[8];
-      frag(k0, xv);
-      const h8 f = {split(xv[0]), split(xv[2]), split(xv[1]), split(xv[3]),
-                    split(xv[4]), split(xv[6]), split(xv[5]), split(xv[7])};
-      *reinterpret_cast<h8*>(a.t8 + ((static_cast<size_t>(tile) * nb + kb) * kWave + lane) * 16) = f;
-    }
+  if (a.t4 != nullptr) {  // slots 0..7 = weights 4g + {0, 2, 16, 18, 1, 3, 17, 19}
+    const int k0[2] = {kb * 32 + 4 * g, kb * 32 + 16 + 4 * g};
+    float xv[8];
+    frag(k0, xv);
+    constexpr int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    constexpr bool q16[8] = {false, false, true, true, false, false, true, true};
+    store(a.t4, xv, ord, q16);
+  }
+  if (a.t8 != nullptr) {  // slots 0..7 = weights 8g + {0, 2, 1, 3, 4, 6, 5, 7}
+    const int k0[2] = {kb * 32 + 8 * g, kb * 32 + 8 * g + 4};
+    float xv[8];
+    frag(k0, xv);
+    constexpr int ord[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    constexpr bool q16[8] = {false, false, false, false, false, false, false, false};
+    store(a.t8, xv, ord, q16);
   }
 }
 
-// B operands and block scales of one 16-row tile, one block pair, one matrix.
-struct PairOps {
-  h8 b0, b1;
-  float d0, d1;
+// Weights in tile order: for every 16-row tile T and block b, the 16 rows' codes in the order the
+// B fragment's lanes use them (lane l = 16 g + j: row j's code bytes 4g .. 4g + 3 of a Q4_0 block,
+// 8g .. 8g + 7 of a Q8_0 block), then the 16 rows' fp16 scales: 288 (Q4_0) or 544 (Q8_0) bytes at
+// (T * nb + b) * bytes.  A wave reads one tile-block with one coalesced load per lane.
+constexpr uint32_t kTileBlockQ4 = 288, kTileBlockQ8 = 544;
+
+__global__ __launch_bounds__(256) void tile_layout_kernel(const uint8_t* __restrict__ W, int rows, int nb,
+                                                          int row_bytes, int q4, uint8_t* __restrict__ out) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;  // (tile, block, lane)
+  const int tiles = (rows + kTileRows - 1) / kTileRows;
+  const int lane = static_cast<int>(idx % kWave);
+  const long tb = idx / kWave;
+  const int blk = static_cast<int>(tb % nb), T = static_cast<int>(tb / nb);
+  if (T >= tiles) return;
+  const int j = lane & 15, g = lane >> 4, row = T * kTileRows + j;
+  const uint32_t bb = q4 ? kTileBlockQ4 : kTileBlockQ8;
+  uint8_t* o = out + static_cast<size_t>(T * nb + blk) * bb;
+  const uint8_t* src = W + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(blk) * (q4 ? 18 : 34);
+  const bool live = row < rows;  // rows past the matrix: zero codes and scales
+  const int nc = q4 ? 4 : 8;
+  for (int c = 0; c < nc; ++c) o[lane * nc + c] = live ? src[2 + nc * g + c] : 0;
+  if (g == 0) {  // the scale after the 64 lanes' codes
+    uint8_t* sc = o + kWave * nc + 2 * j;
+    sc[0] = live ? src[0] : 0;
+    sc[1] = live ? src[1] : 0;
+  }
+}
+
+// B operand and scale of one 16-row tile-block.
+template <bool Q4>
+struct WRegs {
+  uint32_t c0, c1;  // this lane's code bytes (c1 unused for Q4_0)
+  uint32_t sc;      // the lane's row scale, fp16 bits in the low half
 };
 
-__device__ __forceinline__ PairOps pair_ops(const uint8_t* row, bool q4, int m, int g) {
-  PairOps o;
-  const uint32_t* P = reinterpret_cast<const uint32_t*>(row);
-  if (q4) {
-    const uint32_t* pp = P + m * 9;
-    o.d0 = f16lo(pp[0]);
-    o.d1 = f16hi(pp[4]);
-    o.b0 = q4_operand(__builtin_amdgcn_alignbyte(pp[g + 1], pp[g], 2));
-    o.b1 = q4_operand(pp[5 + g]);
+template <bool Q4>
+__device__ __forceinline__ WRegs<Q4> load_w(__amdgpu_buffer_rsrc_t r, uint32_t voff_c, uint32_t voff_s,
+                                            uint32_t so) {
+  WRegs<Q4> w;
+  if constexpr (Q4) {
+    w.c0 = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, voff_c, so, 0));
+    w.c1 = 0;
   } else {
-    const uint32_t* pp = P + m * 17;
-    o.d0 = f16lo(pp[0]);
-    o.d1 = f16hi(pp[8]);
-    o.b0 = q8_operand(__builtin_amdgcn_alignbyte(pp[2 * g + 1], pp[2 * g], 2),
-                      __builtin_amdgcn_alignbyte(pp[2 * g + 2], pp[2 * g + 1], 2));
-    o.b1 = q8_operand(pp[9 + 2 * g], pp[10 + 2 * g]);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff_c, so, 0);
+    w.c0 = static_cast<uint32_t>(v[0]);
+    w.c1 = static_cast<uint32_t>(v[1]);
   }
-  return o;
+  w.sc = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, voff_s, so, 0));
+  return w;
 }
 
-// Phase 3 of both batched kernels: the eight waves' partial sums combined in LDS in a fixed order
-// (the operand LDS is reused), the scale undone, then the epilogue (one K split) or the split's sums
-// to the workspace for finalize_kernel.
-template <int EPI, int RT, int NT>
+// Products of one block for every row tile and matrix: D = A_hi B, D += A_lo B on the matrix core,
+// acc += d D.  Software-pipelined over the (row tile, matrix) units: while unit u's products run on
+// the matrix core, the vector ALU converts unit u + 1's codes and applies unit u - 1's scales, so
+// neither pipe waits on the other (each stage is kept together by a scheduling barrier, and inside
+// it products and vector instructions alternate).
+template <int RT, int NM, int NS, bool Q4>
+__device__ __forceinline__ void block_products(const WRegs<Q4> (&W)[RT][NM], const h8 (&Ax)[NS][2],
+                                               f4v (&acc)[RT][NM][NS]) {
+  constexpr int U = RT * NM;
+  const f4v Z = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto operand = [&](int u) -> h8 {
+    const WRegs<Q4>& w = W[u / NM][u % NM];
+    return Q4 ? q4_operand(w.c0) : q8_operand(w.c0, w.c1);
+  };
+  auto scale = [&](int u) -> float { return f16lo(W[u / NM][u % NM].sc); };
+  h8 b = operand(0);
+  f4v Dp[NS];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    f4v D[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) D[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ax[t][0], b, Z, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) D[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ax[t][1], b, D[t], 0, 0, 0);
+    if (u > 0) {
+      const float d = scale(u - 1);
+      const int rt = (u - 1) / NM, mt = (u - 1) % NM;
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(d, Dp[t][r], acc[rt][mt][t][r]);
+    }
+    if (u + 1 < U) b = operand(u + 1);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) Dp[t] = D[t];
+    constexpr int kValuPer = (12 + 4 * NS + 2 * NS - 1) / (2 * NS);
+#pragma unroll
+    for (int i = 0; i < 2 * NS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // one product
+      __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);  // vector ALU work
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {
+    const float d = scale(U - 1);
+    const int rt = (U - 1) / NM, mt = (U - 1) % NM;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(d, Dp[t][r], acc[rt][mt][t][r]);
+  }
+}
+
+// The wave's blocks b = kb0 + wave + 8 i < kb1: the weights two blocks ahead and the A fragments
+// one block ahead are loaded while the current block's products run.  Loads past a buffer's range
+// read as zeros, so the prefetches need no bounds test.
+template <int RT, int NM, int NS, bool Q4>
+__device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, int kb0, int kb1, int wave, int lane,
+                                       __amdgpu_buffer_rsrc_t tab, uint32_t tile0, uint32_t tstride,
+                                       f4v (&acc)[RT][NM][NS]) {
+  const uint32_t bb = Q4 ? kTileBlockQ4 : kTileBlockQ8;
+  const __amdgpu_buffer_rsrc_t r1 = make_rsrc(jb.W, jb.bytes);
+  const __amdgpu_buffer_rsrc_t r2 = make_rsrc(NM == 2 ? jb.W2 : jb.W, jb.bytes);
+  const uint32_t voff_c = static_cast<uint32_t>(lane) * (Q4 ? 4 : 8);
+  const uint32_t voff_s = (Q4 ? 256u : 512u) + 2u * static_cast<uint32_t>(lane & 15);
+  const uint32_t voff_a = static_cast<uint32_t>(lane) * 16;
+  auto load_wb = [&](WRegs<Q4> (&dst)[RT][NM], int kb) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>((tile_row0 + rt) * nb + kb) * bb);
+      dst[rt][0] = load_w<Q4>(r1, voff_c, voff_s, so);
+      if (NM == 2) dst[rt][NM - 1] = load_w<Q4>(r2, voff_c, voff_s, so);
+    }
+  };
+  auto load_a = [&](h8 (&dst)[NS][2], int kb) {
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t so =
+            __builtin_amdgcn_readfirstlane(tile0 + t * tstride + static_cast<uint32_t>(kb * 2 + h) * kWave * 16);
+        dst[t][h] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(tab, voff_a, so, 0));
+      }
+  };
+  // Fully unrolled over at most kMaxBlocksPerWave blocks.  Every prefetch is issued
+  // unconditionally (a block past this workgroup's range is read and never used; past the matrix
+  // it reads as zeros), so every path has the same loads in flight and the wait before each
+  // block's products covers only that block's loads.
+  WRegs<Q4> W[kMaxBlocksPerWave][RT][NM];
+  h8 A[2][NS][2];
+  const int kb = kb0 + wave;
+  load_wb(W[0], kb);
+  load_wb(W[1], kb + kWavesM);
+  load_a(A[0], kb);
+#pragma unroll
+  for (int i = 0; i < kMaxBlocksPerWave; ++i) {
+    const int b = kb + i * kWavesM;
+    if (b >= kb1) break;
+    if (i + 1 < kMaxBlocksPerWave) load_a(A[(i + 1) & 1], b + kWavesM);
+    if (i + 2 < kMaxBlocksPerWave) load_wb(W[i + 2], b + 2 * kWavesM);
+    block_products<RT, NM, NS, Q4>(W[i], A[i & 1], acc);
+  }
+}
+
+// Phase 3: the eight waves' partial sums reduced through LDS and scattered: every wave writes its
+// D fragments, then wave w adds fragments f = w, w + 8, ... of all eight waves (in wave order, a
+// fixed order) and finishes them from registers: the scale undone and the epilogue (one K split)
+// or the split's sums to the workspace for finalize_kernel.  acc[rt][mt][t] is fragment
+// f = rt * NS + t of matrix mt: lane l holds rows 4 (l / 16) .. + 3 (sequences) of column l % 16.
+template <int EPI, int RT, int NS>
 __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb, uint8_t* lb,
-                                                  float (&acc)[NT][RT][EPI == kEpiSwiglu ? 2 : 1][2], int wave,
-                                                  int lane, int row0, int tile, int ks, int s0) {
+                                                  const f4v (&acc)[RT][EPI == kEpiSwiglu ? 2 : 1][NS], int wave,
+                                                  int lane, int row0, int grp, int ks, int s0) {
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
-  const int S = a.ksplit;
-  const int nloc = min(NT * kSeqTile, a.B - s0);  // this workgroup's sequences s0 .. s0 + nloc - 1
+  constexpr int F = RT * NS;                       // fragments per matrix
+  constexpr int wstep = F * NM * kWave * 4;         // floats per wave
+  f4v* red = reinterpret_cast<f4v*>(lb);          // [wave][f][mt][lane]
+  __syncthreads();  // the operands are no longer read
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) red[(wave * F + rt * NS + t) * NM * kWave + mt * kWave + lane] = acc[rt][mt][t];
   __syncthreads();
-  float* red = reinterpret_cast<float*>(lb);  // [wave][t][r][mt][lane][2]
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        float* p = red + ((((wave * NT + t) * RT + r) * NM + mt) * kWave + lane) * 2;
-        p[0] = acc[t][r][mt][0];
-        p[1] = acc[t][r][mt][1];
-      }
-  __syncthreads();
-  constexpr int wstep = NT * RT * NM * kWave * 2;  // floats per wave
-  // the workgroup's sums for output o = (sequence, row) of matrix mt, waves in order
-  auto wg_sum = [&](int o, int mt) {
-    const int sq = o / ROWS, jr = o % ROWS;
-    const int t = sq / kSeqTile, s = sq % kSeqTile, r = jr / kTileRows, jj = jr % kTileRows;
-    const int src = (jj + 16 * (s >> 1)) * 2 + (s & 1);  // lane holding D rows 4(l/16).., slot
-    const float* p = red + (((t * RT + r) * NM + mt) * kWave) * 2 + src;
-    float sum = p[0];
-#pragma unroll
-    for (int w = 1; w < kWavesM; ++w) sum += p[w * wstep];
-    return sum;
-  };
-  auto epilogue = [&](int o, const float (&v)[NM]) {
-    const int sq = s0 + o / ROWS, row = row0 + o % ROWS;
-    float* y = jb.y + sq * jb.ldy + row;
-    if (EPI == kEpiResidual) {
-      *y = *y + v[0];
-    } else if (EPI == kEpiSwiglu) {
-      *y = silu_m(v[0]) * v[NM - 1];
-    } else {
-      *y = v[0];
-    }
-  };
-  if (S == 1) {
-    for (int o = threadIdx.x; o < ROWS * nloc; o += kT) {
-      if (row0 + o % ROWS >= jb.rows) continue;
-      float v[NM];
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) v[mt] = wg_sum(o, mt) * a.post[s0 + o / ROWS];
-      epilogue(o, v);
-    }
-    return;
-  }
-  // split-K: this split's sums go to the workspace; finalize_kernel adds the splits in index order
-  // and applies the epilogue (the kernel boundary makes every split visible, no fences needed).
+  const int S = a.ksplit, j = lane & 15, g = lane >> 4;
   const size_t gsz = static_cast<size_t>(a.B) * ROWS * NM;
-  float* mine = a.part + (static_cast<size_t>(tile) * S + ks) * gsz + static_cast<size_t>(s0) * ROWS * NM;
-  for (int o = threadIdx.x; o < ROWS * nloc; o += kT) {
+  float* mine = a.part + (static_cast<size_t>(grp) * S + ks) * gsz;
+  for (int f = wave; f < F; f += kWavesM) {
+    const int rt = f / NS, t = f % NS;
+    f4v v[NM];
 #pragma unroll
-    for (int mt = 0; mt < NM; ++mt) mine[o * NM + mt] = wg_sum(o, mt);
+    for (int mt = 0; mt < NM; ++mt) {
+      const f4v* p = red + (f * NM + mt) * kWave + lane;
+      v[mt] = p[0];
+#pragma unroll
+      for (int w = 1; w < kWavesM; ++w) v[mt] += p[w * (wstep / 4)];
+    }
+    const int rl = rt * kTileRows + j, row = row0 + rl;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int sq = s0 + t * kSeqTile + 4 * g + r;
+      if (sq >= a.B) break;
+      if (S > 1) {  // finalize_kernel adds the splits in index order (the kernel boundary makes
+                    // every split visible, no fences needed)
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) mine[(static_cast<size_t>(sq) * ROWS + rl) * NM + mt] = v[mt][r];
+        continue;
+      }
+      if (row >= jb.rows) continue;
+      const float post = a.post[sq];
+      float* y = jb.y + sq * jb.ldy + row;
+      if (EPI == kEpiResidual) {
+        *y = *y + v[0][r] * post;
+      } else if (EPI == kEpiSwiglu) {
+        *y = silu_m(v[0][r] * post) * (v[NM - 1][r] * post);
+      } else {
+        *y = v[0][r] * post;
+      }
+    }
   }
 }
 
-// RT row tiles of 16 rows per workgroup, NT sequence tiles of 8 sequences per launch.
-template <int EPI, int RT, int NT>
+// RT row tiles of 16 rows per workgroup, NS sequence tiles of 16 sequences per workgroup.
+template <int EPI, int RT, int NS>
 __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lb[];
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
-  const int K = a.K, nb = K >> 5, np = K >> 6;
-  const int S = a.ksplit, tile = blockIdx.x / S, ks = blockIdx.x % S;
-  const MJob jb = find_mjob(a, tile);
+  const int nb = a.K >> 5;
+  const int S = a.ksplit, grp = blockIdx.x / S, ks = blockIdx.x % S;
+  const MJob jb = find_mjob(a, grp);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x & (kWave - 1);
-  const int row0 = (tile - jb.tile_begin) * ROWS;
-  const uint32_t rb = static_cast<uint32_t>(jb.row_bytes), rs = a.row_stride;
+  const int row0 = (grp - jb.tile_begin) * ROWS;
   const bool q4 = jb.qtype == EF_QTYPE_Q4_0;
-  const uint32_t pb = q4 ? 36u : 68u;  // bytes per block pair
-  // this workgroup's block pairs [p0, p1): multiples of 4 pairs, so their bytes are 16-byte units
-  const int p0 = ks * a.pairs_per_split, p1 = min(np, p0 + a.pairs_per_split);
-
-  // 1. wave w fetches the split's bytes of rows w, w + 8, ... (rows past the end read as zeros)
-  {
-    const uint32_t mat_bytes = static_cast<uint32_t>(jb.rows) * rb;
-    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(jb.W, mat_bytes);
-    const __amdgpu_buffer_rsrc_t r2 = make_rsrc(EPI == kEpiSwiglu ? jb.W2 : jb.W, mat_bytes);
-    const uint32_t bytes = static_cast<uint32_t>(p1 - p0) * pb;
+  // this workgroup's blocks [kb0, kb1)
+  const int kb0 = ks * a.blocks_per_split, kb1 = min(nb, kb0 + a.blocks_per_split);
+  const int s0 = blockIdx.y * NS * kSeqTile;
+  // A fragments through a buffer resource: the lane's 16 bytes at voffset 16 l, the wave-uniform
+  // fragment offset in a scalar register (no per-lane address arithmetic)
+  const uint32_t tstride = static_cast<uint32_t>(nb) * 2 * kWave * 16;  // bytes per sequence tile
+  const __amdgpu_buffer_rsrc_t tab = make_rsrc(q4 ? a.t4 : a.t8, a.tab_bytes);
+  const uint32_t tile0 = blockIdx.y * NS * tstride;
+  f4v acc[RT][NM][NS];
 #pragma unroll
-    for (int r = 0; r < ROWS / kWavesM; ++r) {
-      const int jr = wave + kWavesM * r;
-      const uint32_t src = static_cast<uint32_t>(row0 + jr) * rb + static_cast<uint32_t>(p0) * pb;
-      dma_copy<kNonTemporal>(r1, src, lb + jr * rs, bytes, lane);
-      if (EPI == kEpiSwiglu) dma_copy<kNonTemporal>(r2, src, lb + a.w_stride + jr * rs, bytes, lane);
-    }
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+      for (int t = 0; t < NS; ++t) acc[rt][mt][t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  const int tile_row0 = row0 / kTileRows;
+  if (q4) {
+    k_loop<RT, NM, NS, true>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc);
+  } else {
+    k_loop<RT, NM, NS, false>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc);
   }
 
-  // 2. this wave's block pairs m = wave, wave + 8, ...; the A fragments of the next pair are
-  //    loaded while the current pair's products run
-  // sequence tiles blockIdx.y * NT .. + NT - 1 of the launch (a grid row per group of tiles)
-  const int j = lane & 15, g = lane >> 4, s0 = blockIdx.y * NT * kSeqTile;
-  const size_t tstride = static_cast<size_t>(nb) * kWave * 16;  // bytes per sequence tile
-  const uint8_t* tab = (q4 ? a.t4 : a.t8) + static_cast<size_t>(lane) * 16 + blockIdx.y * NT * tstride;
-  float acc[NT][RT][NM][2];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) acc[t][r][mt][0] = acc[t][r][mt][1] = 0.0f;
-  const f4v Z = {0.0f, 0.0f, 0.0f, 0.0f};
-  h8 A[2][NT][2];
-  auto load_a = [&](h8 (&dst)[NT][2], int m) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const uint8_t* tp = tab + t * tstride + static_cast<size_t>(2 * m) * kWave * 16;
-      dst[t][0] = *reinterpret_cast<const h8*>(tp);
-      dst[t][1] = *reinterpret_cast<const h8*>(tp + kWave * 16);
-    }
-  };
-  // All products of a row tile are issued before any result is read, so the matrix pipe stays
-  // full instead of draining on every accumulator update.
-  auto compute = [&](const h8 (&Ax)[NT][2], int m) {
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        const PairOps o = pair_ops(lb + mt * a.w_stride + (r * kTileRows + j) * rs, q4, m - p0, g);
-        f4v D[NT][2];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ax[t][0], o.b0, Z, 0, 0, 0);
-          D[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ax[t][1], o.b1, Z, 0, 0, 0);
-        }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          acc[t][r][mt][0] = fmaf(o.d0, D[t][0][0] + D[t][0][1], acc[t][r][mt][0]);
-          acc[t][r][mt][1] = fmaf(o.d0, D[t][0][2] + D[t][0][3], acc[t][r][mt][1]);
-          acc[t][r][mt][0] = fmaf(o.d1, D[t][1][0] + D[t][1][1], acc[t][r][mt][0]);
-          acc[t][r][mt][1] = fmaf(o.d1, D[t][1][2] + D[t][1][3], acc[t][r][mt][1]);
-        }
-      }
-    }
-  };
-  if (p0 + wave < p1) load_a(A[0], p0 + wave);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // weight rows (and the first fragments) landed
-  __syncthreads();
-  for (int m = p0 + wave; m < p1; m += 2 * kWavesM) {
-    const int m1 = m + kWavesM;
-    if (m1 < p1) load_a(A[1], m1);
-    compute(A[0], m);
-    if (m1 < p1) {
-      if (m1 + kWavesM < p1) load_a(A[0], m1 + kWavesM);
-      compute(A[1], m1);
-    }
-  }
-
-  combine_and_store<EPI, RT, NT>(a, jb, lb, acc, wave, lane, row0, tile, ks, s0);
+  combine_and_store<EPI, RT, NS>(a, jb, lb, acc, wave, lane, row0, grp, ks, s0);
 }
 
 struct FinArgs {
@@ -478,30 +570,34 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinArgs a) {
   }
 }
 
-template <int EPI, int RT>
-void* pick_mfma_nt(int nt) {
-  if (nt <= 1) return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, 1>);
-  if (nt <= 2) return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, 2>);
-  if (nt <= 4) return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, 4>);
-  return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, 8>);
+// (RT, NS) shapes the kernels are instantiated for: the ones whose registers fit in 256 VGPRs
+// (two waves per SIMD) without spilling.  SwiGLU keeps two accumulators per output.
+struct Shape {
+  int RT, NS;
+};
+constexpr Shape kShapesStore[] = {{2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {4, 4}, {8, 1}, {8, 2}};
+constexpr Shape kShapesSwiglu[] = {{2, 1}, {2, 2}, {2, 4}, {3, 1}, {3, 2}, {4, 1}, {4, 2}};
+
+template <int EPI, int RT, int NS>
+void* kfn() {
+  return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, NS>);
 }
 
+// The instantiated kernel of shape (rt, ns): one of kShapesStore / kShapesSwiglu.
 template <int EPI>
-void* pick_mfma(int rt, int nt) {
+void* pick_mfma(int rt, int ns) {
   if constexpr (EPI == kEpiSwiglu) {
-    return pick_mfma_nt<EPI, 1>(nt);
+    if (rt == 4) return ns == 2 ? kfn<EPI, 4, 2>() : kfn<EPI, 4, 1>();
+    if (rt == 3) return ns == 2 ? kfn<EPI, 3, 2>() : kfn<EPI, 3, 1>();
+    return ns == 4 ? kfn<EPI, 2, 4>() : (ns == 2 ? kfn<EPI, 2, 2>() : kfn<EPI, 2, 1>());
   } else {
-    return rt == 2 ? pick_mfma_nt<EPI, 2>(nt) : pick_mfma_nt<EPI, 1>(nt);
+    if (rt == 8) return ns == 2 ? kfn<EPI, 8, 2>() : kfn<EPI, 8, 1>();
+    if (rt == 4) return ns == 4 ? kfn<EPI, 4, 4>() : (ns == 2 ? kfn<EPI, 4, 2>() : kfn<EPI, 4, 1>());
+    return ns == 4 ? kfn<EPI, 2, 4>() : (ns == 2 ? kfn<EPI, 2, 2>() : kfn<EPI, 2, 1>());
   }
 }
 
 }  // namespace
-
-// Sequence tiles the kernels are instantiated for: 1, 2, 4 or 8 (a launch covers up to 64 sequences).
-static int tiles_for(int nseq) {
-  const int nt = (std::min(nseq, kMaxTiles * kSeqTile) + kSeqTile - 1) / kSeqTile;
-  return nt <= 1 ? 1 : (nt <= 2 ? 2 : (nt <= 4 ? 4 : 8));
-}
 
 namespace {
 
@@ -509,19 +605,10 @@ namespace {
 struct Plan {
   bool ok = false;
   bool q4 = false, q8 = false;
-  int nm = 1, NT = 1, RT = 1, groups = 0, S = 1, pps = 0, chunk = 0;
-  int NTW = 1, SG = 1;  // sequence tiles per workgroup, and workgroup rows of the grid (NT = NTW * SG)
-  size_t max_rb = 0, tab = 0, part_off = 0, bytes = 0, lds = 0;
-  uint32_t row_stride = 0, w_stride = 0;
+  int nm = 1, NT = 1, RT = 2, NS = 1, SG = 1, groups = 0, S = 1, bps = 0, chunk = 0;
+  size_t tab = 0, part_off = 0, bytes = 0, lds = 0;
+  double cost = 0.0;
 };
-
-// LDS row stride for `pairs` block pairs per row: an odd number of 16-byte units, so the 16 rows a
-// B fragment reads fall in distinct banks.
-uint32_t odd_stride(size_t pairs, size_t pb, size_t max_rb) {
-  const size_t bytes = std::min<size_t>(pairs * pb, max_rb);
-  const size_t units = bytes / 16 + ((bytes / 16) % 2 == 0 ? 1 : 2);
-  return static_cast<uint32_t>(units * 16);
-}
 
 int groups_for(const GemvJob* jobs, int n_jobs, int rows_wg) {
   int g = 0;
@@ -529,16 +616,58 @@ int groups_for(const GemvJob* jobs, int n_jobs, int rows_wg) {
   return g;
 }
 
+// EF_HIP_MFMA_SHAPE=RT,NS,S pins the batched kernel's shape (tuning); 0 fields stay automatic.
+struct MfmaOverride {
+  int RT = 0, NS = 0, S = 0;
+};
+const MfmaOverride& mfma_override() {
+  static const MfmaOverride ov = [] {
+    MfmaOverride o;
+    const char* e = std::getenv("EF_HIP_MFMA_SHAPE");
+    int rt = 0, ns = 0, sp = 0;
+    if (e != nullptr && std::sscanf(e, "%d,%d,%d", &rt, &ns, &sp) == 3) {
+      o.RT = rt;
+      o.NS = ns;
+      o.S = sp;
+    }
+    return o;
+  }();
+  return ov;
+}
+
+// Estimated time (CU cycles) of one shape: per workgroup its matrix-core time plus most of its
+// vector-ALU time (measured on MI355X, the two overlap only partly), or its operand stream if that
+// is longer; times the rounds of workgroups (one resident per CU), against the weights' HBM time;
+// plus the split-K finalize launch and partial-sum traffic.  Per block and 16-row tile: 2 NS
+// products of 16 cycles and about 12 + 4 NS VALU instructions of 4 cycles, over the CU's 4 SIMDs;
+// 2 KB of A operands per sequence tile and the tile-block's weights through the CU's L2 port at
+// ~40 B/cycle.
+double shape_cost(int rt, int nm, int ns, int sg, int groups, int S, int bps, size_t wbytes, size_t part_bytes,
+                  int cus) {
+  const double units = static_cast<double>(rt) * nm * bps;
+  const double mfma = units * 2.0 * ns * 16.0 / 4.0;
+  const double valu = units * (12.0 + 4.0 * ns) * 4.0 / 4.0;
+  const double oper = (2048.0 * ns * bps + units * 300.0) / 40.0;
+  const double wg = std::max(mfma + 0.7 * valu, oper) + 2500.0;
+  const long wgs = static_cast<long>(groups) * S * sg;
+  const double rounds = std::ceil(static_cast<double>(wgs) / cus);
+  const double hbm = static_cast<double>(wbytes) * 2.4e9 / 5.0e12;  // cycles at 2.4 GHz, ~5 TB/s
+  double t = std::max(rounds * wg, hbm + 2500.0);
+  if (S > 1) t += 3600.0 + static_cast<double>(part_bytes) / (20.0 * cus);  // launch + partial traffic
+  return t;
+}
+
 Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
   Plan p;
   if (mfma_gemv_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return p;
   const size_t K = jobs[0].W->cols;
-  if (K % 256 != 0) return p;  // pairs come in 16-byte multiples of 4 for the LDS-DMA row copies
+  if (K % 32 != 0 || K > 65536) return p;
+  size_t wbytes = 0;
   for (int j = 0; j < n_jobs; ++j) {
     if (jobs[j].W->qtype != EF_QTYPE_Q4_0 && jobs[j].W->qtype != EF_QTYPE_Q8_0) return Plan{};
     p.q4 = p.q4 || jobs[j].W->qtype == EF_QTYPE_Q4_0;
     p.q8 = p.q8 || jobs[j].W->qtype == EF_QTYPE_Q8_0;
-    p.max_rb = std::max(p.max_rb, jobs[j].W->row_bytes);
+    wbytes += jobs[j].W->rows * jobs[j].W->row_bytes * (jobs[j].W2 ? 2 : 1);
     if (jobs[j].x != jobs[0].x || (jobs[j].ldx ? jobs[j].ldx : ldx) != (jobs[0].ldx ? jobs[0].ldx : ldx))
       return p;  // one activation matrix per launch
   }
@@ -546,50 +675,92 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   if (reinterpret_cast<uintptr_t>(jobs[0].x) % 16 != 0 || xld % 4 != 0) return p;
   p.nm = epi == kEpiSwiglu ? 2 : 1;
   p.chunk = std::min(batch, kMaxTiles * kSeqTile);
-  p.NT = tiles_for(batch);
-  // Two row tiles halve the fragment re-reads of large batches; SwiGLU already applies every
-  // fragment to two matrices (and a second row tile would not fit in registers).
-  p.RT = p.NT >= 4 && p.nm == 1 ? 2 : 1;
-  const int rows_wg = p.RT * kTileRows;
-  p.groups = groups_for(jobs, n_jobs, rows_wg);
-  // Every workgroup streams the activation fragments of its K range through its CU's L2 port
-  // (B x K x 4 bytes for the whole range).  Split K (one extra, tiny finalize launch) only when
-  // that exceeds 512 KB; splits are multiples of 4 block pairs, at least 8 (one per wave).
-  const int np = static_cast<int>(K / 64);
-  const size_t frag_bytes = static_cast<size_t>(p.chunk) * K * 4;
-  int S = static_cast<int>((frag_bytes + (512u << 10) - 1) / (512u << 10));
-  S = std::max(1, std::min({S, np / 8, 8}));
-  int pps = (np + S - 1) / S;
-  pps = (pps + 3) / 4 * 4;
-  p.S = (np + pps - 1) / pps;
-  p.pps = pps;
-  // Sequence groups: a workgroup takes NTW of the launch's NT sequence tiles, halving NTW (and the
-  // fragment bytes each workgroup streams) until every CU has a workgroup.  A workgroup's time is
-  // mostly its fragment stream, so small row counts (q / o at 64 sequences: 64 workgroups of 32
-  // rows) finish in a fraction of the time on 4x the CUs.
+  p.NT = (p.chunk + kSeqTile - 1) / kSeqTile;
+  const int nb = static_cast<int>(K / 32);
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
-  p.NTW = p.NT;
-  while (p.NTW > 1 && static_cast<long>(p.groups) * p.S * (p.NT / p.NTW) < cus) p.NTW /= 2;
-  p.SG = p.NT / p.NTW;
-  const size_t pb = p.q8 ? 68 : 36;
-  p.row_stride = odd_stride(static_cast<size_t>(pps), pb, p.max_rb);
-  p.w_stride = static_cast<uint32_t>(rows_wg * p.row_stride);
-  p.lds = std::max<size_t>(static_cast<size_t>(p.nm) * p.w_stride,
-                           static_cast<size_t>(kWavesM) * p.NTW * p.RT * p.nm * kWave * 2 * 4);
   const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
-  if (p.lds > lim) return p;
-  // Layout: the A tables, the scales, the split-K partial sums.
-  p.tab = static_cast<size_t>(p.NT) * (K / 32) * kWave * 16;
+  const MfmaOverride& ov = mfma_override();
+  // every instantiated (RT, NS) and split S whose LDS fits, the cheapest by shape_cost (ties: the
+  // first found)
+  bool found = false;
+  const Shape* shapes = p.nm == 2 ? kShapesSwiglu : kShapesStore;
+  const int n_shapes = p.nm == 2 ? static_cast<int>(sizeof(kShapesSwiglu) / sizeof(Shape))
+                                 : static_cast<int>(sizeof(kShapesStore) / sizeof(Shape));
+  for (int si = 0; si < n_shapes; ++si) {
+    const int rt = shapes[si].RT, ns = shapes[si].NS;
+    if ((ov.RT > 0 && rt != ov.RT) || (ov.NS > 0 && ns != ov.NS) || (ns > 1 && p.NT < ns)) continue;
+    const int sg = (p.NT + ns - 1) / ns;
+    const int rows_wg = rt * kTileRows;
+    const int groups = groups_for(jobs, n_jobs, rows_wg);
+    // the workgroup's partial sums of every wave in LDS for the reduction
+    const size_t lds = static_cast<size_t>(kWavesM) * rt * p.nm * ns * kWave * 4 * sizeof(float);
+    if (lds > lim) continue;
+    for (int s_try = 1; s_try <= std::min(32, std::max(1, nb / 8)); ++s_try) {
+      const int bps = (nb + s_try - 1) / s_try;
+      const int S = (nb + bps - 1) / bps;
+      if (S != s_try || (ov.S > 0 && S != ov.S) || bps > kWavesM * kMaxBlocksPerWave) continue;
+      const size_t part = S > 1 ? static_cast<size_t>(groups) * S * p.chunk * rows_wg * p.nm * sizeof(float) : 0;
+      const double c = shape_cost(rt, p.nm, ns, sg, groups, S, bps, wbytes, 2 * part, cus);
+      if (!found || c < p.cost) {
+        found = true;
+        p.cost = c;
+        p.RT = rt;
+        p.NS = ns;
+        p.SG = sg;
+        p.groups = groups;
+        p.S = S;
+        p.bps = bps;
+        p.lds = lds;
+      }
+    }
+  }
+  if (!found) return Plan{};
+  // Layout: the A tables (every sequence tile of the grid, zeros past the batch), the scales, the
+  // split-K partial sums.
+  p.tab = static_cast<size_t>(p.SG) * p.NS * nb * 2 * kWave * 16;
   size_t off = (p.q4 ? p.tab : 0) + (p.q8 ? p.tab : 0) + kMaxTiles * kSeqTile * sizeof(float);
   off = (off + 255) & ~size_t(255);
   p.part_off = off;
-  if (p.S > 1) off += static_cast<size_t>(p.groups) * p.S * p.chunk * rows_wg * p.nm * sizeof(float);
+  if (p.S > 1) off += static_cast<size_t>(p.groups) * p.S * p.chunk * p.RT * kTileRows * p.nm * sizeof(float);
   p.bytes = off;
   p.ok = true;
   return p;
 }
 
 }  // namespace
+
+size_t tiled_bytes(const ef_hip_weight_s* w) {
+  const size_t tiles = (w->rows + kTileRows - 1) / kTileRows, nb = w->cols / 32;
+  return tiles * nb * (w->qtype == EF_QTYPE_Q4_0 ? kTileBlockQ4 : kTileBlockQ8);
+}
+
+int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s) {
+  if (w->tiled != nullptr) return EF_HIP_OK;
+  EFH_CHECK(w->qtype == EF_QTYPE_Q4_0 || w->qtype == EF_QTYPE_Q8_0, "tile layout: packed types only");
+  EFH_CHECK(w->cols % 32 == 0, "tile layout: cols must be a multiple of 32");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  EFH_HIP(hipStreamIsCapturing(s, &st));
+  EFH_CHECK(st == hipStreamCaptureStatusNone,
+            "batched GEMV: the weight's tile-order copy must be made before graph capture (a batched call "
+            "outside capture, or engine creation, makes it)");
+  const size_t bytes = tiled_bytes(w);
+  EFH_CHECK(bytes < (size_t(1) << 32), "tile layout: matrix too large for one buffer resource");
+  uint8_t* out = nullptr;
+  EFH_HIP(hipMalloc(&out, bytes));
+  const size_t tiles = (w->rows + kTileRows - 1) / kTileRows, nb = w->cols / 32;
+  const size_t threads = tiles * nb * kWave;
+  hipLaunchKernelGGL(tile_layout_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s, w->dev,
+                     static_cast<int>(w->rows), static_cast<int>(nb), static_cast<int>(w->row_bytes),
+                     w->qtype == EF_QTYPE_Q4_0 ? 1 : 0, out);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    (void)hipFree(out);
+    return fail_hip(e, "tile_layout_kernel");
+  }
+  w->tiled = out;
+  return EF_HIP_OK;
+}
 
 size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
   const Plan p = plan_mfma(jobs, n_jobs, epi, batch, ldx);
@@ -602,6 +773,10 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
   const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, ldx);
   if (!pl.ok) return EF_HIP_OK;
   if (norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 != 0) return EF_HIP_OK;
+  for (int j = 0; j < n_jobs; ++j) {
+    EFH_RC(ensure_tiled(jobs[j].W, stream));
+    if (jobs[j].W2 != nullptr) EFH_RC(ensure_tiled(jobs[j].W2, stream));
+  }
   const size_t K = jobs[0].W->cols;
   const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
   // workspace: the caller's, else a stream-ordered allocation freed after the launches
@@ -617,14 +792,12 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
   float* post = reinterpret_cast<float*>(base + (pl.q4 ? pl.tab : 0) + (pl.q8 ? pl.tab : 0));
   int rc = EF_HIP_OK;
   MArgs a{};
-  a.row_stride = pl.row_stride;
-  a.w_stride = pl.w_stride;
   a.ksplit = pl.S;
-  a.pairs_per_split = pl.pps;
+  a.blocks_per_split = pl.bps;
   a.part = reinterpret_cast<float*>(base + pl.part_off);
-  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(pl.RT, pl.NTW)
-                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(pl.RT, pl.NTW)
-                                                     : pick_mfma<kEpiSwiglu>(pl.RT, pl.NTW));
+  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore>(pl.RT, pl.NS)
+                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual>(pl.RT, pl.NS)
+                                                     : pick_mfma<kEpiSwiglu>(pl.RT, pl.NS));
   const int rows_wg = pl.RT * kTileRows;
   for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += pl.chunk) {
     const int nb = std::min(pl.chunk, batch - b0);
@@ -638,31 +811,34 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
     p.t4 = t4;
     p.t8 = t8;
     p.post = post;
-    hipLaunchKernelGGL(xfrag_kernel, dim3(kPrepSplit, pl.NT), dim3(kTP), 0, stream, p);  // tiles past B get zeros
+    const int nbk = static_cast<int>(K / 32);
+    hipLaunchKernelGGL(xfrag_kernel, dim3((nbk + kPrepBlocks - 1) / kPrepBlocks, pl.SG * pl.NS), dim3(kTP), 0, stream,
+                       p);  // tiles past B get zeros
     a.n_jobs = n_jobs;
     a.K = static_cast<int>(K);
     a.B = nb;
     a.n_tiles = pl.NT;
     a.t4 = t4;
     a.t8 = t8;
+    a.tab_bytes = static_cast<uint32_t>(pl.tab);
     a.post = post;
     int tiles = 0;
     for (int j = 0; j < n_jobs; ++j) {
       MJob& d = a.job[j];
       const size_t yld = jobs[j].ldy ? jobs[j].ldy : ldy;
-      d.W = jobs[j].W->dev;
-      d.W2 = jobs[j].W2 ? jobs[j].W2->dev : nullptr;
+      d.W = jobs[j].W->tiled;
+      d.W2 = jobs[j].W2 ? jobs[j].W2->tiled : nullptr;
       d.y = jobs[j].y + b0 * yld;
       d.rows = static_cast<int>(jobs[j].W->rows);
       d.qtype = jobs[j].W->qtype;
-      d.row_bytes = static_cast<int>(jobs[j].W->row_bytes);
+      d.bytes = static_cast<uint32_t>(tiled_bytes(jobs[j].W));
       d.ldy = static_cast<long>(yld);
       d.tile_begin = tiles;
       tiles += (d.rows + rows_wg - 1) / rows_wg;
     }
     void* params[] = {&a};
-    // the chunk's sequences cover ceil(nb / 8) tiles; grid rows past them would have no sequences
-    const int sg = std::min(pl.SG, (nb + pl.NTW * kSeqTile - 1) / (pl.NTW * kSeqTile));
+    // the chunk's sequences cover ceil(nb / 16) tiles; grid rows past them would have no sequences
+    const int sg = std::min(pl.SG, (nb + pl.NS * kSeqTile - 1) / (pl.NS * kSeqTile));
     hipError_t e = hipLaunchKernel(fn, dim3(tiles * pl.S, sg), dim3(kT), params, pl.lds, stream);
     if (e != hipSuccess) {
       rc = fail_hip(e, "gemv_mfma_kernel");
