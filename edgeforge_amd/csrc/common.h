@@ -2,6 +2,8 @@
 // small device helpers used by several kernels.  gfx950 (MI355X) only: wave64, 160 KB LDS per CU.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -104,6 +106,59 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
+}
+
+// Cross-lane sums on the data-parallel-primitive (DPP) paths: a VALU operand modifier, where a
+// __shfl_xor is an LDS permute with its round trip.  gfx9 DPP controls: quad_perm [1,0,3,2] (0xB1)
+// and [2,3,0,1] (0x4E), row_mirror (0x140), row_half_mirror (0x141), row_bcast:15 (0x142) and
+// row_bcast:31 (0x143); a row is 16 lanes, lanes outside row_mask read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_d(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b & 0xFFFFFFFFu), CTRL, ROW_MASK, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), CTRL, ROW_MASK, 0xF, false);
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(static_cast<unsigned>(hi)) << 32) |
+                                                     static_cast<unsigned>(lo)));
+}
+
+// Sum over aligned groups of G lanes (G = 8, 16 or 32).  G = 8, 16: every lane of a group holds
+// its sum; G = 32: lanes 16..31 of each half-wave do.  Lane G - 1 of a group always does.
+template <int G, typename T>
+__device__ __forceinline__ T group_sum_dpp(T v) {
+  auto mv = [](T x, auto ctrl) {
+    if constexpr (sizeof(T) == 8) {
+      return dpp_d<decltype(ctrl)::value>(x);
+    } else {
+      return dpp_f<decltype(ctrl)::value>(x);
+    }
+  };
+  v = v + mv(v, std::integral_constant<int, 0xB1>{});
+  v = v + mv(v, std::integral_constant<int, 0x4E>{});
+  v = v + mv(v, std::integral_constant<int, 0x141>{});
+  if constexpr (G >= 16) v = v + mv(v, std::integral_constant<int, 0x140>{});
+  if constexpr (G >= 32) {
+    if constexpr (sizeof(T) == 8) {
+      v = v + dpp_d<0x142, 0xA>(v);
+    } else {
+      v = v + dpp_f<0x142, 0xA>(v);
+    }
+  }
+  return v;
+}
+
+// Wave-wide double sum through DPP, returned on every lane (lane 63 holds it, then a broadcast).
+__device__ __forceinline__ double wave_sum_d_dpp(double v) {
+  v = group_sum_dpp<32>(v);
+  v = v + dpp_d<0x143, 0xC>(v);
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = __builtin_amdgcn_readlane(static_cast<int>(b & 0xFFFFFFFFu), 63);
+  const unsigned hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), 63);
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
 }  // namespace efh

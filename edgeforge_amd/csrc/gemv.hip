@@ -87,10 +87,7 @@ __device__ __forceinline__ void store_x4(float4 v, int i, float* lds_x, float* l
   *reinterpret_cast<float4*>(lds_x + (i >> 6) * kSlot + (i & 63)) = v;
   // K % 32 == 0, so the 8 threads of a block are active together and the xor partners stay
   // inside the aligned group of 8.
-  float s = (v.x + v.y) + (v.z + v.w);
-  s += __shfl_xor(s, 1, kWave);
-  s += __shfl_xor(s, 2, kWave);
-  s += __shfl_xor(s, 4, kWave);
+  const float s = group_sum_dpp<8>((v.x + v.y) + (v.z + v.w));
   if ((threadIdx.x & 7) == 0) lds_xs[i >> 5] = s;
 }
 
@@ -122,7 +119,7 @@ __device__ void xload_finish(const float* __restrict__ x, const float* __restric
       if (i < K) ss += sq_d(r.x[k]);
     }
     for (int i = threadIdx.x * 4 + kReg; i < K; i += kThreads * 4) ss += sq_d(*reinterpret_cast<const float4*>(x + i));
-    ss = wave_sum_d(ss);
+    ss = wave_sum_d_dpp(ss);
     if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
     __syncthreads();
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
@@ -315,11 +312,8 @@ __device__ __forceinline__ void pairs_body(const Args& a, const JobDev& jb, int 
     }
   }
 #pragma unroll
-  for (int r = 0; r < RR; ++r) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, kWave);
-  }
-  if (t != 0 || nvalid <= 0) return;
+  for (int r = 0; r < RR; ++r) acc[r] = group_sum_dpp<G>(acc[r]);
+  if (t != G - 1 || nvalid <= 0) return;  // lane G - 1 holds the group's sums
   float* y = jb.y + b * jb.ldy + row0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -394,6 +388,30 @@ __device__ __forceinline__ float4 lds_read4(const float* p) {
   f4n v;
   asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
   return make_float4(v.x, v.y, v.z, v.w);
+}
+// Two 16-byte LDS reads issued together, one wait for both.
+__device__ __forceinline__ void lds_read4x2(const float* p0, const float* p1, float4& v0, float4& v1) {
+  f4n a, b;
+  asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(a), "=&v"(b)
+               : "v"(lds_off(p0)), "v"(lds_off(p1))
+               : "memory");
+  v0 = make_float4(a.x, a.y, a.z, a.w);
+  v1 = make_float4(b.x, b.y, b.z, b.w);
+}
+__device__ __forceinline__ void lds_read4x4(const float* p0, const float* p1, const float* p2, const float* p3,
+                                            float4& v0, float4& v1, float4& v2, float4& v3) {
+  f4n a, b, c, d;
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+      : "v"(lds_off(p0)), "v"(lds_off(p1)), "v"(lds_off(p2)), "v"(lds_off(p3))
+      : "memory");
+  v0 = make_float4(a.x, a.y, a.z, a.w);
+  v1 = make_float4(b.x, b.y, b.z, b.w);
+  v2 = make_float4(c.x, c.y, c.z, c.w);
+  v3 = make_float4(d.x, d.y, d.z, d.w);
 }
 __device__ __forceinline__ void lds_write4(float* p, float4 v) {
   const f4n w = {v.x, v.y, v.z, v.w};
@@ -505,30 +523,53 @@ __global__ __launch_bounds__(NW * kWave) void gemv_dma_kernel(Args a) {
   // weight rows too)
   asm volatile("s_barrier" ::: "memory");
 
-  // 2. normalise x into the padded slots (+ block sums), while the weight rows are in flight
+  // 2. normalise x into the padded slots (+ block sums), while the weight rows are in flight.
+  //    K <= 8 NT (every float4 of x in two per thread, read once): x and the norm weights come in
+  //    one batch of LDS reads and stay in registers; longer rows loop.
   {
-    float inv = 1.0f;
-    if (a.norm_w != nullptr) {
-      double ss = 0.0;
-      for (int i = threadIdx.x * 4; i < K; i += NT * 4) ss += sq_d(lds_read4(raw_x + i));
-      ss = wave_sum_d(ss);
+    // K % 32 == 0: the 8 threads of a block are active together, the group sum stays inside
+    auto put = [&](int i, float4 v) {
+      lds_write4(lds_x + (i >> 6) * kSlot + (i & 63), v);
+      const float bs = group_sum_dpp<8>((v.x + v.y) + (v.z + v.w));
+      if ((threadIdx.x & 7) == 0) lds_write1(lds_xs + (i >> 5), bs);
+    };
+    auto norm_inv = [&](double ss) -> float {
+      ss = wave_sum_d_dpp(ss);
       if (lane == 0) red[wave] = ss;
       lds_barrier();
       double tot = 0.0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) tot += red[w];  // waves in order
-      inv = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)));
-    }
-    for (int i = threadIdx.x * 4; i < K; i += NT * 4) {
-      float4 v = lds_read4(raw_x + i);
-      if (a.norm_w != nullptr) v = norm4(v, lds_read4(raw_nw + i), inv);
-      lds_write4(lds_x + (i >> 6) * kSlot + (i & 63), v);
-      // K % 32 == 0: the 8 threads of a block are active together, xor partners stay in the group
-      float bs = (v.x + v.y) + (v.z + v.w);
-      bs += __shfl_xor(bs, 1, kWave);
-      bs += __shfl_xor(bs, 2, kWave);
-      bs += __shfl_xor(bs, 4, kWave);
-      if ((threadIdx.x & 7) == 0) lds_write1(lds_xs + (i >> 5), bs);
+      return static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)));
+    };
+    if (K <= 2 * NT * 4) {
+      const int i0 = threadIdx.x * 4, i1 = i0 + NT * 4;
+      const bool h0 = i0 < K, h1 = i1 < K;
+      const int j0 = h0 ? i0 : 0, j1 = h1 ? i1 : 0;  // in-range addresses for idle threads
+      float4 x0, x1;
+      if (a.norm_w != nullptr) {
+        float4 w0, w1;
+        lds_read4x4(raw_x + j0, raw_x + j1, raw_nw + j0, raw_nw + j1, x0, x1, w0, w1);
+        const float inv = norm_inv((h0 ? sq_d(x0) : 0.0) + (h1 ? sq_d(x1) : 0.0));
+        x0 = norm4(x0, w0, inv);
+        x1 = norm4(x1, w1, inv);
+      } else {
+        lds_read4x2(raw_x + j0, raw_x + j1, x0, x1);
+      }
+      if (h0) put(i0, x0);
+      if (h1) put(i1, x1);
+    } else {
+      float inv = 1.0f;
+      if (a.norm_w != nullptr) {
+        double ss = 0.0;
+        for (int i = threadIdx.x * 4; i < K; i += NT * 4) ss += sq_d(lds_read4(raw_x + i));
+        inv = norm_inv(ss);
+      }
+      for (int i = threadIdx.x * 4; i < K; i += NT * 4) {
+        float4 v = lds_read4(raw_x + i);
+        if (a.norm_w != nullptr) v = norm4(v, lds_read4(raw_nw + i), inv);
+        put(i, v);
+      }
     }
     __syncthreads();
   }
@@ -545,11 +586,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_dma_kernel(Args a) {
     dma_body<EF_QTYPE_Q8_0, EPI, G, R>(lds_x, lds_xs, wl, a.w_stride, np, static_cast<int>(rb), t, grp, acc);
   }
 #pragma unroll
-  for (int r = 0; r < RR; ++r) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, kWave);
-  }
-  if (t != 0 || nvalid <= 0) return;
+  for (int r = 0; r < RR; ++r) acc[r] = group_sum_dpp<G>(acc[r]);
+  if (t != G - 1 || nvalid <= 0) return;  // lane G - 1 holds the group's sums
   float* y = jb.y + b * jb.ldy + row0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
