@@ -151,6 +151,24 @@ __device__ __forceinline__ T group_sum_dpp(T v) {
   return v;
 }
 
+// Wave-wide float max through DPP, returned on every lane.  Lanes a DPP step does not feed keep
+// their own value (max with itself), so negative values are safe.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_self_f(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_self_f<0xB1>(v));
+  v = fmaxf(v, dpp_self_f<0x4E>(v));
+  v = fmaxf(v, dpp_self_f<0x141>(v));
+  v = fmaxf(v, dpp_self_f<0x140>(v));
+  v = fmaxf(v, dpp_self_f<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_self_f<0x143, 0xC>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Wave-wide double sum through DPP, returned on every lane (lane 63 holds it, then a broadcast).
 __device__ __forceinline__ double wave_sum_d_dpp(double v) {
   v = group_sum_dpp<32>(v);

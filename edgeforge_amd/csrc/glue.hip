@@ -94,8 +94,8 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
       if (sub == 0)
         for (; i < hd; ++i) a0 += qs[i] * kt[i];  // dot_f32's tail joins partial 0
       float s = a0 + a1;                           // (acc[2s] + acc[2s+1])
-      s = s + __shfl_xor(s, 1, kWave);             // (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
-      s = s + __shfl_xor(s, 2, kWave);             // the two halves, low half first on lane 0
+      s = s + dpp_f<0xB1>(s);  // lane ^ 1 (DPP quad_perm): (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
+      s = s + dpp_f<0x4E>(s);  // lane ^ 2: the two halves, low half first on lane 0
       if (sub == 0) sc[c0 + quad] = s * scale;
     }
     __syncthreads();
@@ -103,7 +103,7 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
   // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
   float mx = -INFINITY;
   for (int tp = t; tp < n_pos; tp += blockDim.x) mx = fmaxf(mx, sc[tp]);
-  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  mx = wave_max_dpp(mx);
   if ((t & (kWave - 1)) == 0) red[t / kWave] = mx;
   __syncthreads();
   mx = static_cast<float>(red[0]);
@@ -115,7 +115,7 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
     sc[tp] = e;
     s += static_cast<double>(e);
   }
-  s = wave_sum_d(s);
+  s = wave_sum_d_dpp(s);
   if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
   __syncthreads();
   double tot = 0.0;
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const float* xb = x + blockIdx.x * ld;
   double ss = 0.0;
   for (int i = threadIdx.x; i < n; i += blockDim.x) ss += static_cast<double>(xb[i]) * static_cast<double>(xb[i]);
-  ss = wave_sum_d(ss);
+  ss = wave_sum_d_dpp(ss);
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
   __syncthreads();
   const double tot = (red[0] + red[1]) + (red[2] + red[3]);
