@@ -113,7 +113,6 @@ __device__ __forceinline__ void dma_copy(__amdgpu_buffer_rsrc_t r, uint32_t src_
 }
 
 __device__ __forceinline__ float f16lo(uint32_t v) { return half_bits_to_float(v & 0xFFFFu); }
-__device__ __forceinline__ float f16hi(uint32_t v) { return half_bits_to_float(v >> 16); }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 

@@ -18,6 +18,7 @@ struct AttnArgs {
   long ldq;
   int H, KV, hd, max_seq;
   float scale;          // float(1 / sqrt(hd))
+  int pre_vrows;        // set by launch_attention: the first chunk's V rows have their own LDS
 };
 
 // Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of

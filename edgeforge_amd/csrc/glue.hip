@@ -9,6 +9,8 @@
 // over positions in order (:168-172).
 #include <cmath>
 
+#include <utility>
+
 #include "glue.h"
 
 #pragma clang fp contract(off)
@@ -69,19 +71,49 @@ __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long 
   }
 }
 
+// The decode kernel requests the first chunk's cached K and V rows (thread t: float4 slots
+// t + kAttnThreads j, row slot / (hd / 4)) before its q / k / v work, so their latency overlaps it,
+// and stages them in LDS with the new row at `pos` once that is formed.  kPreSlots covers hd <= 128.
+constexpr int kPreSlots = 8;
+typedef float pre_f4 __attribute__((ext_vector_type(4)));
+struct PreSlots {
+  pre_f4 s0, s1, s2, s3, s4, s5, s6, s7;
+  template <int J>
+  __device__ __forceinline__ pre_f4& at() {
+    if constexpr (J == 0) return s0;
+    else if constexpr (J == 1) return s1;
+    else if constexpr (J == 2) return s2;
+    else if constexpr (J == 3) return s3;
+    else if constexpr (J == 4) return s4;
+    else if constexpr (J == 5) return s5;
+    else if constexpr (J == 6) return s6;
+    else return s7;
+  }
+};
+template <typename F, int... J>
+__device__ __forceinline__ void for_slots_impl(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <typename F>
+__device__ __forceinline__ void for_slots(F&& f) {
+  for_slots_impl(f, std::make_integer_sequence<int, kPreSlots>{});
+}
+
 // Causal attention of one (query head, row) over positions 0 .. n_pos-1 of one KV head: scores in
 // kern::dot_f32's order, softmax_inplace, then p.v in position order (src/kernels.cpp:153-174).
 // qs (roped query) is in LDS; K and V rows come from the cache except position `cur`, which is
 // taken from kn / vn (the decode step's new row; cur = -1 when every row is in the cache).
+// With USE_PRE the first chunk is already staged: its K rows in `rows`, its V rows in `vrows`.
+template <bool USE_PRE>
 __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, double* red, const float* kc,
                                        const float* vc, long kvd, const float* kn, const float* vn, int cur,
-                                       int n_pos, int hd, float scale, float* out) {
+                                       int n_pos, int hd, float scale, float* out, const float* vrows) {
   const int t = threadIdx.x;
   // scores
   const int quad = t >> 2, sub = t & 3;
   for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
     const int n = min(kAttnChunk, n_pos - c0);
-    stage_rows(rows, kc, kvd, kn, cur, c0, n, hd);
+    if (!USE_PRE || c0 > 0) stage_rows(rows, kc, kvd, kn, cur, c0, n, hd);
     __syncthreads();
     if (quad < n) {
       const float* kt = rows + quad * hd;
@@ -125,12 +157,17 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
   float o = 0.0f;
   for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
     const int n = min(kAttnChunk, n_pos - c0);
-    stage_rows(rows, vc, kvd, vn, cur, c0, n, hd);
+    const float* vr = rows;
+    if (USE_PRE && c0 == 0) {
+      vr = vrows;
+    } else {
+      stage_rows(rows, vc, kvd, vn, cur, c0, n, hd);
+    }
     __syncthreads();
     if (t < hd) {
       for (int r = 0; r < n; ++r) {
         const float p = sc[c0 + r] * inv;
-        o += p * rows[r * hd + t];
+        o += p * vr[r * hd + t];
       }
     }
     __syncthreads();
@@ -139,6 +176,7 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
 }
 
 
+template <bool PRE>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   const int h = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
@@ -158,6 +196,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   const float* kc = a.kcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;  // this layer, sequence, head
   const float* vc = a.vcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;
   const int t = threadIdx.x;
+  // the first chunk's cached K / V rows are requested before the q / k / v work below
+  const bool pre = PRE && hd * kAttnChunk <= 4 * kPreSlots * kAttnThreads && a.pre_vrows;
+  const int n0 = min(kAttnChunk, n_pos), q4n = hd / 4;
+  // one register pair per slot (separate variables: an indexed array would live in scratch)
+  PreSlots pk, pv;
+  if (pre) {
+    for_slots([&](auto J) {
+      const int idx = t + kAttnThreads * decltype(J)::value, r = idx / q4n, c = idx - r * q4n;
+      if (r < n0 && r != pos) {
+        pk.template at<decltype(J)::value>() = reinterpret_cast<const pre_f4*>(kc + static_cast<long>(r) * kvd)[c];
+        pv.template at<decltype(J)::value>() = reinterpret_cast<const pre_f4*>(vc + static_cast<long>(r) * kvd)[c];
+      }
+    });
+  }
   if (t < half) {
     const float qa = q[t], qb = q[t + half], ka = k_new[t], kb = k_new[t + half];
     qs[t] = qa * cr[t] - qb * sr[t];
@@ -175,8 +227,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
       vw[i] = vn[i];
     }
   }
-  attend(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
-         a.ctx + static_cast<long>(b) * a.ldq + h * hd);
+  if (pre) {
+    float* vrows = sc + ((a.max_seq + 1) & ~1) + 8;  // after the reduction slots (4 doubles)
+    for_slots([&](auto J) {
+      const int idx = t + kAttnThreads * decltype(J)::value, r = idx / q4n, c = idx - r * q4n;
+      if (r < n0) {
+        reinterpret_cast<pre_f4*>(rows + r * hd)[c] =
+            r == pos ? reinterpret_cast<const pre_f4*>(kn)[c] : pk.template at<decltype(J)::value>();
+        reinterpret_cast<pre_f4*>(vrows + r * hd)[c] =
+            r == pos ? reinterpret_cast<const pre_f4*>(vn)[c] : pv.template at<decltype(J)::value>();
+      }
+    });
+    attend<true>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
+                 a.ctx + static_cast<long>(b) * a.ldq + h * hd, vrows);
+  } else {
+    attend<false>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
+                  a.ctx + static_cast<long>(b) * a.ldq + h * hd, nullptr);
+  }
 }
 
 // Prefill, step 1: every row r = (sequence b, chunk index i) at position p = *pos_dev + i gets RoPE
@@ -222,8 +289,8 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(Prefill
   __syncthreads();
   const float* kc = a.a.kcache + (static_cast<long>(b) * a.a.max_seq) * kvd + g * hd;
   const float* vc = a.a.vcache + (static_cast<long>(b) * a.a.max_seq) * kvd + g * hd;
-  attend(qs, rows, sc, red, kc, vc, kvd, nullptr, nullptr, -1, p + 1, hd, a.a.scale,
-         a.a.ctx + static_cast<long>(r) * a.a.ldq + h * hd);
+  attend<false>(qs, rows, sc, red, kc, vc, kvd, nullptr, nullptr, -1, p + 1, hd, a.a.scale,
+                a.a.ctx + static_cast<long>(r) * a.a.ldq + h * hd, nullptr);
 }
 
 // x[r] = row hist[b][*pos_dev + i] of the embedding table for every prefill row r = (b, i).
@@ -319,8 +386,21 @@ int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s) {
 }
 
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
-  const size_t lds = attention_lds_bytes(a.hd, a.max_seq);
-  hipLaunchKernelGGL(attention_kernel, dim3(a.H, batch), dim3(kAttnThreads), lds, s, a);
+  // With few workgroups (latency-bound: a small batch) the decode kernel prefetches the first
+  // chunk's K / V rows and stages the V rows in a second LDS buffer when it fits; with many, the
+  // lighter kernel keeps more workgroups resident.
+  AttnArgs b = a;
+  size_t lds = attention_lds_bytes(a.hd, a.max_seq);
+  const size_t vrows = static_cast<size_t>(kAttnChunk) * a.hd * sizeof(float);
+  const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
+  const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
+  b.pre_vrows = lds + vrows <= lim && static_cast<long>(a.H) * batch <= 2L * cus ? 1 : 0;
+  if (b.pre_vrows) {
+    lds += vrows;
+    hipLaunchKernelGGL(attention_kernel<true>, dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+  } else {
+    hipLaunchKernelGGL(attention_kernel<false>, dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+  }
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }
