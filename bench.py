@@ -163,6 +163,9 @@ def main() -> int:
     ap.add_argument("--only-kernel", action="store_true",
                     help="profiling mode: a 256 MiB device copy (counter calibration), then only the rotating "
                          "gate/up GEMV launches; prints their average time")
+    ap.add_argument("--only-batched", action="store_true",
+                    help="profiling mode: only the B=64 Q4_0 5632x2048 matvec launches (fragment preparation + "
+                         "matrix-core GEMV) over rotating replicas; prints their average time")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -189,6 +192,10 @@ def main() -> int:
         avg_ms, nbytes, reps = profile_gate_up(H, L, model, batch=1)
         print(json.dumps({"copy_bytes": n, "gate_up_avg_us": round(avg_ms * 1e3, 3), "bytes_per_launch": nbytes,
                           "replicas": reps}), flush=True)
+        return 0
+    if args.only_batched:
+        ms, nbytes = profile_plain(H, L, model, (1, "w_gate"), L.Q4_0, 18, batch=64, launches=200)
+        print(json.dumps({"q4_0_5632x2048_b64_us": round(ms * 1e3, 3), "bytes_per_launch": nbytes}), flush=True)
         return 0
     rng = np.random.default_rng(23)
     prompt = rng.integers(0, TINYLLAMA.V, 23).astype(np.int32)

@@ -166,34 +166,71 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
   const int K = a.K, tile = blockIdx.y, nb = K >> 5;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const bool has_norm = a.norm_w != nullptr;
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 4u;
+  // Every load below goes through a buffer resource (zeros past its end: sequences past the batch,
+  // a missing norm, blocks past K) and is issued before any of them is used, so the kernel waits on
+  // memory about once instead of once per load.
+  // 2a. this wave's fragment inputs: block kb, lane l = sequence l % 16 and k group l / 16; both
+  //     column orders (Q4_0: weights 4g..4g+3 and 4g+16..4g+19 of the block, Q8_0: 8g..8g+7)
+  const int kb = blockIdx.x * kPrepBlocks + wave;
+  const int i = lane & 15, g = lane >> 4, sq_f = tile * kSeqTile + i;
+  // one resource over the chunk's rows (B * ldx floats, < 16 MiB); a lane of a sequence past the
+  // batch, or of a block past K, addresses the resource's end and reads zeros
+  const uint32_t x_bytes = static_cast<uint32_t>(a.B) * static_cast<uint32_t>(a.ldx) * 4u;
+  const __amdgpu_buffer_rsrc_t rx_all = make_rsrc(a.x, x_bytes);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, has_norm ? row_bytes : 0u);
+  const bool frag_live = sq_f < a.B && kb < nb;
+  const uint32_t kf = static_cast<uint32_t>(kb) * 128u;  // byte offset of the block in a row
+  const uint32_t row0 = static_cast<uint32_t>(sq_f) * static_cast<uint32_t>(a.ldx) * 4u;
+  const uint32_t o4[2] = {kf + 16u * g, kf + 64u + 16u * g}, o8[2] = {kf + 32u * g, kf + 32u * g + 16u};
+  // the first table's inputs now (Q4_0's when present); a launch with both tables loads the Q8_0
+  // order's after the statistics
+  const bool q4_first = a.t4 != nullptr;
+  float4 fx[2], fw[2];
+  auto load_frag = [&](const uint32_t (&o)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      fx[h] = buf_f4(rx_all, frag_live ? row0 + o[h] : x_bytes);
+      fw[h] = buf_f4(rw, kb < nb ? o[h] : row_bytes);
+    }
+  };
+  load_frag(q4_first ? o4 : o8);
   // 1. per-sequence sum of squares (double, kern::rmsnorm) and max |x| (wave s reduces sequence
-  //    s), and max |norm weight| (every thread)
+  //    s), and max |norm weight| (every thread), 8 loads in flight per lane
   {
-    const int sq = tile * kSeqTile + wave;
+    const int sq = tile * kSeqTile + __builtin_amdgcn_readfirstlane(wave);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (sq < a.B ? sq : 0) * a.ldx, sq < a.B ? row_bytes : 0u);
     double ss = 0.0;
     float ax = 0.0f, aw = 0.0f;
-    if (sq < a.B) {
-      const float* xr = a.x + sq * a.ldx;
-      for (int k = lane * 4; k < K; k += kWave * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(xr + k);
-        ss += static_cast<double>(v.x) * static_cast<double>(v.x);
-        ss += static_cast<double>(v.y) * static_cast<double>(v.y);
-        ss += static_cast<double>(v.z) * static_cast<double>(v.z);
-        ss += static_cast<double>(v.w) * static_cast<double>(v.w);
-        ax = fmaxf(ax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    // the norm weights' first 8192 values are requested with the rows (zeros without a norm)
+    const float4 wn0 = buf_f4(rw, threadIdx.x * 16u), wn1 = buf_f4(rw, (kTP + threadIdx.x) * 16u);
+    constexpr int kU = 8;
+    for (uint32_t base = 0; base < row_bytes; base += kU * kWave * 16u) {
+      float4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = buf_f4(rx, base + (u * kWave + lane) * 16u);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        ss += static_cast<double>(v[u].x) * static_cast<double>(v[u].x);
+        ss += static_cast<double>(v[u].y) * static_cast<double>(v[u].y);
+        ss += static_cast<double>(v[u].z) * static_cast<double>(v[u].z);
+        ss += static_cast<double>(v[u].w) * static_cast<double>(v[u].w);
+        ax = fmaxf(ax, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
       }
     }
+    aw = fmaxf(fmaxf(fmaxf(fabsf(wn0.x), fabsf(wn0.y)), fmaxf(fabsf(wn0.z), fabsf(wn0.w))),
+               fmaxf(fmaxf(fabsf(wn1.x), fabsf(wn1.y)), fmaxf(fabsf(wn1.z), fabsf(wn1.w))));
     if (has_norm) {
-      for (int k = threadIdx.x * 4; k < K; k += kTP * 4) {
-        const float4 w = *reinterpret_cast<const float4*>(a.norm_w + k);
-        aw = fmaxf(aw, fmaxf(fmaxf(fabsf(w.x), fabsf(w.y)), fmaxf(fabsf(w.z), fabsf(w.w))));
+      for (uint32_t base = 2 * kTP * 16u; base < row_bytes; base += 2 * kTP * 16u) {
+        const float4 w0 = buf_f4(rw, base + threadIdx.x * 16u);
+        const float4 w1 = buf_f4(rw, base + (kTP + threadIdx.x) * 16u);
+        aw = fmaxf(aw, fmaxf(fmaxf(fabsf(w0.x), fabsf(w0.y)), fmaxf(fabsf(w0.z), fabsf(w0.w))));
+        aw = fmaxf(aw, fmaxf(fmaxf(fabsf(w1.x), fabsf(w1.y)), fmaxf(fabsf(w1.z), fabsf(w1.w))));
       }
     }
-    ss = wave_sum_d(ss);
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-      ax = fmaxf(ax, __shfl_xor(ax, o, kWave));
-      aw = fmaxf(aw, __shfl_xor(aw, o, kWave));
-    }
+    ss = wave_sum_d_dpp(ss);
+    ax = wave_max_dpp(ax);
+    aw = wave_max_dpp(aw);
     if (lane == 0) {
       s_ss[wave] = ss;
       s_ax[wave] = ax;
@@ -218,21 +255,16 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
     if (blockIdx.x == 0 && sq < a.B) a.post[sq] = ldexpf(1.0f, e);
   }
   __syncthreads();
-  // 2. fragments: wave w writes block 16 x + w, lane l the 8 values of sequence l % 16 and k group
-  //    l / 16, hi and lo.  The 8 values of a Q4_0 fragment are weights 4g..4g+3 and 4g+16..4g+19
-  //    of the block, of a Q8_0 fragment 8g..8g+7: two float4 each.
-  const int kb = blockIdx.x * kPrepBlocks + wave;
+  // 2b. fragments: wave w writes block 16 x + w, lane l the 8 values of sequence l % 16 and k group
+  //     l / 16, hi and lo
   if (kb >= nb) return;
-  const int i = lane & 15, g = lane >> 4, sq = tile * kSeqTile + i;
-  const bool live = sq < a.B;
   const float inv = s_mul[i], pre = s_pre[i];
-  const float* xr = a.x + (live ? sq : 0) * a.ldx;
-  auto frag = [&](const int (&k0)[2], float (&out)[8]) {
+  auto frag = [&](float (&out)[8]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      float4 v = live ? *reinterpret_cast<const float4*>(xr + k0[h]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 v = fx[h];
       if (has_norm) {  // HF order: w * (x * inv)
-        const float4 w = *reinterpret_cast<const float4*>(a.norm_w + k0[h]);
+        const float4 w = fw[h];
         v.x = w.x * (v.x * inv);
         v.y = w.y * (v.y * inv);
         v.z = w.z * (v.z * inv);
@@ -261,17 +293,16 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
     *reinterpret_cast<h8*>(f + kWave * 16) = lo;
   };
   if (a.t4 != nullptr) {  // slots 0..7 = weights 4g + {0, 2, 16, 18, 1, 3, 17, 19}
-    const int k0[2] = {kb * 32 + 4 * g, kb * 32 + 16 + 4 * g};
     float xv[8];
-    frag(k0, xv);
+    frag(xv);
     constexpr int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
     constexpr bool q16[8] = {false, false, true, true, false, false, true, true};
     store(a.t4, xv, ord, q16);
   }
   if (a.t8 != nullptr) {  // slots 0..7 = weights 8g + {0, 2, 1, 3, 4, 6, 5, 7}
-    const int k0[2] = {kb * 32 + 8 * g, kb * 32 + 8 * g + 4};
+    if (q4_first) load_frag(o8);
     float xv[8];
-    frag(k0, xv);
+    frag(xv);
     constexpr int ord[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     constexpr bool q16[8] = {false, false, false, false, false, false, false, false};
     store(a.t8, xv, ord, q16);
