@@ -8,6 +8,8 @@
 // the max, uses float exp and a double sum (:77-92), and each output dimension accumulates p * v
 // over positions in order (:168-172).
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 #include <utility>
 
@@ -54,11 +56,38 @@ __global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long r
 // src/kernels.cpp:133-146), the new k / v written into the cache at pos by the first head of each
 // KV group, then causal attention over positions 0..pos (positions < pos from the cache, pos from
 // LDS, so no head waits on another).  K and V rows are staged through LDS in chunks of kAttnChunk
-// positions with coalesced float4 loads.  Scores use four lanes per position: lane s of a
-// quad accumulates the dot_f32 partials 2s and 2s+1 (kern::dot_f32's eight partials, i % 8), and
-// two shuffles finish the reference's pairwise tree exactly.  P.V keeps the reference's order: one
-// thread per output dimension accumulates positions in increasing order.
-constexpr int kAttnChunk = kAttnThreads / 4;
+// positions with coalesced float4 loads, each row at a stride of hd + 4 floats so that the lanes
+// of a wave reading 16-byte pieces of different rows hit different banks.  A score is one thread's
+// dot product with kern::dot_f32's eight partials (i % 8) and its pairwise tree.  P.V keeps the
+// reference's order: one thread per output dimension accumulates positions in increasing order.
+constexpr int kAttnChunk = 64;
+
+__host__ __device__ constexpr int row_ld(int hd) { return hd + 4; }  // floats between staged rows
+// Per-head kernel LDS after the scores: 4 reduction doubles, then (with the first-chunk prefetch)
+// the first chunk's V rows at this float offset from the scores, a multiple of 4.
+__host__ __device__ constexpr int vrows_offset(int max_seq) { return (((max_seq + 1) & ~1) + 8 + 3) & ~3; }
+
+// q . k over hd values (both in LDS, 16-byte aligned) in kern::dot_f32's order: partial j sums the
+// products i = j mod 8 in increasing i, a tail joins partial 0, then
+// ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)) (src/kernels.cpp:27-43).
+__device__ __forceinline__ float dot_f32_lds(const float* qv, const float* kv, int hd) {
+  float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
+  int i = 0;
+  for (; i + 8 <= hd; i += 8) {
+    const float4 qa = *reinterpret_cast<const float4*>(qv + i), qb = *reinterpret_cast<const float4*>(qv + i + 4);
+    const float4 ka = *reinterpret_cast<const float4*>(kv + i), kb = *reinterpret_cast<const float4*>(kv + i + 4);
+    p0 += qa.x * ka.x;
+    p1 += qa.y * ka.y;
+    p2 += qa.z * ka.z;
+    p3 += qa.w * ka.w;
+    p4 += qb.x * kb.x;
+    p5 += qb.y * kb.y;
+    p6 += qb.z * kb.z;
+    p7 += qb.w * kb.w;
+  }
+  for (; i < hd; ++i) p0 += qv[i] * kv[i];
+  return ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7));
+}
 
 __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long kvd, const float* cur, int pos,
                                            int c0, int n, int hd) {
@@ -67,7 +96,7 @@ __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long 
   for (int idx = threadIdx.x; idx < n * q; idx += blockDim.x) {
     const int r = idx / q, c = idx - r * q, tp = c0 + r;
     const float* src = tp == pos ? cur : cache + static_cast<long>(tp) * kvd;
-    reinterpret_cast<float4*>(dst + r * hd)[c] = reinterpret_cast<const float4*>(src)[c];
+    reinterpret_cast<float4*>(dst + r * row_ld(hd))[c] = reinterpret_cast<const float4*>(src)[c];
   }
 }
 
@@ -108,28 +137,13 @@ template <bool USE_PRE>
 __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, double* red, const float* kc,
                                        const float* vc, long kvd, const float* kn, const float* vn, int cur,
                                        int n_pos, int hd, float scale, float* out, const float* vrows) {
-  const int t = threadIdx.x;
-  // scores
-  const int quad = t >> 2, sub = t & 3;
+  const int t = threadIdx.x, ld = row_ld(hd);
+  // scores: one thread per position of the chunk
   for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
     const int n = min(kAttnChunk, n_pos - c0);
     if (!USE_PRE || c0 > 0) stage_rows(rows, kc, kvd, kn, cur, c0, n, hd);
     __syncthreads();
-    if (quad < n) {
-      const float* kt = rows + quad * hd;
-      float a0 = 0.0f, a1 = 0.0f;
-      int i = 0;
-      for (; i + 8 <= hd; i += 8) {
-        a0 += qs[i + 2 * sub] * kt[i + 2 * sub];
-        a1 += qs[i + 2 * sub + 1] * kt[i + 2 * sub + 1];
-      }
-      if (sub == 0)
-        for (; i < hd; ++i) a0 += qs[i] * kt[i];  // dot_f32's tail joins partial 0
-      float s = a0 + a1;                           // (acc[2s] + acc[2s+1])
-      s = s + dpp_f<0xB1>(s);  // lane ^ 1 (DPP quad_perm): (a0+a1)+(a2+a3) and (a4+a5)+(a6+a7)
-      s = s + dpp_f<0x4E>(s);  // lane ^ 2: the two halves, low half first on lane 0
-      if (sub == 0) sc[c0 + quad] = s * scale;
-    }
+    if (t < n) sc[c0 + t] = dot_f32_lds(qs, rows + t * ld, hd) * scale;
     __syncthreads();
   }
   // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
@@ -167,7 +181,7 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
     if (t < hd) {
       for (int r = 0; r < n; ++r) {
         const float p = sc[c0 + r] * inv;
-        o += p * vr[r * hd + t];
+        o += p * vr[r * ld + t];
       }
     }
     __syncthreads();
@@ -185,8 +199,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   float* qs = sm;              // [hd]
   float* kn = sm + hd;         // [hd] roped new k
   float* vn = sm + 2 * hd;     // [hd] new v
-  float* rows = sm + 3 * hd;   // [kAttnChunk][hd] staged K or V rows
-  float* sc = rows + kAttnChunk * hd;  // [n_pos] scores / probabilities
+  float* rows = sm + 3 * hd;   // [kAttnChunk][row_ld(hd)] staged K or V rows
+  float* sc = rows + kAttnChunk * row_ld(hd);  // [n_pos] scores / probabilities
   double* red = reinterpret_cast<double*>(sc + ((a.max_seq + 1) & ~1));
   const float* cr = a.cos_t + static_cast<long>(pos) * half;
   const float* sr = a.sin_t + static_cast<long>(pos) * half;
@@ -228,13 +242,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
   }
   if (pre) {
-    float* vrows = sc + ((a.max_seq + 1) & ~1) + 8;  // after the reduction slots (4 doubles)
+    float* vrows = sc + vrows_offset(a.max_seq);  // after the reduction slots, 16-byte aligned
     for_slots([&](auto J) {
       const int idx = t + kAttnThreads * decltype(J)::value, r = idx / q4n, c = idx - r * q4n;
       if (r < n0) {
-        reinterpret_cast<pre_f4*>(rows + r * hd)[c] =
+        reinterpret_cast<pre_f4*>(rows + r * row_ld(hd))[c] =
             r == pos ? reinterpret_cast<const pre_f4*>(kn)[c] : pk.template at<decltype(J)::value>();
-        reinterpret_cast<pre_f4*>(vrows + r * hd)[c] =
+        reinterpret_cast<pre_f4*>(vrows + r * row_ld(hd))[c] =
             r == pos ? reinterpret_cast<const pre_f4*>(vn)[c] : pv.template at<decltype(J)::value>();
       }
     });
@@ -243,6 +257,182 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   } else {
     attend<false>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
                   a.ctx + static_cast<long>(b) * a.ldq + h * hd, nullptr);
+  }
+}
+
+// One (KV group g, sequence b) per workgroup of kGroupThreads: the group's hpg query heads share
+// each staged K / V chunk, so the cache is read once per group instead of once per head (the
+// large-batch decode; launch_attention picks it).  Every head's arithmetic is the per-head
+// kernel's, operation for operation: a quad of lanes per (head, position) score with the same
+// partials and DPP tree, the softmax sums laid out as 256 threads (each half of the workgroup
+// takes every other head: thread t % 256 sums positions t % 256 + 256 i, then the four waves in
+// order), and one thread per (head, dimension) accumulating p * v over positions in order.
+constexpr int kGroupThreads = 512;
+constexpr int kGroupMaxOut = 4;  // (head, dimension) outputs per thread
+
+// Slots of the first chunk's K and V rows held in registers by each thread of the group kernel:
+// kAttnChunk rows of hd / 4 float4 over kGroupThreads threads (hd <= 128).
+constexpr int kGroupPreSlots = 4;
+struct GroupPre {
+  pre_f4 s0, s1, s2, s3;
+  template <int J>
+  __device__ __forceinline__ pre_f4& at() {
+    if constexpr (J == 0) return s0;
+    else if constexpr (J == 1) return s1;
+    else if constexpr (J == 2) return s2;
+    else return s3;
+  }
+};
+template <typename F>
+__device__ __forceinline__ void for_group_slots(F&& f) {
+  for_slots_impl(f, std::make_integer_sequence<int, kGroupPreSlots>{});
+}
+
+__global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int g = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
+  const int hpg = a.H / a.KV, kvd = a.KV * hd, sp = (a.max_seq + 1) & ~1;
+  float* qs = sm;                      // [hpg][hd] roped queries
+  float* kn = qs + hpg * hd;           // [hd] roped new k
+  float* vn = kn + hd;                 // [hd] new v
+  const int ld = row_ld(hd);
+  float* rows = vn + hd;                  // [kAttnChunk][ld] staged K rows (later chunks: K or V)
+  float* vrows = rows + kAttnChunk * ld;  // [kAttnChunk][ld] the first chunk's V rows
+  float* sc = vrows + kAttnChunk * ld;    // [hpg][sp] scores / probabilities
+  float* invs = sc + hpg * sp;            // [hpg] 1 / sum of each head's exponentials
+  const float* q = a.q + static_cast<long>(b) * a.ldq + g * hpg * hd;
+  const float* k_new = a.knew + static_cast<long>(b) * kvd + g * hd;
+  const float* v_new = a.vnew + static_cast<long>(b) * kvd + g * hd;
+  const float* kc = a.kcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;
+  const float* vc = a.vcache + (static_cast<long>(b) * a.max_seq) * kvd + g * hd;
+  const int t = threadIdx.x;
+  // The first chunk's cached rows (every row below max_seq is in bounds; rows at or past the
+  // position are replaced or unused) are requested with the position, q, k and v.
+  const int q4n = hd / 4, n_pre = min(kAttnChunk, a.max_seq);
+  GroupPre pk, pv;
+  for_group_slots([&](auto J) {
+    const int idx = t + kGroupThreads * decltype(J)::value, r = idx / q4n, c = idx - r * q4n;
+    if (r < n_pre) {
+      pk.template at<decltype(J)::value>() = reinterpret_cast<const pre_f4*>(kc + static_cast<long>(r) * kvd)[c];
+      pv.template at<decltype(J)::value>() = reinterpret_cast<const pre_f4*>(vc + static_cast<long>(r) * kvd)[c];
+    }
+  });
+  const int pos = *a.pos_dev, n_pos = pos + 1;
+  const float* cr = a.cos_t + static_cast<long>(pos) * half;
+  const float* sr = a.sin_t + static_cast<long>(pos) * half;
+  for (int idx = t; idx < hpg * half; idx += kGroupThreads) {
+    const int hh = idx / half, j = idx - hh * half;
+    const float qa = q[hh * hd + j], qb = q[hh * hd + j + half];
+    qs[hh * hd + j] = qa * cr[j] - qb * sr[j];
+    qs[hh * hd + j + half] = qb * cr[j] + qa * sr[j];
+  }
+  if (t < half) {
+    const float ka = k_new[t], kb = k_new[t + half];
+    kn[t] = ka * cr[t] - kb * sr[t];
+    kn[t + half] = kb * cr[t] + ka * sr[t];
+  }
+  for (int i = t; i < hd; i += kGroupThreads) vn[i] = v_new[i];
+  __syncthreads();
+  {  // k / v at pos for later steps
+    float* kw = a.kcache + (static_cast<long>(b) * a.max_seq + pos) * kvd + g * hd;
+    float* vw = a.vcache + (static_cast<long>(b) * a.max_seq + pos) * kvd + g * hd;
+    for (int i = t; i < hd; i += kGroupThreads) {
+      kw[i] = kn[i];
+      vw[i] = vn[i];
+    }
+  }
+  const int n0 = min(kAttnChunk, n_pos);
+  for_group_slots([&](auto J) {
+    const int idx = t + kGroupThreads * decltype(J)::value, r = idx / q4n, c = idx - r * q4n;
+    if (r < n0) {
+      reinterpret_cast<pre_f4*>(rows + r * ld)[c] =
+          r == pos ? reinterpret_cast<const pre_f4*>(kn)[c] : pk.template at<decltype(J)::value>();
+      reinterpret_cast<pre_f4*>(vrows + r * ld)[c] =
+          r == pos ? reinterpret_cast<const pre_f4*>(vn)[c] : pv.template at<decltype(J)::value>();
+    }
+  });
+  // scores: thread -> (head, position) of the chunk, positions across the lanes of a wave (one
+  // query row broadcast, distinct K rows)
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    if (c0 > 0) stage_rows(rows, kc, kvd, kn, pos, c0, n, hd);
+    __syncthreads();
+    for (int pr = t; pr < hpg * kAttnChunk; pr += kGroupThreads) {
+      const int hh = pr / kAttnChunk, r = pr - hh * kAttnChunk;
+      if (r < n) sc[hh * sp + c0 + r] = dot_f32_lds(qs + hh * hd, rows + r * ld, hd) * a.scale;
+    }
+    __syncthreads();
+  }
+  // softmax: one wave per head.  The per-head kernel's sums run over 256 threads (thread v takes
+  // positions v + 256 i, then a DPP tree per wave, then the four waves in order); lane l here
+  // keeps that layout's four threads l, 64 + l, 128 + l, 192 + l as four partial sums.
+  {
+    const int wave = t / kWave, lane = t & (kWave - 1);
+    for (int hh = wave; hh < hpg; hh += kGroupThreads / kWave) {
+      float* sh = sc + hh * sp;
+      float mx = -INFINITY;
+      for (int tp = lane; tp < n_pos; tp += kWave) mx = fmaxf(mx, sh[tp]);
+      mx = wave_max_dpp(mx);
+      double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+      for (int base = 0; base < n_pos; base += 4 * kWave) {
+        auto take = [&](int tp, double& acc) {
+          if (tp < n_pos) {
+            const float e = expf(sh[tp] - mx);
+            sh[tp] = e;
+            acc += static_cast<double>(e);
+          }
+        };
+        take(base + lane, s0);
+        take(base + kWave + lane, s1);
+        take(base + 2 * kWave + lane, s2);
+        take(base + 3 * kWave + lane, s3);
+      }
+      s0 = wave_sum_d_dpp(s0);
+      s1 = wave_sum_d_dpp(s1);
+      s2 = wave_sum_d_dpp(s2);
+      s3 = wave_sum_d_dpp(s3);
+      double tot = 0.0;
+      tot += s0;
+      tot += s1;
+      tot += s2;
+      tot += s3;
+      if (lane == 0) invs[hh] = static_cast<float>(1.0 / tot);
+    }
+  }
+  __syncthreads();
+  // out[h][d] = sum_t p_t v_t[d], positions in order
+  float o[kGroupMaxOut], inv[kGroupMaxOut];
+#pragma unroll
+  for (int u = 0; u < kGroupMaxOut; ++u) {
+    o[u] = 0.0f;
+    const int hh = (t + u * kGroupThreads) / hd;
+    inv[u] = hh < hpg ? invs[hh] : 0.0f;
+  }
+  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, n_pos - c0);
+    const float* vr = c0 == 0 ? vrows : rows;
+    if (c0 > 0) {
+      stage_rows(rows, vc, kvd, vn, pos, c0, n, hd);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kGroupMaxOut; ++u) {
+      const int idx = t + u * kGroupThreads, hh = idx / hd, d = idx - hh * hd;
+      if (hh < hpg) {
+        const float* ph = sc + hh * sp + c0;
+        for (int r = 0; r < n; ++r) {
+          const float pv_ = ph[r] * inv[u];
+          o[u] += pv_ * vr[r * ld + d];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + g * hpg * hd;
+#pragma unroll
+  for (int u = 0; u < kGroupMaxOut; ++u) {
+    const int idx = t + u * kGroupThreads;
+    if (idx < hpg * hd) out[idx] = o[u];
   }
 }
 
@@ -282,7 +472,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(Prefill
   const int hd = a.a.hd, g = h / (a.a.H / a.a.KV), kvd = a.a.KV * hd;
   float* qs = sm;
   float* rows = sm + 3 * hd;
-  float* sc = rows + kAttnChunk * hd;
+  float* sc = rows + kAttnChunk * row_ld(hd);
   double* red = reinterpret_cast<double*>(sc + ((a.a.max_seq + 1) & ~1));
   const float* q = a.a.q + static_cast<long>(r) * a.a.ldq + h * hd;
   for (int i = threadIdx.x; i < hd; i += blockDim.x) qs[i] = q[i];
@@ -358,7 +548,8 @@ int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld,
 }
 
 size_t attention_lds_bytes(int hd, int max_seq) {
-  return ((3 + static_cast<size_t>(kAttnChunk)) * hd + ((max_seq + 1) & ~1)) * sizeof(float) + 4 * sizeof(double);
+  return (3 * static_cast<size_t>(hd) + static_cast<size_t>(kAttnChunk) * row_ld(hd) + vrows_offset(max_seq)) *
+         sizeof(float);
 }
 
 int launch_prefill_attention(const PrefillArgs& a, int rows, hipStream_t s) {
@@ -385,15 +576,42 @@ int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s) {
   return EF_HIP_OK;
 }
 
+size_t attention_group_lds_bytes(int hpg, int hd, int max_seq) {
+  return (static_cast<size_t>(hpg + 2) * hd + 2 * static_cast<size_t>(kAttnChunk) * row_ld(hd) +
+          static_cast<size_t>(hpg) * ((max_seq + 1) & ~1) + hpg) *
+         sizeof(float);
+}
+
+// EF_HIP_ATTENTION=head / group forces a decode attention kernel (where the group kernel applies);
+// read at every launch, so an engine created after a change captures the new choice.
+int attention_choice() {
+  const char* v = std::getenv("EF_HIP_ATTENTION");
+  if (v == nullptr) return 0;
+  if (std::strcmp(v, "head") == 0) return 1;
+  if (std::strcmp(v, "group") == 0) return 2;
+  return 0;
+}
+
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
+  const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
+  const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
+  // Many sequences: one workgroup per (KV group, sequence) when that fills the chip (or is forced)
+  // and the group's scores fit in LDS.
+  const int hpg = a.H / a.KV, choice = attention_choice();
+  const size_t glds = attention_group_lds_bytes(hpg, a.hd, a.max_seq);
+  const bool group_ok = hpg >= 2 && a.hd % 8 == 0 && a.hd * kAttnChunk <= 4 * kGroupPreSlots * kGroupThreads && hpg * a.hd <= kGroupMaxOut * kGroupThreads &&
+                        glds <= lim;
+  if (group_ok && (choice == 2 || (choice == 0 && static_cast<long>(a.KV) * batch >= cus / 2))) {
+    hipLaunchKernelGGL(attention_group_kernel, dim3(a.KV, batch), dim3(kGroupThreads), glds, s, a);
+    EFH_HIP(hipGetLastError());
+    return EF_HIP_OK;
+  }
   // With few workgroups (latency-bound: a small batch) the decode kernel prefetches the first
   // chunk's K / V rows and stages the V rows in a second LDS buffer when it fits; with many, the
   // lighter kernel keeps more workgroups resident.
   AttnArgs b = a;
   size_t lds = attention_lds_bytes(a.hd, a.max_seq);
-  const size_t vrows = static_cast<size_t>(kAttnChunk) * a.hd * sizeof(float);
-  const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
-  const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
+  const size_t vrows = static_cast<size_t>(kAttnChunk) * row_ld(a.hd) * sizeof(float);
   b.pre_vrows = lds + vrows <= lim && static_cast<long>(a.H) * batch <= 2L * cus ? 1 : 0;
   if (b.pre_vrows) {
     lds += vrows;
