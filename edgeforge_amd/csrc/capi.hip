@@ -389,20 +389,33 @@ int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* 
     ws_bytes = gemv_mfma_workspace_bytes(&j0, 1, epi, batch, ldx);
     if (ws_bytes > 0) EFH_HIP(hipMalloc(&ws, ws_bytes));
   }
-  EFH_HIP(hipEventRecord(e0, s));
-  for (int i = 0; i < launches && rc == EF_HIP_OK; ++i) {
-    const size_t k = static_cast<size_t>(i) % n_weights;
-    const GemvJob j{W[k], epi == kEpiSwiglu ? W2[k] : nullptr, x, y};
-    rc = launch_gemv(&j, 1, epi, norm_w, eps, batch, ldx, ldy, s, ws, ws_bytes);
+  // the launches run as one captured HIP graph (as the decode engine runs its steps), so the time
+  // is the device's, not the host's launch rate
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipError_t he = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (he == hipSuccess) {
+    for (int i = 0; i < launches && rc == EF_HIP_OK; ++i) {
+      const size_t k = static_cast<size_t>(i) % n_weights;
+      const GemvJob j{W[k], epi == kEpiSwiglu ? W2[k] : nullptr, x, y};
+      rc = launch_gemv(&j, 1, epi, norm_w, eps, batch, ldx, ldy, s, ws, ws_bytes);
+    }
+    he = hipStreamEndCapture(s, &graph);
   }
-  EFH_HIP(hipEventRecord(e1, s));
-  EFH_HIP(hipEventSynchronize(e1));
-  if (ws != nullptr) (void)hipFree(ws);
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   float ms = 0.0f;
-  EFH_HIP(hipEventElapsedTime(&ms, e0, e1));
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipEventRecord(e0, s);
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipGraphLaunch(exec, s);
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipEventRecord(e1, s);
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipEventSynchronize(e1);
+  if (he == hipSuccess && rc == EF_HIP_OK) he = hipEventElapsedTime(&ms, e0, e1);
+  if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+  if (graph != nullptr) (void)hipGraphDestroy(graph);
+  if (ws != nullptr) (void)hipFree(ws);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   if (rc != EF_HIP_OK) return rc;
+  if (he != hipSuccess) return fail_hip(he, "profile_matvec: graph capture / launch");
   *avg_ms = ms / static_cast<float>(launches);
   return EF_HIP_OK;
 }

@@ -145,9 +145,11 @@ int ef_hip_sample(const float* logits_dev, size_t vocab, int batch, size_t ld, c
 int ef_hip_argmax(const float* x_dev, size_t n, int batch, size_t ld, int32_t* out_dev, void* stream);
 
 /* ---- profiling (the reference's per-op timing, src/bench_decode.cpp:164-231) -------------------
- * Launches `launches` GEMVs back to back on `stream`, cycling over n_weights weight handles (so the
+ * Runs `launches` GEMVs back to back on `stream` as one captured HIP graph (launch overhead
+ * excluded, as in the decode engine's step graphs), cycling over n_weights weight handles (so the
  * matrices come from HBM, not the 256 MB Infinity Cache), bracketed by HIP events on that stream;
- * *avg_ms is the mean time per launch.  epi: 0 = y = W x, 1 = y += W x, 2 = y = silu(W x)*(W2 x)
+ * *avg_ms is the mean time per launch (for batch > 1 a launch is the fragment preparation and the
+ * matrix-core GEMV).  `stream` must be capturable (not the null stream).  epi: 0 = y = W x, 1 = y += W x, 2 = y = silu(W x)*(W2 x)
  * (W2 then holds n_weights up matrices); norm_w_dev as in ef_hip_matvec_swiglu. */
 int ef_hip_profile_matvec(int epi, const ef_hip_weight* W, const ef_hip_weight* W2, size_t n_weights,
                           const float* x_dev, const float* norm_w_dev, float eps, float* y_dev, int batch,
