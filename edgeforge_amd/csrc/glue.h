@@ -19,6 +19,7 @@ struct AttnArgs {
   int H, KV, hd, max_seq;
   float scale;          // float(1 / sqrt(hd))
   int pre_vrows;        // set by launch_attention: the first chunk's V rows have their own LDS
+  int chunk;            // set by launch_attention: rows of the LDS staging buffer (>= 64)
 };
 
 // Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of

@@ -66,6 +66,11 @@ __host__ __device__ constexpr int row_ld(int hd) { return hd + 4; }  // floats b
 // Per-head kernel LDS after the scores: 4 reduction doubles, then (with the first-chunk prefetch)
 // the first chunk's V rows at this float offset from the scores, a multiple of 4.
 __host__ __device__ constexpr int vrows_offset(int max_seq) { return (((max_seq + 1) & ~1) + 8 + 3) & ~3; }
+// Floats of the staging buffer: kAttnChunk padded rows, or `chunk` (a multiple of 4) rows in
+// padded 4-row groups for the large-chunk path.
+__host__ __device__ constexpr int stage_floats(int hd, int chunk) {
+  return chunk > 64 ? (chunk / 4) * (4 * hd + 4) : 64 * (hd + 4);
+}
 
 // q . k over hd values (both in LDS, 16-byte aligned) in kern::dot_f32's order: partial j sums the
 // products i = j mod 8 in increasing i, a tail joins partial 0, then
@@ -97,6 +102,31 @@ __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long 
     const int r = idx / q, c = idx - r * q, tp = c0 + r;
     const float* src = tp == pos ? cur : cache + static_cast<long>(tp) * kvd;
     reinterpret_cast<float4*>(dst + r * row_ld(hd))[c] = reinterpret_cast<const float4*>(src)[c];
+  }
+}
+
+// Large chunks (hd = 64 only): rows c0 .. c0+n-1 of one KV head by LDS-DMA, one full-wave
+// buffer_load ... lds per 4 rows (lane l's 16 bytes land at the group's LDS address + 16 l, so a
+// group of 4 rows is 1 KB contiguous), groups kGroupFloats apart (16 bytes of padding), every
+// group issued before one wait; row `pos` is overwritten from `cur` after a barrier.  n rounded up to
+// 4 must fit the buffer (rows past n read zeros).  The caller's barrier publishes them.
+constexpr int kDmaHd = 64, kGroupFloats = 4 * kDmaHd + 4;
+__device__ __forceinline__ int dma_row_off(int r) { return (r >> 2) * kGroupFloats + (r & 3) * kDmaHd; }
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void stage_rows_dma(float* dst, const float* cache, long kvd, const float* cur, int pos,
+                                               int c0, int n) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(cache + static_cast<long>(c0) * kvd,
+                                             static_cast<uint32_t>(n) * static_cast<uint32_t>(kvd) * 4u);
+  const uint32_t lane_off = (static_cast<uint32_t>(lane >> 4) * static_cast<uint32_t>(kvd) + 4u * (lane & 15)) * 4u;
+  for (int j = wave; j < (n + 3) / 4; j += nw)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + j * kGroupFloats), 16,
+                                             static_cast<uint32_t>(4 * j) * static_cast<uint32_t>(kvd) * 4u + lane_off,
+                                             0, 0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (pos >= c0 && pos < c0 + n) {
+    __syncthreads();  // the group holding `pos` may come from another wave's load
+    for (int i = threadIdx.x; i < kDmaHd; i += blockDim.x) dst[dma_row_off(pos - c0) + i] = cur[i];
   }
 }
 
@@ -133,17 +163,38 @@ __device__ __forceinline__ void for_slots(F&& f) {
 // qs (roped query) is in LDS; K and V rows come from the cache except position `cur`, which is
 // taken from kn / vn (the decode step's new row; cur = -1 when every row is in the cache).
 // With USE_PRE the first chunk is already staged: its K rows in `rows`, its V rows in `vrows`.
-template <bool USE_PRE>
+template <bool USE_PRE, bool BIG = false>
 __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, double* red, const float* kc,
                                        const float* vc, long kvd, const float* kn, const float* vn, int cur,
-                                       int n_pos, int hd, float scale, float* out, const float* vrows) {
+                                       int n_pos, int hd, float scale, float* out, const float* vrows,
+                                       int big_chunk = kAttnChunk) {
+  // With BIG, every chunk after the first (kAttnChunk rows, USE_PRE) has big_chunk rows (hd = 64)
+  // staged by LDS-DMA in 4-row groups.  The chunking does not change any operation's order.
   const int t = threadIdx.x, ld = row_ld(hd);
-  // scores: one thread per position of the chunk
-  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
-    const int n = min(kAttnChunk, n_pos - c0);
-    if (!USE_PRE || c0 > 0) stage_rows(rows, kc, kvd, kn, cur, c0, n, hd);
+  constexpr bool big = BIG;
+  const int chunk = BIG ? big_chunk : kAttnChunk;
+  auto step_at = [&](int c0) { return USE_PRE && c0 == 0 ? kAttnChunk : chunk; };
+  auto grouped = [&](int c0) { return big && !(USE_PRE && c0 == 0); };  // layout of the chunk at c0
+  auto stage = [&](const float* cache, const float* cur_row, int c0, int n) {
+    if constexpr (big) {
+      stage_rows_dma(rows, cache, kvd, cur_row, cur, c0, n);
+    } else {
+      stage_rows(rows, cache, kvd, cur_row, cur, c0, n, hd);
+    }
+  };
+  // scores: one thread per position of the chunk; in a grouped chunk lane l of a wave takes row
+  // 4 (l % 16) + l / 16 of its 64, so the 16 lanes of each LDS phase read 16 different groups
+  for (int c0 = 0; c0 < n_pos; c0 += step_at(c0)) {
+    const int n = min(step_at(c0), n_pos - c0);
+    if (!USE_PRE || c0 > 0) stage(kc, kn, c0, n);
     __syncthreads();
-    if (t < n) sc[c0 + t] = dot_f32_lds(qs, rows + t * ld, hd) * scale;
+    if (grouped(c0)) {
+      const int l = t & (kWave - 1), lr = 4 * (l & 15) + (l >> 4);
+      for (int r = (t - l) + lr; r < ((n + kWave - 1) & ~(kWave - 1)); r += blockDim.x)
+        if (r < n) sc[c0 + r] = dot_f32_lds(qs, rows + dma_row_off(r), hd) * scale;
+    } else if (t < n) {  // n <= kAttnChunk <= blockDim.x
+      sc[c0 + t] = dot_f32_lds(qs, rows + t * ld, hd) * scale;
+    }
     __syncthreads();
   }
   // softmax_inplace: max, float exp(x - max), double sum, scale by float(1 / sum)
@@ -169,19 +220,26 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
   const float inv = static_cast<float>(1.0 / tot);
   // out[d] = sum_t p_t v_t[d], positions in order
   float o = 0.0f;
-  for (int c0 = 0; c0 < n_pos; c0 += kAttnChunk) {
-    const int n = min(kAttnChunk, n_pos - c0);
+  for (int c0 = 0; c0 < n_pos; c0 += step_at(c0)) {
+    const int n = min(step_at(c0), n_pos - c0);
     const float* vr = rows;
     if (USE_PRE && c0 == 0) {
       vr = vrows;
     } else {
-      stage_rows(rows, vc, kvd, vn, cur, c0, n, hd);
+      stage(vc, vn, c0, n);
     }
     __syncthreads();
     if (t < hd) {
-      for (int r = 0; r < n; ++r) {
-        const float p = sc[c0 + r] * inv;
-        o += p * vr[r * ld + t];
+      if (grouped(c0)) {
+        for (int r = 0; r < n; ++r) {
+          const float p = sc[c0 + r] * inv;
+          o += p * vr[dma_row_off(r) + t];
+        }
+      } else {
+        for (int r = 0; r < n; ++r) {
+          const float p = sc[c0 + r] * inv;
+          o += p * vr[r * ld + t];
+        }
       }
     }
     __syncthreads();
@@ -190,7 +248,7 @@ __device__ __forceinline__ void attend(const float* qs, float* rows, float* sc, 
 }
 
 
-template <bool PRE>
+template <bool PRE, bool BIG>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   const int h = blockIdx.x, b = blockIdx.y, hd = a.hd, half = hd / 2;
@@ -199,8 +257,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   float* qs = sm;              // [hd]
   float* kn = sm + hd;         // [hd] roped new k
   float* vn = sm + 2 * hd;     // [hd] new v
-  float* rows = sm + 3 * hd;   // [kAttnChunk][row_ld(hd)] staged K or V rows
-  float* sc = rows + kAttnChunk * row_ld(hd);  // [n_pos] scores / probabilities
+  float* rows = sm + 3 * hd;   // staged K or V rows: [kAttnChunk][row_ld(hd)], or a.chunk grouped rows
+  float* sc = rows + (BIG ? stage_floats(hd, a.chunk) : kAttnChunk * row_ld(hd));  // [n_pos] scores / probabilities
   double* red = reinterpret_cast<double*>(sc + ((a.max_seq + 1) & ~1));
   const float* cr = a.cos_t + static_cast<long>(pos) * half;
   const float* sr = a.sin_t + static_cast<long>(pos) * half;
@@ -252,8 +310,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             r == pos ? reinterpret_cast<const pre_f4*>(vn)[c] : pv.template at<decltype(J)::value>();
       }
     });
-    attend<true>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
-                 a.ctx + static_cast<long>(b) * a.ldq + h * hd, vrows);
+    attend<true, BIG>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
+                      a.ctx + static_cast<long>(b) * a.ldq + h * hd, vrows, a.chunk);
   } else {
     attend<false>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
                   a.ctx + static_cast<long>(b) * a.ldq + h * hd, nullptr);
@@ -607,17 +665,30 @@ int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
     return EF_HIP_OK;
   }
   // With few workgroups (latency-bound: a small batch) the decode kernel prefetches the first
-  // chunk's K / V rows and stages the V rows in a second LDS buffer when it fits; with many, the
-  // lighter kernel keeps more workgroups resident.
+  // chunk's K / V rows, stages the V rows in a second LDS buffer and stages every later chunk with
+  // as many rows as the LDS holds (one round trip per chunk); with many, the lighter kernel keeps
+  // more workgroups resident.
   AttnArgs b = a;
+  b.chunk = kAttnChunk;
   size_t lds = attention_lds_bytes(a.hd, a.max_seq);
-  const size_t vrows = static_cast<size_t>(kAttnChunk) * row_ld(a.hd) * sizeof(float);
+  const size_t ld = row_ld(a.hd), vrows = static_cast<size_t>(kAttnChunk) * ld * sizeof(float);
   b.pre_vrows = lds + vrows <= lim && static_cast<long>(a.H) * batch <= 2L * cus ? 1 : 0;
   if (b.pre_vrows) {
     lds += vrows;
-    hipLaunchKernelGGL(attention_kernel<true>, dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+    // large chunks only when every workgroup runs in one round (they cost occupancy)
+    const size_t base = lds - static_cast<size_t>(stage_floats(a.hd, kAttnChunk)) * sizeof(float);
+    const size_t group_bytes = static_cast<size_t>(4 * a.hd + 4) * sizeof(float);
+    const long want = std::min<long>(a.max_seq - kAttnChunk, static_cast<long>((lim - base) / group_bytes) * 4);
+    if (a.hd == kDmaHd && static_cast<long>(a.H) * batch <= cus && want >= 2 * kAttnChunk) {
+      b.chunk = static_cast<int>((want + 3) & ~3L);
+      if (base + static_cast<size_t>(stage_floats(a.hd, b.chunk)) * sizeof(float) > lim) b.chunk -= 4;
+      lds = base + static_cast<size_t>(stage_floats(a.hd, b.chunk)) * sizeof(float);
+      hipLaunchKernelGGL((attention_kernel<true, true>), dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+    } else {
+      hipLaunchKernelGGL((attention_kernel<true, false>), dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+    }
   } else {
-    hipLaunchKernelGGL(attention_kernel<false>, dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
+    hipLaunchKernelGGL((attention_kernel<false, false>), dim3(a.H, batch), dim3(kAttnThreads), lds, s, b);
   }
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;

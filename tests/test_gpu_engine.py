@@ -175,3 +175,38 @@ def test_group_attention_bit_identical_to_per_head(hip, cfg, B, monkeypatch):
         eng.close()
     assert np.array_equal(out["head"][0], out["group"][0])
     assert np.array_equal(out["head"][1], out["group"][1])
+
+
+LONG = Config(D=256, F=512, H=4, KV=2, hd=64, V=512, L=2, max_pos=512)
+
+
+def test_long_context_decode_matches_oracle(hip):
+    """Decode past a 280-token prompt: the per-head attention stages the positions after its first
+    64 in one LDS-DMA chunk; greedy tokens and the last logits match the oracle."""
+    print("[case] long-context decode, 280-token prompt", flush=True)
+    dm = DeviceModel.synthetic(LONG, seed=19)
+    om = OracleModel(dm)
+    prompt = [int(v) for v in D.rng(9).integers(0, LONG.V, 280)]
+    want, want_logits, _, _ = om.run_once(prompt, 12)
+    eng = Engine(dm, max_seq=300)
+    got, _, _ = eng.generate([prompt], 12)
+    assert got[0].tolist() == want.tolist()
+    assert _logit_err(eng.logits()[0], want_logits[-1]) < 1e-4
+    eng.close()
+
+
+def test_long_context_group_and_head_attention_identical(hip, monkeypatch):
+    """Positions 250..261: the per-head kernel (large LDS-DMA chunks) and the KV-group kernel
+    (64-row chunks) give identical logits and tokens."""
+    print("[case] long-context group vs per-head attention", flush=True)
+    dm = DeviceModel.synthetic(LONG, seed=23)
+    prompts = D.rng(43).integers(0, LONG.V, size=(2, 250)).astype(np.int32)
+    out = {}
+    for kind in ("head", "group"):
+        monkeypatch.setenv("EF_HIP_ATTENTION", kind)
+        eng = Engine(dm, max_seq=300, batch=2)
+        toks, _, _ = eng.generate(prompts, 12)
+        out[kind] = (toks, eng.logits())
+        eng.close()
+    assert np.array_equal(out["head"][0], out["group"][0])
+    assert np.array_equal(out["head"][1], out["group"][1])
