@@ -309,6 +309,130 @@ __global__ __launch_bounds__(kTP) void xfrag_kernel(PrepArgs a) {
   }
 }
 
+// One workgroup per sequence (K <= kSeqPrepMaxK): thread t owns fragment pairs p = t + 256 j
+// (block p / 4, k group p % 4) of sequence blockIdx.x, so the values it converts are also its share
+// of the per-sequence statistics and the row is read once, every load issued before the first
+// wait.  Sequences past the batch (up to the last table tile) get zero fragments.
+constexpr int kSeqPrepThreads = 256, kSeqPrepPairs = 4;
+constexpr int kSeqPrepMaxK = 32 * kSeqPrepThreads * kSeqPrepPairs / 4;  // 8192
+
+__global__ __launch_bounds__(kSeqPrepThreads) void xfrag_seq_kernel(PrepArgs a) {
+  __shared__ double s_ss[kSeqPrepThreads / kWave];
+  __shared__ float s_ax[kSeqPrepThreads / kWave], s_aw[kSeqPrepThreads / kWave];
+  const int sq = blockIdx.x, tile = sq / kSeqTile, i = sq % kSeqTile;
+  const int K = a.K, nb = K >> 5, npairs = nb * 4;
+  const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+  const bool has_norm = a.norm_w != nullptr, live = sq < a.B;
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 4u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (live ? sq : 0) * a.ldx, live ? row_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, has_norm ? row_bytes : 0u);
+  // byte offsets of a pair's two float4 in the Q4_0 order (weights 4g.. and 16 + 4g.. of the block)
+  // or the Q8_0 order (8g .. 8g + 7); pairs past the row read zeros
+  auto offs = [&](int pr, bool q4, uint32_t (&o)[2]) {
+    const uint32_t kb = static_cast<uint32_t>(pr >> 2), g = static_cast<uint32_t>(pr & 3);
+    const uint32_t base = pr < npairs ? kb * 128u : row_bytes;
+    o[0] = base + (q4 ? 16u * g : 32u * g);
+    o[1] = base + (q4 ? 64u + 16u * g : 32u * g + 16u);
+  };
+  const bool q4_first = a.t4 != nullptr;
+  f4v xv[kSeqPrepPairs][2], wv[kSeqPrepPairs][2];
+#pragma unroll
+  for (int j = 0; j < kSeqPrepPairs; ++j) {
+    uint32_t o[2];
+    offs(t + kSeqPrepThreads * j, q4_first, o);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rx, o[h], 0, 0));
+      wv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rw, o[h], 0, 0));
+    }
+  }
+  // statistics: every value of the row (and of the norm weights) is in exactly one thread's pairs
+  double ss = 0.0;
+  float ax = 0.0f, aw = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kSeqPrepPairs; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = xv[j][h][e];
+        ss += static_cast<double>(v) * static_cast<double>(v);
+        ax = fmaxf(ax, fabsf(v));
+        aw = fmaxf(aw, fabsf(wv[j][h][e]));
+      }
+  ss = wave_sum_d_dpp(ss);
+  ax = wave_max_dpp(ax);
+  aw = wave_max_dpp(aw);
+  if (lane == 0) {
+    s_ss[wave] = ss;
+    s_ax[wave] = ax;
+    s_aw[wave] = aw;
+  }
+  __syncthreads();
+  double tot = 0.0;
+  ax = 0.0f;
+  aw = 0.0f;
+  for (int w = 0; w < kSeqPrepThreads / kWave; ++w) {
+    tot += s_ss[w];
+    ax = fmaxf(ax, s_ax[w]);
+    aw = fmaxf(aw, s_aw[w]);
+  }
+  if (!has_norm) aw = 1.0f;
+  const float inv = has_norm ? static_cast<float>(1.0 / sqrt(tot / static_cast<double>(K) + static_cast<double>(a.eps)))
+                             : 1.0f;
+  const float bound = ax * inv * aw * 1.0001f;  // >= max |w * (x * inv)|
+  int ex = 0;
+  if (bound > 0.0f && bound <= 3.0e38f) ex = ilogbf(bound) - 14;  // bound * 2^-ex < 2^15
+  const float pre = ldexpf(1.0f, -ex);
+  if (t == 0 && live) a.post[sq] = ldexpf(1.0f, ex);
+  // fragments: hi and lo of the 8 values in slot order, slots with q16 set divided by 16
+  auto emit = [&](uint8_t* table, int pr, const f4v (&x2)[2], const f4v (&w2)[2], bool q4) {
+    if (pr >= npairs) return;
+    float v[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y = x2[h][e];
+        if (has_norm) y = w2[h][e] * (y * inv);  // HF order: w * (x * inv)
+        v[4 * h + e] = y * pre;
+      }
+    // Q4_0 slots 0..7 = weights 4g + {0, 2, 16, 18, 1, 3, 17, 19}; Q8_0 = 8g + {0, 2, 1, 3, 4, 6, 5, 7}
+    constexpr int ord4[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    constexpr int ord8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    h8 hi, lo;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float xp = v[q4 ? ord4[u] : ord8[u]];
+      const _Float16 hh = static_cast<_Float16>(xp);
+      const _Float16 ll = static_cast<_Float16>(xp - static_cast<float>(hh));
+      const _Float16 qs = static_cast<_Float16>(q4 && (u & 2) ? 0.0625f : 1.0f);  // exact powers of two
+      hi[u] = hh * qs;
+      lo[u] = ll * qs;
+    }
+    const int kb = pr >> 2, g = pr & 3;
+    uint8_t* f = table + ((static_cast<size_t>(tile) * nb + kb) * 2 * kWave + (16 * g + i)) * 16;
+    *reinterpret_cast<h8*>(f) = hi;
+    *reinterpret_cast<h8*>(f + kWave * 16) = lo;
+  };
+#pragma unroll
+  for (int j = 0; j < kSeqPrepPairs; ++j) emit(q4_first ? a.t4 : a.t8, t + kSeqPrepThreads * j, xv[j], wv[j], q4_first);
+  if (q4_first && a.t8 != nullptr) {  // both tables: the Q8_0 order's values, read again
+#pragma unroll
+    for (int j = 0; j < kSeqPrepPairs; ++j) {
+      uint32_t o[2];
+      offs(t + kSeqPrepThreads * j, false, o);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        xv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rx, o[h], 0, 0));
+        wv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rw, o[h], 0, 0));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kSeqPrepPairs; ++j) emit(a.t8, t + kSeqPrepThreads * j, xv[j], wv[j], false);
+  }
+}
+
 // Weights in tile order: for every 16-row tile T and block b, the 16 rows' codes in the order the
 // B fragment's lanes use them (lane l = 16 g + j: row j's code bytes 4g .. 4g + 3 of a Q4_0 block,
 // 8g .. 8g + 7 of a Q8_0 block), then the 16 rows' fp16 scales: 288 (Q4_0) or 544 (Q8_0) bytes at
@@ -842,8 +966,12 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
     p.t8 = t8;
     p.post = post;
     const int nbk = static_cast<int>(K / 32);
-    hipLaunchKernelGGL(xfrag_kernel, dim3((nbk + kPrepBlocks - 1) / kPrepBlocks, pl.SG * pl.NS), dim3(kTP), 0, stream,
-                       p);  // tiles past B get zeros
+    if (K <= static_cast<size_t>(kSeqPrepMaxK)) {  // tiles past B get zeros
+      hipLaunchKernelGGL(xfrag_seq_kernel, dim3(pl.SG * pl.NS * kSeqTile), dim3(kSeqPrepThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL(xfrag_kernel, dim3((nbk + kPrepBlocks - 1) / kPrepBlocks, pl.SG * pl.NS), dim3(kTP), 0,
+                         stream, p);
+    }
     a.n_jobs = n_jobs;
     a.K = static_cast<int>(K);
     a.B = nb;
