@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 SMALL = Config(D=256, F=512, H=4, KV=2, hd=64, V=512, L=3, max_pos=64)
 ODD = Config(D=96, F=160, H=3, KV=1, hd=32, V=200, L=2, max_pos=32)  # generic (cols % 64 != 0) GEMV path
+WIDE = Config(D=512, F=768, H=4, KV=2, hd=128, V=300, L=2, max_pos=64)  # head_dim 128
 
 
 def _logit_err(a, b):
@@ -26,7 +27,8 @@ def _top2_margin(l):
     return float(s[-1] - s[-2])
 
 
-@pytest.mark.parametrize("cfg,q8", [(SMALL, {(0, "wk"), (1, "wv"), (2, "w_down")}), (ODD, {(1, "wq")})])
+@pytest.mark.parametrize("cfg,q8", [(SMALL, {(0, "wk"), (1, "wv"), (2, "w_down")}), (ODD, {(1, "wq")}),
+                                    (WIDE, {(0, "wo")})])
 def test_forward_logits_match_oracle_each_position(hip, cfg, q8):
     print(f"[case] engine forward {cfg}", flush=True)
     dm = DeviceModel.synthetic(cfg, seed=7, q8=q8)
@@ -141,7 +143,7 @@ def test_engine_rejects_bad_tokens_and_positions(tinyllama):
     eng.close()
 
 
-@pytest.mark.parametrize("cfg", [SMALL, ODD])
+@pytest.mark.parametrize("cfg", [SMALL, ODD, WIDE])
 def test_group_attention_forward_matches_oracle(hip, cfg, monkeypatch):
     """The KV-group decode attention (one workgroup per KV group and sequence, forced here at B=1;
     ODD has three query heads per group) against the oracle's Transformer at every position."""
@@ -159,7 +161,7 @@ def test_group_attention_forward_matches_oracle(hip, cfg, monkeypatch):
     eng.close()
 
 
-@pytest.mark.parametrize("cfg,B", [(ODD, 3), (TINYLLAMA, 8)])
+@pytest.mark.parametrize("cfg,B", [(ODD, 3), (WIDE, 2), (TINYLLAMA, 8)])
 def test_group_attention_bit_identical_to_per_head(hip, cfg, B, monkeypatch):
     """Both decode attention kernels keep the reference's operation order per head, so a batch
     decoded with either gives identical logits and tokens."""
