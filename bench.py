@@ -24,6 +24,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak, published
 PUBLISHED_CPU_TPS = 21.92  # reference AVX2, 6 threads, Ryzen 5 7530U (bench/report_DESKTOP-IH5KR28.md:198)
 
 
@@ -235,6 +236,10 @@ def main() -> int:
     extra["q4_0_5632x2048_b64_gbs"] = round(q4b_bytes / (q4b_ms * 1e-3) / 1e9, 1)
     extra["q4_0_5632x2048_b64_hbm_frac"] = round(q4b_bytes / (q4b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     extra["q4_0_5632x2048_b64_us"] = round(q4b_ms * 1e3, 2)
+    # matrix-core view of the same launches: 2 fp16 products (hi and lo parts of x) per weight
+    q4b_flops = 2 * 2 * 64 * 5632 * 2048
+    extra["q4_0_5632x2048_b64_mfma_tflops"] = round(q4b_flops / (q4b_ms * 1e-3) / 1e12, 1)
+    extra["q4_0_5632x2048_b64_mfma_frac"] = round(q4b_flops / (q4b_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
     lm_ms, lm_bytes = profile_plain(H, L, model, "lm_head", L.Q8_0, 34, batch=1)
     extra["lm_head_q8_0_b1_gbs"] = round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1)
     mb = membench(L)
