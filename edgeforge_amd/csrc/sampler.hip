@@ -11,8 +11,8 @@
 //    full bitonic sort of all keys in the workspace;
 //  * the softmax over the kept ids, the top-p cut, its renormalisation and the CDF walk are the
 //    reference's sequential double loops, run by one thread in the same order.  They stop early
-//    only when every remaining term is below half an ulp of the running sum, since such terms
-//    (non-increasing, as the keys are sorted) can no longer change it;
+//    at the first term that leaves the running sum unchanged: the terms are sorted, non-negative
+//    and non-increasing, so no later one can change it either;
 //  * the draw is std::uniform_real_distribution<double>(0, 1) over a std::mt19937_64 kept on the
 //    device (one state per sequence), advanced once per call exactly when temperature > 0.
 // The one libm call is exp(double); the device's exp and glibc's agree to the last bit except in
@@ -29,6 +29,7 @@ namespace efh {
 namespace {
 
 constexpr int kThreads = 1024;
+constexpr int kRegSlots = 32;  // logits per thread on the register path (V <= 32768)
 constexpr int kMaxTopK = 1024;
 constexpr int kMtN = 312, kMtM = 156;
 
@@ -90,6 +91,11 @@ __device__ __forceinline__ uint64_t make_key(float v, uint32_t id) {
   return (static_cast<uint64_t>(order_bits(v)) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - id);
 }
 __device__ __forceinline__ uint32_t key_id(uint64_t k) { return 0xFFFFFFFFu - static_cast<uint32_t>(k); }
+// The logit a key was made from (-0 comes back as +0, which no later operation tells apart).
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t u = static_cast<uint32_t>(k >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
 
 // First maximum (strict >, scan order) of x[0..n): returns the index.  NaN never replaces the
 // running best; a NaN at index 0 is the answer, as in the sequential scan (kern::argmax,
@@ -229,43 +235,123 @@ __device__ void bitonic_global(uint64_t* g, int n, uint64_t* lds) {
       __syncthreads();
     }
   };
-  for (int base = 0; base < n; base += chunk) {  // every k <= chunk inside the chunk
-    for (int i = threadIdx.x; i < chunk; i += blockDim.x) lds[i] = g[base + i];
+  // chunk copies and the passes through memory keep 8 loads in flight per thread
+  auto load_chunk = [&](int base) {
+    for (int i0 = threadIdx.x; i0 < chunk; i0 += 8 * blockDim.x) {
+      uint64_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u * blockDim.x;
+        v[u] = i < chunk ? g[base + i] : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u * blockDim.x;
+        if (i < chunk) lds[i] = v[u];
+      }
+    }
     __syncthreads();
-    for (int k = 2; k <= chunk; k <<= 1) local_pass(base, k, k >> 1);
+  };
+  auto store_chunk = [&](int base) {
     for (int i = threadIdx.x; i < chunk; i += blockDim.x) g[base + i] = lds[i];
     __syncthreads();
+  };
+  for (int base = 0; base < n; base += chunk) {  // every k <= chunk inside the chunk
+    load_chunk(base);
+    for (int k = 2; k <= chunk; k <<= 1) local_pass(base, k, k >> 1);
+    store_chunk(base);
   }
   for (int k = chunk * 2; k <= n; k <<= 1) {
     for (int j = k >> 1; j >= chunk; j >>= 1) {
-      for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const int l = i ^ j;
-        if (l > i) {
-          const uint64_t x = g[i], y = g[l];
+      // the pairs (i, i ^ j) with bit j of i clear: q-th pair i = (q & (j-1)) | ((q & ~(j-1)) << 1)
+      const int half = n >> 1;
+      for (int q0 = threadIdx.x; q0 < half; q0 += 8 * blockDim.x) {
+        uint64_t x[8], y[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = q0 + u * blockDim.x;
+          const int i = (q & (j - 1)) | ((q & ~(j - 1)) << 1);
+          x[u] = q < half ? g[i] : 0ull;
+          y[u] = q < half ? g[i | j] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = q0 + u * blockDim.x;
+          if (q >= half) continue;
+          const int i = (q & (j - 1)) | ((q & ~(j - 1)) << 1);
           const bool desc = (i & k) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            g[i] = y;
-            g[l] = x;
+          if (desc ? (x[u] < y[u]) : (x[u] > y[u])) {
+            g[i] = y[u];
+            g[i | j] = x[u];
           }
         }
       }
       __syncthreads();
     }
     for (int base = 0; base < n; base += chunk) {
-      for (int i = threadIdx.x; i < chunk; i += blockDim.x) lds[i] = g[base + i];
-      __syncthreads();
+      load_chunk(base);
       local_pass(base, k, chunk >> 1);
-      for (int i = threadIdx.x; i < chunk; i += blockDim.x) g[base + i] = lds[i];
-      __syncthreads();
+      store_chunk(base);
     }
   }
 }
 
-// Half an ulp of a positive finite double s: adding any t < half_ulp(s) leaves s unchanged.
-__device__ __forceinline__ double half_ulp(double s) {
-  int e;
-  (void)frexp(s, &e);  // s = m * 2^e, m in [0.5, 1)
-  return ldexp(1.0, e - 54);
+
+// ---- sequential loops of the sampler ---------------------------------------------------------------
+// The reference's double sums, nucleus cut and CDF walk are left-to-right loops; thread 0 runs them
+// in that order.  A global array is staged into LDS kStage values at a time by the whole
+// workgroup, so thread 0 reads LDS; an array already in LDS is read in place.  step(v, i) consumes
+// element i and returns true to stop; every thread returns thread 0's stop index (n if none).
+constexpr int kStage = 4096;
+// Thread 0's pass over src[0..m) (element i is number base + i), eight values per group: the
+// reads of a group overlap, and step(v, cnt, first) consumes cnt <= 8 values in order, returning
+// the position in the group where the loop ends (-1: go on).  Returns the index where it ended,
+// or m.
+template <typename F>
+__device__ __forceinline__ int consume(const double* src, int m, int base, F& step) {
+  int i = 0;
+  for (; i + 8 <= m; i += 8) {  // whole groups: the count is a constant once step is inlined
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[i + u];
+    const int e = step(v, 8, base + i);
+    if (e >= 0) return i + e;
+  }
+  if (i < m) {
+    const int cnt = m - i;
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = u < cnt ? src[i + u] : 0.0;
+    const int e = step(v, cnt, base + i);
+    if (e >= 0) return i + e;
+  }
+  return m;
+}
+
+template <typename F>
+__device__ int serial_loop(const double* p, int n, bool in_lds, double* stage, int* s_stop, F&& step) {
+  if (in_lds) {
+    if (threadIdx.x == 0) *s_stop = consume(p, n, 0, step);
+    __syncthreads();
+    const int r = *s_stop;
+    __syncthreads();
+    return r;
+  }
+  int stop = n;
+  for (int base = 0; base < n; base += kStage) {
+    const int m = min(kStage, n - base);
+    for (int i = threadIdx.x; i < m; i += blockDim.x) stage[i] = p[base + i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int i = consume(stage, m, base, step);
+      *s_stop = i < m ? base + i : n;
+    }
+    __syncthreads();
+    stop = *s_stop;
+    __syncthreads();  // stage and s_stop are rewritten next round
+    if (stop < n) break;
+  }
+  return stop;
 }
 
 // ---- the sampler --------------------------------------------------------------------------------------------
@@ -314,19 +400,22 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ uint64_t s_keys[kChunk];  // 32 KB: top-k candidates / sort chunk
-  __shared__ uint32_t s_hist[256];
+  constexpr int kWaves = kThreads / kWave;
+  __shared__ uint32_t s_hist[256], s_sfx[256];
+  __shared__ uint32_t s_whist[kWaves * 256];  // per-wave histograms of the radix select
   __shared__ float s_val[kThreads / kWave];
   __shared__ int s_idx[kThreads / kWave];
-  __shared__ int s_cnt, s_keep;
+  __shared__ int s_cnt, s_keep, s_stop;
   __shared__ uint64_t s_prefix, s_mask;
   __shared__ int s_need, s_done;
   __shared__ double s_sum;
   __shared__ uint32_t s_seen[(32768 + 31) / 32];
+  __shared__ double s_prob[kMaxTopK];  // the kept probabilities of the top-k path
 
   const int b = blockIdx.x, V = a.vocab;
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
   float* work = reinterpret_cast<float*>(ws);                                   // [V]
-  double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));        // [V]
+  double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));        // [V] (no top-k)
   uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + ((V * 8 + 255) & ~255));  // [npow2]
   const float* lg = a.logits + b * a.ld;
 
@@ -335,26 +424,69 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     const double pe = softmax_prob(lg, V, a.eos_id, s_red);
     if (threadIdx.x == 0) a.eos_p[b] = pe;
   }
+  // Sampled top-k with V <= kRegSlots * kThreads keeps the logits in registers (thread t holds ids
+  // t + kThreads j): penalty, temperature and the radix select never go through memory.
+  const bool topk = a.top_k > 0 && a.top_k < V && a.top_k <= kMaxTopK;
+  const bool reg = a.temperature > 0.0f && topk && V <= kRegSlots * kThreads;
+  float rv[kRegSlots];
+  auto for_each_value = [&](auto&& f) {
+    if (reg) {
+#pragma unroll
+      for (int j = 0; j < kRegSlots; ++j) {
+        const int id = threadIdx.x + kThreads * j;
+        if (id < V) f(rv[j], id);
+      }
+    } else {
+      for (int i = threadIdx.x; i < V; i += blockDim.x) f(work[i], i);
+    }
+  };
+  if (reg) {
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) {
+      const int id = threadIdx.x + kThreads * j;
+      rv[j] = id < V ? lg[id] : 0.0f;
+    }
+    if (a.penalty != 1.0f) {  // every id of the history once: mark them, then each owner applies it
+      const int n = a.hist_len[b];
+      const int32_t* h = a.hist + b * a.hist_ld;
+      for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
+      __syncthreads();
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int t = h[i];
+        if (t >= 0 && t < V) atomicOr(&s_seen[t >> 5], 1u << (t & 31));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kRegSlots; ++j) {
+        const int id = threadIdx.x + kThreads * j;
+        if (id < V && (s_seen[id >> 5] >> (id & 31) & 1u))
+          rv[j] = rv[j] > 0.0f ? __fdiv_rn(rv[j], a.penalty) : rv[j] * a.penalty;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) rv[j] = __fdiv_rn(rv[j], a.temperature);
+  } else {
   for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = lg[i];
   __syncthreads();
-  // repetition penalty: each unique in-range history id once, in history order (src/sampler.cpp:16-24)
+  // repetition penalty: each unique in-range history id once (src/sampler.cpp:16-24).  The result
+  // depends only on which ids occur (each penalised value is a function of its own logit), so the
+  // history entries are taken in parallel: the entry whose atomicOr sets its id's bit applies it.
   if (a.penalty != 1.0f) {
     const int n = a.hist_len[b];
     const int32_t* h = a.hist + b * a.hist_ld;
     if (V <= 32768) {
       for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
       __syncthreads();
-      if (threadIdx.x == 0) {
-        for (int i = 0; i < n; ++i) {
-          const int t = h[i];
-          if (t < 0 || t >= V || (s_seen[t >> 5] >> (t & 31) & 1u)) continue;
-          s_seen[t >> 5] |= 1u << (t & 31);
-          const float l = work[t];
-          work[t] = l > 0.0f ? __fdiv_rn(l, a.penalty) : l * a.penalty;
-        }
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int t = h[i];
+        if (t < 0 || t >= V) continue;
+        const uint32_t bit = 1u << (t & 31);
+        if (atomicOr(&s_seen[t >> 5], bit) & bit) continue;
+        const float l = work[t];
+        work[t] = l > 0.0f ? __fdiv_rn(l, a.penalty) : l * a.penalty;
       }
-    } else if (threadIdx.x == 0) {  // large vocabularies: first-occurrence test by scanning
-      for (int i = 0; i < n; ++i) {
+    } else {  // large vocabularies: the first occurrence of each id applies it
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int t = h[i];
         if (t < 0 || t >= V) continue;
         bool dup = false;
@@ -375,8 +507,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = __fdiv_rn(work[i], a.temperature);
   __threadfence_block();
   __syncthreads();
+  }
 
-  const bool topk = a.top_k > 0 && a.top_k < V && a.top_k <= kMaxTopK;
   int keep = V;
   const uint64_t* sorted = nullptr;
   if (topk) {
@@ -389,36 +521,56 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       s_cnt = 0;
     }
     __syncthreads();
+    // Each wave counts into its own histogram (keys of similar logits share their top digits,
+    // and one shared histogram serialises those atomics across the waves).  The digit d kept is
+    // the largest with S(d) = (keys still in play with digit >= d) >= need, found by a parallel
+    // suffix sum; need then drops by S(d + 1).
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
     for (int shift = 56; shift >= 0 && !s_done; shift -= 8) {
-      for (int i = threadIdx.x; i < 256; i += blockDim.x) s_hist[i] = 0u;
+      for (int i = threadIdx.x; i < kWaves * 256; i += blockDim.x) s_whist[i] = 0u;
       __syncthreads();
       const uint64_t prefix = s_prefix, mask = s_mask;
-      for (int i = threadIdx.x; i < V; i += blockDim.x) {
-        const uint64_t k = make_key(work[i], i);
-        if ((k & mask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255u], 1u);
+      for_each_value([&](float v, int i) {
+        const uint64_t k = make_key(v, i);
+        if ((k & mask) == prefix) atomicAdd(&s_whist[wave * 256 + ((k >> shift) & 255u)], 1u);
+      });
+      __syncthreads();
+      if (threadIdx.x < 256) {  // digit d = threadIdx.x: 4 waves of 64 digits
+        const int d = threadIdx.x;
+        uint32_t c = 0;
+        for (int w = 0; w < kWaves; ++w) c += s_whist[w * 256 + d];
+        s_hist[d] = c;
+        uint32_t sfx = c;  // suffix sum over the wave's digits >= d
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t v = __shfl_down(sfx, o, kWave);
+          if (lane + o < kWave) sfx += v;
+        }
+        s_sfx[d] = sfx;
       }
       __syncthreads();
-      if (threadIdx.x == 0) {
-        int need = s_need, d = 255;
-        for (; d > 0; --d) {
-          if (static_cast<int>(s_hist[d]) >= need) break;
-          need -= static_cast<int>(s_hist[d]);
+      if (threadIdx.x < 256) {
+        const int d = threadIdx.x, need = s_need;
+        uint32_t above = 0;  // the waves of higher digits
+        for (int w = d / kWave + 1; w < 4; ++w) above += s_sfx[w * kWave];
+        const uint32_t S = s_sfx[d] + above, S1 = S - s_hist[d];  // S(d), S(d + 1)
+        if ((static_cast<int>(S) >= need || d == 0) && static_cast<int>(S1) < need) {
+          const int rest = need - static_cast<int>(S1);
+          s_need = rest;
+          s_prefix = prefix | (static_cast<uint64_t>(d) << shift);
+          s_mask = mask | (255ull << shift);
+          if (static_cast<int>(s_hist[d]) == rest) s_done = 1;
         }
-        s_need = need;
-        s_prefix = prefix | (static_cast<uint64_t>(d) << shift);
-        s_mask = mask | (255ull << shift);
-        if (static_cast<int>(s_hist[d]) == need) s_done = 1;
       }
       __syncthreads();
     }
     const uint64_t prefix = s_prefix, mask = s_mask;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) {
-      const uint64_t k = make_key(work[i], i);
+    for_each_value([&](float v, int i) {
+      const uint64_t k = make_key(v, i);
       if ((k & mask) >= prefix) {
         const int pos = atomicAdd(&s_cnt, 1);
         if (pos < kChunk) s_keys[pos] = k;
       }
-    }
+    });
     __syncthreads();
     int n2 = 1;
     while (n2 < a.top_k) n2 <<= 1;
@@ -435,67 +587,98 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     bitonic_global(keys, a.npow2, s_keys);
     sorted = keys;
   }
-  // softmax over the kept ids in double (src/sampler.cpp:42-49)
-  const float mx = work[key_id(sorted[0])];
-  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(work[key_id(sorted[i])] - mx));
+  // softmax over the kept ids in double (src/sampler.cpp:42-49); with top-k the kept probabilities
+  // live in LDS, otherwise the sequential loops below stage them through the sort buffer (free
+  // once the keys are sorted)
+  const bool in_lds = topk;
+  if (topk) prob = s_prob;
+  const float mx = key_value(sorted[0]);
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(key_value(sorted[i]) - mx));
   __threadfence_block();
   __syncthreads();
-  if (threadIdx.x == 0) {
+  double* stage = reinterpret_cast<double*>(s_keys);
+  static_assert(sizeof(s_keys) >= kStage * sizeof(double), "staging buffer");
+  {
+    // thread 0's running sum; a group that leaves it unchanged ends the loop (terms after the
+    // first unchanged one add nothing either, so checking once per group gives the same sum)
     double sum = 0.0;
-    for (int i = 0; i < keep; ++i) {
-      if (prob[i] < half_ulp(sum) && sum > 0.0) break;
-      sum += prob[i];
-    }
-    s_sum = sum;
+    serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = sum;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < cnt) sum = sum + v[u];
+      return (sum == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_sum = sum;
+    __syncthreads();
   }
-  __syncthreads();
   const double sum = s_sum;
   for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / sum;
   __threadfence_block();
   __syncthreads();
   if (a.top_p < 1.0f) {  // nucleus (src/sampler.cpp:50-61)
-    if (threadIdx.x == 0) {
-      double cum = 0.0;
-      int n = 0;
-      while (n < keep) {
-        if (cum > 0.0 && prob[n] < half_ulp(cum)) {
-          n = keep;  // cum is final and below top_p: the loop would run to the end
-          break;
+    double cum = 0.0;
+    const double tp = static_cast<double>(a.top_p);
+    // n = the number of terms taken; once cum is final and below top_p the loop would take all
+    // the running sums of a group in registers; the first that reaches top_p ends the loop, a
+    // group that leaves cum unchanged ends it with all terms kept
+    int n = serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = cum;
+      int hit = -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u < cnt && hit < 0) {
+          cum = cum + v[u];
+          if (cum >= tp) hit = u;
         }
-        cum += prob[n++];
-        if (cum >= static_cast<double>(a.top_p)) break;
       }
-      const int kp = n > 1 ? n : 1;
-      double s2 = 0.0;
-      for (int i = 0; i < kp; ++i) {
-        if (s2 > 0.0 && prob[i] < half_ulp(s2)) break;
-        s2 += prob[i];
-      }
-      s_keep = kp;
-      s_sum = s2;
-    }
+      if (hit >= 0) return hit;
+      return (cum == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_keep = n < keep && cum >= tp ? n + 1 : keep;  // cum < tp: every term
     __syncthreads();
-    keep = s_keep;
-    const double s2 = s_sum;
-    for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / s2;
+    const int kp = s_keep > 1 ? s_keep : 1;
+    double s2 = 0.0;
+    serial_loop(prob, kp, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = s2;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < cnt) s2 = s2 + v[u];
+      return (s2 == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_sum = s2;
+    __syncthreads();
+    keep = kp;
+    const double s2b = s_sum;
+    for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / s2b;
     __threadfence_block();
     __syncthreads();
   }
-  if (threadIdx.x == 0) {  // draw and CDF walk (src/sampler.cpp:62-69)
+  // draw and CDF walk (src/sampler.cpp:62-69)
+  double r = 0.0;
+  if (threadIdx.x == 0) {
     MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
-    const double r = mt_uniform(st);
-    int res = static_cast<int>(key_id(sorted[keep - 1]));
-    double cum = 0.0;
-    for (int i = 0; i < keep; ++i) {
-      if (cum > 0.0 && prob[i] < half_ulp(cum)) break;  // cum is final: r >= cum, so the last id
-      cum += prob[i];
-      if (r < cum) {
-        res = static_cast<int>(key_id(sorted[i]));
-        break;
+    r = mt_uniform(st);
+  }
+  double cum = 0.0;
+  int pick = keep - 1;  // the first i with r < cum; the last kept id when the sum ends below r
+  serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int first) {
+    const double before = cum;
+    int hit = -1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (u < cnt && hit < 0) {
+        cum = cum + v[u];
+        if (r < cum) hit = u;
       }
     }
-    a.out[b] = res;
-  }
+    if (hit >= 0) {
+      pick = first + hit;
+      return hit;
+    }
+    return (cum == before && before > 0.0) ? 0 : -1;  // cum is final and r >= cum
+  });
+  if (threadIdx.x == 0) a.out[b] = static_cast<int>(key_id(sorted[pick]));
 }
 
 }  // namespace
