@@ -214,65 +214,118 @@ __device__ void bitonic_lds(uint64_t* a, int n) {  // n power of two, <= 2 * blo
   }
 }
 
-// Full sort of n (power of two) keys in global memory.  Every compare-exchange distance below
-// kChunk runs on kChunk-element chunks held in LDS; larger distances go through memory.
+// Full sort of n (power of two, >= kChunk) keys in global memory, descending.  Each kChunk-key
+// chunk is held in registers, kChunk / kThreads keys per thread (thread t holds chunk positions
+// t + kThreads u), and a compare-exchange step of distance j runs where the partners are: in the
+// same thread (j >= kThreads), in the same wave (j < 64, a shuffle), or across waves (one LDS
+// exchange, double-buffered, one barrier).  Distances of a chunk or more go through memory.
 constexpr int kChunk = 4096;
-__device__ void bitonic_global(uint64_t* g, int n, uint64_t* lds) {
-  const int chunk = n < kChunk ? n : kChunk;
-  auto local_pass = [&](int base, int k, int jmax) {
-    for (int j = jmax; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < chunk; i += blockDim.x) {
-        const int l = i ^ j;
-        if (l > i) {
-          const uint64_t x = lds[i], y = lds[l];
-          const bool desc = ((base + i) & k) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            lds[i] = y;
-            lds[l] = x;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  };
-  // chunk copies and the passes through memory keep 8 loads in flight per thread
-  auto load_chunk = [&](int base) {
-    for (int i0 = threadIdx.x; i0 < chunk; i0 += 8 * blockDim.x) {
-      uint64_t v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + u * blockDim.x;
-        v[u] = i < chunk ? g[base + i] : 0ull;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + u * blockDim.x;
-        if (i < chunk) lds[i] = v[u];
+constexpr int kKeysPerThread = kChunk / kThreads;  // 4
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const int lo = __shfl_xor(static_cast<int>(v & 0xFFFFFFFFu), m, kWave);
+  const int hi = __shfl_xor(static_cast<int>(v >> 32), m, kWave);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+// Sort of n <= 64 keys (power of two) in LDS, descending, by wave 0 alone: one key per lane,
+// partners exchanged by shuffles, no barrier inside.
+__device__ void bitonic_wave(uint64_t* a, int n) {
+  if (threadIdx.x < kWave) {
+    const int i = threadIdx.x;
+    uint64_t x = i < n ? a[i] : 0ull;
+    for (int k = 2; k <= n; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint64_t y = shfl_xor_u64(x, j);
+        const bool take_max = ((i & k) == 0) == ((i & j) == 0);
+        x = take_max ? (x > y ? x : y) : (x < y ? x : y);
       }
     }
-    __syncthreads();
-  };
-  auto store_chunk = [&](int base) {
-    for (int i = threadIdx.x; i < chunk; i += blockDim.x) g[base + i] = lds[i];
-    __syncthreads();
-  };
-  for (int base = 0; base < n; base += chunk) {  // every k <= chunk inside the chunk
-    load_chunk(base);
-    for (int k = 2; k <= chunk; k <<= 1) local_pass(base, k, k >> 1);
-    store_chunk(base);
+    if (i < n) a[i] = x;
   }
-  for (int k = chunk * 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j >= chunk; j >>= 1) {
+  __syncthreads();
+}
+
+// Steps j = jmax .. 1 of bitonic stage k on the chunk at global index `base` (x: this thread's keys).
+// Every thread of the block calls it (it has barriers); buf holds 2 * kChunk keys.
+__device__ void chunk_steps(uint64_t (&x)[kKeysPerThread], int base, int k, int jmax, uint64_t* buf, int& parity) {
+  const int t = threadIdx.x;
+  for (int j = jmax; j > 0; j >>= 1) {
+    uint64_t y[kKeysPerThread];
+    static_assert(kKeysPerThread == 4, "partner selection below");
+    if (j >= kThreads) {  // partners in this thread: u ^ (j / kThreads), spelled out (no indexing)
+      if (j == kThreads) {
+        y[0] = x[1];
+        y[1] = x[0];
+        y[2] = x[3];
+        y[3] = x[2];
+      } else {
+        y[0] = x[2];
+        y[1] = x[3];
+        y[2] = x[0];
+        y[3] = x[1];
+      }
+    } else if (j >= kWave) {
+      uint64_t* b = buf + parity * kChunk;
+#pragma unroll
+      for (int u = 0; u < kKeysPerThread; ++u) b[t + kThreads * u] = x[u];
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < kKeysPerThread; ++u) y[u] = b[(t ^ j) + kThreads * u];
+      parity ^= 1;  // the next exchange writes the other buffer, so no second barrier is needed
+    } else {
+#pragma unroll
+      for (int u = 0; u < kKeysPerThread; ++u) y[u] = shfl_xor_u64(x[u], j);
+    }
+#pragma unroll
+    for (int u = 0; u < kKeysPerThread; ++u) {
+      const int i = base + t + kThreads * u;
+      const bool desc = (i & k) == 0, lower = (i & j) == 0;
+      // descending pair: the lower index keeps the larger key
+      const bool take_max = desc == lower;
+      x[u] = take_max ? (x[u] > y[u] ? x[u] : y[u]) : (x[u] < y[u] ? x[u] : y[u]);
+    }
+  }
+}
+
+__device__ void bitonic_global(uint64_t* g, int n, uint64_t* buf) {
+  const int t = threadIdx.x;
+  if (n < kChunk) {  // small vocabularies: the whole array in LDS
+    for (int i = t; i < n; i += blockDim.x) buf[i] = g[i];
+    __syncthreads();
+    bitonic_lds(buf, n);
+    for (int i = t; i < n; i += blockDim.x) g[i] = buf[i];
+    __syncthreads();
+    return;
+  }
+  int parity = 0;
+  auto load = [&](uint64_t (&x)[kKeysPerThread], int base) {
+#pragma unroll
+    for (int u = 0; u < kKeysPerThread; ++u) x[u] = g[base + t + kThreads * u];
+  };
+  auto store = [&](const uint64_t (&x)[kKeysPerThread], int base) {
+#pragma unroll
+    for (int u = 0; u < kKeysPerThread; ++u) g[base + t + kThreads * u] = x[u];
+  };
+  for (int base = 0; base < n; base += kChunk) {  // every stage k <= kChunk inside the chunk
+    uint64_t x[kKeysPerThread];
+    load(x, base);
+    for (int k = 2; k <= kChunk; k <<= 1) chunk_steps(x, base, k, k >> 1, buf, parity);
+    store(x, base);
+  }
+  __syncthreads();
+  for (int k = kChunk * 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j >= kChunk; j >>= 1) {
       // the pairs (i, i ^ j) with bit j of i clear: q-th pair i = (q & (j-1)) | ((q & ~(j-1)) << 1)
       const int half = n >> 1;
-      for (int q0 = threadIdx.x; q0 < half; q0 += 8 * blockDim.x) {
-        uint64_t x[8], y[8];
+      for (int q0 = t; q0 < half; q0 += 8 * blockDim.x) {
+        uint64_t xa[8], ya[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int q = q0 + u * blockDim.x;
           const int i = (q & (j - 1)) | ((q & ~(j - 1)) << 1);
-          x[u] = q < half ? g[i] : 0ull;
-          y[u] = q < half ? g[i | j] : 0ull;
+          xa[u] = q < half ? g[i] : 0ull;
+          ya[u] = q < half ? g[i | j] : 0ull;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -280,22 +333,23 @@ __device__ void bitonic_global(uint64_t* g, int n, uint64_t* lds) {
           if (q >= half) continue;
           const int i = (q & (j - 1)) | ((q & ~(j - 1)) << 1);
           const bool desc = (i & k) == 0;
-          if (desc ? (x[u] < y[u]) : (x[u] > y[u])) {
-            g[i] = y[u];
-            g[i | j] = x[u];
+          if (desc ? (xa[u] < ya[u]) : (xa[u] > ya[u])) {
+            g[i] = ya[u];
+            g[i | j] = xa[u];
           }
         }
       }
       __syncthreads();
     }
-    for (int base = 0; base < n; base += chunk) {
-      load_chunk(base);
-      local_pass(base, k, chunk >> 1);
-      store_chunk(base);
+    for (int base = 0; base < n; base += kChunk) {
+      uint64_t x[kKeysPerThread];
+      load(x, base);
+      chunk_steps(x, base, k, kChunk >> 1, buf, parity);
+      store(x, base);
     }
+    __syncthreads();
   }
 }
-
 
 // ---- sequential loops of the sampler ---------------------------------------------------------------
 // The reference's double sums, nucleus cut and CDF walk are left-to-right loops; thread 0 runs them
@@ -399,7 +453,7 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
 }
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
-  __shared__ uint64_t s_keys[kChunk];  // 32 KB: top-k candidates / sort chunk
+  __shared__ uint64_t s_keys[2 * kChunk];  // 64 KB: top-k candidates / sort exchange buffers
   constexpr int kWaves = kThreads / kWave;
   __shared__ uint32_t s_hist[256], s_sfx[256];
   __shared__ uint32_t s_whist[kWaves * 256];  // per-wave histograms of the radix select
@@ -576,7 +630,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     while (n2 < a.top_k) n2 <<= 1;
     for (int i = a.top_k + threadIdx.x; i < n2; i += blockDim.x) s_keys[i] = 0ull;
     __syncthreads();
-    bitonic_lds(s_keys, n2);
+    if (n2 <= kWave) {
+      bitonic_wave(s_keys, n2);
+    } else {
+      bitonic_lds(s_keys, n2);
+    }
     keep = a.top_k;
     sorted = s_keys;
   } else {
