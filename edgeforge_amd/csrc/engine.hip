@@ -259,10 +259,15 @@ int ensure_prefill(ef_hip_engine e, size_t rows) {
     const GemvJob gu{w.w_gate, w.w_up, bufs[0], bufs[5], c.D, c.F};
     const GemvJob dn{w.w_down, nullptr, bufs[5], bufs[0], c.F, c.D};
     // every row count a launch may use (a last chunk is shorter): the plan depends on
-    // min(rows, 64) only, so 2 .. 64 and the full count cover all of them
-    const int top = static_cast<int>(std::min<size_t>(rows, 64));
-    for (int R = 2; R <= top + 1; ++R) {
-      const int r = R <= top ? R : static_cast<int>(rows);
+    // min(rows, gemv_mfma_max_rows()) only; row counts up to 128 one by one, then every multiple
+    // of a 16-row tile (within a tile count the workspace grows with the rows), and the full count
+    const int cap = static_cast<int>(std::min<size_t>(rows, gemv_mfma_max_rows()));
+    std::vector<int> counts;
+    for (int r = 2; r <= std::min(cap, 128); ++r) counts.push_back(r);
+    for (int r = 144; r <= cap; r += 16) counts.push_back(r);
+    counts.push_back(cap);
+    counts.push_back(static_cast<int>(rows));
+    for (const int r : counts) {
       const GemvJob lm{e->lm_head, nullptr, bufs[0], nullptr, c.D, c.V};
       need = std::max({need, gemv_mfma_workspace_bytes(qkv, 3, kEpiStore, r, c.D),
                        gemv_mfma_workspace_bytes(&o, 1, kEpiResidual, r, c.D),

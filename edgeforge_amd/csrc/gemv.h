@@ -33,6 +33,8 @@ bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU 
 // for the same launch) holds the prepared activation fragments and the split-K partial sums;
 // without it the launch allocates stream-ordered memory.  0 when the launch does not take this path.
 size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx);
+// Rows (sequences) one matrix-core launch covers; larger batches run in chunks of this size.
+int gemv_mfma_max_rows();
 // The batched path reads Q4_0 / Q8_0 matrices from a tile-order copy (w->tiled, tiled_bytes(w)
 // bytes).  ensure_tiled makes it when missing (allocates; refused while `s` is capturing a graph).
 size_t tiled_bytes(const ef_hip_weight_s* w);

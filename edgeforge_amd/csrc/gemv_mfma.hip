@@ -54,7 +54,7 @@ constexpr int kTP = 1024;                       // prep workgroup
 constexpr int kWavesP = kTP / kWave;
 constexpr int kTileRows = 16;
 constexpr int kSeqTile = 16;                    // sequences per A operand (one per row)
-constexpr int kMaxTiles = 4;                    // sequence tiles per launch: 64 sequences
+constexpr int kMaxTiles = 64;                   // sequence tiles per launch: 1024 sequences (rows)
 constexpr int kMaxJobsM = 4;
 constexpr int kPrepBlocks = kTP / kWave;        // blocks per xfrag workgroup: one per wave
 constexpr int kMaxBlocksPerWave = 8;            // K blocks per wave of one batched GEMV workgroup
@@ -872,6 +872,7 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   // Layout: the A tables (every sequence tile of the grid, zeros past the batch), the scales, the
   // split-K partial sums.
   p.tab = static_cast<size_t>(p.SG) * p.NS * nb * 2 * kWave * 16;
+  if (p.tab >= (size_t(1) << 32)) return Plan{};  // one buffer resource per table
   size_t off = (p.q4 ? p.tab : 0) + (p.q8 ? p.tab : 0) + kMaxTiles * kSeqTile * sizeof(float);
   off = (off + 255) & ~size_t(255);
   p.part_off = off;
@@ -915,6 +916,8 @@ int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s) {
   w->tiled = out;
   return EF_HIP_OK;
 }
+
+int gemv_mfma_max_rows() { return kMaxTiles * kSeqTile; }
 
 size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
   const Plan p = plan_mfma(jobs, n_jobs, epi, batch, ldx);

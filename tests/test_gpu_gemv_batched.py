@@ -3,9 +3,9 @@
 Every sequence of a batch must meet the single-vector gates:
 |gpu - exact| <= 1e-5 * sum|w x| per row (tests/test_qinfer.cpp:95) and max |gpu - cpu fp32| <= 1e-4
 against the oracle's AVX2 kernel (src/qkernels.cpp:131-180) on that sequence alone.  Shapes cover
-batches that are not a multiple of the 8-sequence tile, more than 64 sequences (several launches),
-row counts that leave a partial workgroup, Q8_0, a K split (K = 5632 at B = 64) and mixed-type
-launches; epilogues and the fused RMSNorm are checked against the oracle's separate operations.
+batches that are not a multiple of the 16-sequence tile, many tiles in one launch, more than 1024
+sequences (several launches), row counts that leave a partial workgroup, Q8_0, a K split (K = 5632
+at B = 64) and mixed-type launches; epilogues and the fused RMSNorm are checked against the oracle's separate operations.
 """
 import numpy as np
 import pytest
@@ -27,7 +27,9 @@ def _batch_x(seed, batch, cols):
     (O.Q4_0, 512, 2048, 5),      # one partial sequence tile
     (O.Q8_0, 300, 2048, 16),     # Q8_0, rows leave a partial workgroup
     (O.Q4_0, 2048, 5632, 64),    # K split across workgroups
-    (O.Q4_0, 37, 256, 70),       # two launches (64 + 6 sequences), tiny K
+    (O.Q4_0, 37, 256, 70),       # tiny K, a partial last tile
+    (O.Q4_0, 96, 512, 300),      # 19 sequence tiles in one launch
+    (O.Q8_0, 37, 256, 1100),     # two launches (1024 + 76 sequences)
     (O.Q8_0, 64, 512, 2),
 ])
 def test_batched_gemv_each_sequence_meets_the_gates(hip, qtype, rows, cols, batch):
