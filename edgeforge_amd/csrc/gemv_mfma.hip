@@ -538,27 +538,33 @@ __device__ __forceinline__ void block_products(const WRegs<Q4> (&W)[RT][NM], con
 }
 
 // The wave's blocks b = kb0 + wave + 8 i < kb1: the weights two blocks ahead and the A fragments
-// one block ahead are loaded while the current block's products run.  Loads past a buffer's range
-// read as zeros, so the prefetches need no bounds test.
+// one block ahead are loaded while the current block's products run.  Prefetches past the row
+// read its last block instead, so they need no bounds test.
 template <int RT, int NM, int NS, bool Q4>
 __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, int kb0, int kb1, int wave, int lane,
                                        __amdgpu_buffer_rsrc_t tab, uint32_t tile0, uint32_t tstride,
                                        f4v (&acc)[RT][NM][NS]) {
   const uint32_t bb = Q4 ? kTileBlockQ4 : kTileBlockQ8;
+  const int last_tile = static_cast<int>(jb.bytes / (static_cast<uint32_t>(nb) * bb)) - 1;
   const __amdgpu_buffer_rsrc_t r1 = make_rsrc(jb.W, jb.bytes);
   const __amdgpu_buffer_rsrc_t r2 = make_rsrc(NM == 2 ? jb.W2 : jb.W, jb.bytes);
   const uint32_t voff_c = static_cast<uint32_t>(lane) * (Q4 ? 4 : 8);
   const uint32_t voff_s = (Q4 ? 256u : 512u) + 2u * static_cast<uint32_t>(lane & 15);
   const uint32_t voff_a = static_cast<uint32_t>(lane) * 16;
+  // prefetches past the row read its last block and row tiles past the matrix its last tile (never
+  // used): every load stays inside its buffer
   auto load_wb = [&](WRegs<Q4> (&dst)[RT][NM], int kb) {
+    kb = min(kb, nb - 1);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>((tile_row0 + rt) * nb + kb) * bb);
+      const int tr = min(tile_row0 + rt, last_tile);
+      const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tr * nb + kb) * bb);
       dst[rt][0] = load_w<Q4>(r1, voff_c, voff_s, so);
       if (NM == 2) dst[rt][NM - 1] = load_w<Q4>(r2, voff_c, voff_s, so);
     }
   };
   auto load_a = [&](h8 (&dst)[NS][2], int kb) {
+    kb = min(kb, nb - 1);
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
@@ -569,9 +575,9 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
       }
   };
   // Fully unrolled over at most kMaxBlocksPerWave blocks.  Every prefetch is issued
-  // unconditionally (a block past this workgroup's range is read and never used; past the matrix
-  // it reads as zeros), so every path has the same loads in flight and the wait before each
-  // block's products covers only that block's loads.
+  // unconditionally (a block past this workgroup's range is read and never used), so every path
+  // has the same loads in flight and the wait before each block's products covers only that
+  // block's loads.
   WRegs<Q4> W[kMaxBlocksPerWave][RT][NM];
   h8 A[2][NS][2];
   const int kb = kb0 + wave;

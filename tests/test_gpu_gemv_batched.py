@@ -23,6 +23,7 @@ def _batch_x(seed, batch, cols):
     return np.stack([D.activations_with_outliers(seed + b, cols) for b in range(batch)]).astype(np.float32)
 
 
+
 @pytest.mark.parametrize("qtype,rows,cols,batch", [
     (O.Q4_0, 512, 2048, 5),      # one partial sequence tile
     (O.Q8_0, 300, 2048, 16),     # Q8_0, rows leave a partial workgroup
@@ -100,3 +101,44 @@ def test_batched_mixed_type_jobs_with_norm(hip):
         for i, (qt, rows) in enumerate(shapes):
             cpu = O.matvec(qt, keep[i].reshape(-1), h)
             assert np.abs(outs[i].numpy()[b, :rows] - cpu).max() <= ABS_TOL, (b, i)
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0])
+def test_batched_gemv_dynamic_range(hip, qtype):
+    """Sequences 12 decades apart, one block 1e5 above the rest of its sequence and an all-zero
+    sequence in one launch: each sequence meets the gates on its own (every sequence has its own
+    power-of-two scale), and the zero sequence gives exact zeros."""
+    rows, cols, B = 96, 2048, 20
+    print(f"[case] batched gemv dynamic range qtype={qtype}", flush=True)
+    packed = D.random_rows(qtype, rows, cols, seed=91)
+    X = _batch_x(500, B, cols) * (10.0 ** np.linspace(-6.0, 6.0, B))[:, None]
+    X[3, 64:96] *= 1e5
+    X[7, :] = 0.0
+    X = X.astype(np.float32)
+    W = hip.Weight(qtype, rows, cols, host=packed)
+    dx = hip.DeviceArray.from_host(X)
+    dy = hip.DeviceArray((B, rows))
+    hip.matvec(W, dx, dy, batch=B)
+    got = dy.numpy()
+    w64 = D.dequant_exact(qtype, packed, cols)
+    for b in range(B):
+        assert D.rel_dot_error(w64, X[b], got[b]).max() < REL_TOL, b
+    assert not got[7].any()
+
+
+def test_batched_norm_long_rows(hip):
+    """An RMSNorm fused into a product whose rows are longer than one workgroup's blocks (K = 4096,
+    a K split): the results meet the gates against the oracle's norm + matvec."""
+    B, cols, rows = 6, 4096, 128
+    X = np.stack([D.normal(80 + b, cols) for b in range(B)]).astype(np.float32)
+    nw = (1.0 + 0.05 * D.normal(81, cols)).astype(np.float32)
+    packed = O.quantize(O.Q4_0, D.normal(82, (rows, cols), 0.02))
+    W = hip.Weight(O.Q4_0, rows, cols, host=packed)
+    out = hip.DeviceArray((B, rows))
+    hip.matvec_jobs_rmsnorm([(W, hip.DeviceArray.from_host(X), out)], hip.DeviceArray.from_host(nw), 1e-5,
+                            batch=B, ldx=cols, ldy=rows)
+    L = O.lib()
+    for b in range(B):
+        h = np.empty(cols, np.float32)
+        L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), cols, 1e-5)
+        assert np.abs(out.numpy()[b] - O.matvec(O.Q4_0, packed.reshape(-1), h)).max() <= ABS_TOL, b
