@@ -94,20 +94,27 @@ def profile_plain(H, L, model, key, qtype, block, batch: int, launches: int = 40
     return avg.value, gemv_bytes(w0.rows, w0.cols, block, batch=batch)
 
 
+CPU_RUNS = {"threads": 7, "one": 3}  # timed runs per thread count; the medians are reported
+
+
 def cpu_baseline(model, prompt, n: int = 32):
     """The reference CPU path (oracle: AVX2 + persistent thread pool, src/qkernels.cpp:131-297,
     src/threadpool.cpp) on this host, same weights, the reference protocol: (n-1)/decode_s, at the
-    default thread count and at one thread (the ladder's first row, src/bench_decode.cpp:73-81)."""
+    default thread count and at one thread (the ladder's first row, src/bench_decode.cpp:73-81),
+    each the median of CPU_RUNS timed runs (about 10-15 s of CPU work in all)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle as O  # noqa: F401  (checker / baseline only)
     from oracle.model import OracleModel, cpu_threads
     om = OracleModel(model)
     threads = cpu_threads()
     out = {}
-    for t in (threads, 1):
+    for t, runs in ((threads, CPU_RUNS["threads"]), (1, CPU_RUNS["one"])):
         om.run_once(prompt[:4], 2, threads=t)  # warm-up (src/bench_decode.cpp:90-95)
-        _, _, pre, dec = om.run_once(prompt, n, threads=t)
-        out[t] = (n - 1) / dec
+        rates = []
+        for _ in range(runs):
+            _, _, pre, dec = om.run_once(prompt, n, threads=t)
+            rates.append((n - 1) / dec)
+        out[t] = float(np.median(rates))
     return out[threads], threads, out[1]
 
 
@@ -272,8 +279,9 @@ def main() -> int:
         cpu = {"value": round(cpu_tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
                "value_1_thread": round(cpu1, 3), "physical_cores": phys, "logical_cpus": logical,
                "cpu_model": cpu_model_name(),
-               "sample": "one sequence, 23-token prompt + 32 greedy steps (tok/s = 31/decode_s), full config-5 "
-                         "weights, oracle AVX2 + thread pool; the same run on 1 thread as value_1_thread"}
+               "sample": f"one sequence, 23-token prompt + 32 greedy steps (tok/s = 31/decode_s), full config-5 "
+                         f"weights, oracle AVX2 + thread pool; median of {CPU_RUNS['threads']} runs, and of "
+                         f"{CPU_RUNS['one']} runs on 1 thread as value_1_thread"}
 
     out = {
         "metric": "decode tok/s at TinyLlama-1.1B shapes B=1/64; Q4_0 matvec GB/s % of HBM peak",
