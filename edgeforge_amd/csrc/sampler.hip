@@ -425,6 +425,7 @@ struct SampleArgs {
   int npow2;
   int eos_id;     // with eos_p: P(eos_id) under softmax(logits) per sequence
   double* eos_p;  // [batch] or null
+  int phase;      // 0: one launch; 1: stop once the keys are written (the sort runs in other launches)
 };
 
 // P(id) under softmax of the raw logits, in double (prob_of, src/chat.cpp:35-42): max, then the sum
@@ -450,6 +451,102 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
   __syncthreads();
   if (id < 0 || id >= V) return 0.0;
   return exp(static_cast<double>(lg[id]) - m) / tot;
+}
+
+// The sampler after the sort (src/sampler.cpp:42-69): softmax over the kept ids, the nucleus, the
+// draw and the CDF walk.  `sorted` holds the keys in descending order, `stage` kStage doubles of LDS.
+__device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, int keep, bool topk, double* prob,
+                            double* s_prob, double* stage, int& s_stop, double& s_sum, int& s_keep) {
+  // softmax over the kept ids in double (src/sampler.cpp:42-49); with top-k the kept probabilities
+  // live in LDS, otherwise the sequential loops below stage them through the sort buffer (free
+  // once the keys are sorted)
+  const bool in_lds = topk;
+  if (topk) prob = s_prob;
+  const float mx = key_value(sorted[0]);
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(key_value(sorted[i]) - mx));
+  __threadfence_block();
+  __syncthreads();
+  {
+    // thread 0's running sum; a group that leaves it unchanged ends the loop (terms after the
+    // first unchanged one add nothing either, so checking once per group gives the same sum)
+    double sum = 0.0;
+    serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = sum;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < cnt) sum = sum + v[u];
+      return (sum == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_sum = sum;
+    __syncthreads();
+  }
+  const double sum = s_sum;
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / sum;
+  __threadfence_block();
+  __syncthreads();
+  if (a.top_p < 1.0f) {  // nucleus (src/sampler.cpp:50-61)
+    double cum = 0.0;
+    const double tp = static_cast<double>(a.top_p);
+    // n = the number of terms taken; once cum is final and below top_p the loop would take all
+    // the running sums of a group in registers; the first that reaches top_p ends the loop, a
+    // group that leaves cum unchanged ends it with all terms kept
+    int n = serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = cum;
+      int hit = -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u < cnt && hit < 0) {
+          cum = cum + v[u];
+          if (cum >= tp) hit = u;
+        }
+      }
+      if (hit >= 0) return hit;
+      return (cum == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_keep = n < keep && cum >= tp ? n + 1 : keep;  // cum < tp: every term
+    __syncthreads();
+    const int kp = s_keep > 1 ? s_keep : 1;
+    double s2 = 0.0;
+    serial_loop(prob, kp, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+      const double before = s2;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < cnt) s2 = s2 + v[u];
+      return (s2 == before && before > 0.0) ? 0 : -1;
+    });
+    if (threadIdx.x == 0) s_sum = s2;
+    __syncthreads();
+    keep = kp;
+    const double s2b = s_sum;
+    for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / s2b;
+    __threadfence_block();
+    __syncthreads();
+  }
+  // draw and CDF walk (src/sampler.cpp:62-69)
+  double r = 0.0;
+  if (threadIdx.x == 0) {
+    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
+    r = mt_uniform(st);
+  }
+  double cum = 0.0;
+  int pick = keep - 1;  // the first i with r < cum; the last kept id when the sum ends below r
+  serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int first) {
+    const double before = cum;
+    int hit = -1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (u < cnt && hit < 0) {
+        cum = cum + v[u];
+        if (r < cum) hit = u;
+      }
+    }
+    if (hit >= 0) {
+      pick = first + hit;
+      return hit;
+    }
+    return (cum == before && before > 0.0) ? 0 : -1;  // cum is final and r >= cum
+  });
+  if (threadIdx.x == 0) a.out[b] = static_cast<int>(key_id(sorted[pick]));
 }
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
@@ -640,103 +737,70 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   } else {
     if (a.top_k > 0 && a.top_k < V) keep = a.top_k;  // k above the LDS path: full sort, keep k
     for (int i = threadIdx.x; i < a.npow2; i += blockDim.x) keys[i] = i < V ? make_key(work[i], i) : 0ull;
+    if (a.phase == 1) return;  // chunk_sort_kernel, rank_merge_kernel and sample_tail_kernel follow
     __threadfence_block();
     __syncthreads();
     bitonic_global(keys, a.npow2, s_keys);
     sorted = keys;
   }
-  // softmax over the kept ids in double (src/sampler.cpp:42-49); with top-k the kept probabilities
-  // live in LDS, otherwise the sequential loops below stage them through the sort buffer (free
-  // once the keys are sorted)
-  const bool in_lds = topk;
-  if (topk) prob = s_prob;
-  const float mx = key_value(sorted[0]);
-  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(key_value(sorted[i]) - mx));
-  __threadfence_block();
-  __syncthreads();
-  double* stage = reinterpret_cast<double*>(s_keys);
   static_assert(sizeof(s_keys) >= kStage * sizeof(double), "staging buffer");
-  {
-    // thread 0's running sum; a group that leaves it unchanged ends the loop (terms after the
-    // first unchanged one add nothing either, so checking once per group gives the same sum)
-    double sum = 0.0;
-    serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
-      const double before = sum;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u < cnt) sum = sum + v[u];
-      return (sum == before && before > 0.0) ? 0 : -1;
-    });
-    if (threadIdx.x == 0) s_sum = sum;
-    __syncthreads();
-  }
-  const double sum = s_sum;
-  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / sum;
-  __threadfence_block();
-  __syncthreads();
-  if (a.top_p < 1.0f) {  // nucleus (src/sampler.cpp:50-61)
-    double cum = 0.0;
-    const double tp = static_cast<double>(a.top_p);
-    // n = the number of terms taken; once cum is final and below top_p the loop would take all
-    // the running sums of a group in registers; the first that reaches top_p ends the loop, a
-    // group that leaves cum unchanged ends it with all terms kept
-    int n = serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
-      const double before = cum;
-      int hit = -1;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (u < cnt && hit < 0) {
-          cum = cum + v[u];
-          if (cum >= tp) hit = u;
-        }
-      }
-      if (hit >= 0) return hit;
-      return (cum == before && before > 0.0) ? 0 : -1;
-    });
-    if (threadIdx.x == 0) s_keep = n < keep && cum >= tp ? n + 1 : keep;  // cum < tp: every term
-    __syncthreads();
-    const int kp = s_keep > 1 ? s_keep : 1;
-    double s2 = 0.0;
-    serial_loop(prob, kp, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
-      const double before = s2;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u < cnt) s2 = s2 + v[u];
-      return (s2 == before && before > 0.0) ? 0 : -1;
-    });
-    if (threadIdx.x == 0) s_sum = s2;
-    __syncthreads();
-    keep = kp;
-    const double s2b = s_sum;
-    for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = prob[i] / s2b;
-    __threadfence_block();
-    __syncthreads();
-  }
-  // draw and CDF walk (src/sampler.cpp:62-69)
-  double r = 0.0;
-  if (threadIdx.x == 0) {
-    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
-    r = mt_uniform(st);
-  }
-  double cum = 0.0;
-  int pick = keep - 1;  // the first i with r < cum; the last kept id when the sum ends below r
-  serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int first) {
-    const double before = cum;
-    int hit = -1;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (u < cnt && hit < 0) {
-        cum = cum + v[u];
-        if (r < cum) hit = u;
-      }
+  sample_tail(a, b, sorted, keep, topk, prob, s_prob, reinterpret_cast<double*>(s_keys), s_stop, s_sum, s_keep);
+}
+
+// ---- the full sort across workgroups (no top-k, large vocabularies) ---------------------------------
+// Workspace of one sequence: work [V] floats, prob [V] doubles, keys [npow2], merged [npow2].
+__device__ __forceinline__ uint64_t* keys_of(const SampleArgs& a, int b) {
+  uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
+  return reinterpret_cast<uint64_t*>(ws + ((a.vocab * 4 + 255) & ~255) + ((a.vocab * 8 + 255) & ~255));
+}
+__device__ __forceinline__ uint64_t* merged_of(const SampleArgs& a, int b) {
+  return keys_of(a, b) + ((static_cast<size_t>(a.npow2) * 8 + 255) & ~size_t{255}) / 8;
+}
+
+// Each kChunk-key run of the keys sorted in place (descending), one workgroup per run.
+__global__ __launch_bounds__(kThreads) void chunk_sort_kernel(SampleArgs a) {
+  __shared__ uint64_t s_keys[2 * kChunk];
+  bitonic_global(keys_of(a, blockIdx.y) + static_cast<size_t>(blockIdx.x) * kChunk, kChunk, s_keys);
+}
+
+// The sorted runs merged in one pass: key i of run r goes to i + (keys of every run r' < r that are
+// >= it) + (keys of every run r' > r that are > it), counted by binary search in each descending run:
+// the runs' ties resolve by run index, so the positions are a permutation and the result is the
+// descending order.
+__global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
+  const uint64_t* keys = keys_of(a, blockIdx.y);
+  uint64_t* out = merged_of(a, blockIdx.y);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= a.npow2) return;
+  const int runs = a.npow2 / kChunk, r = e / kChunk;
+  const uint64_t x = keys[e];
+  int pos = e - r * kChunk;
+  for (int q = 0; q < runs; ++q) {
+    if (q == r) continue;
+    const uint64_t* run = keys + static_cast<size_t>(q) * kChunk;
+    int lo = 0, hi = kChunk;  // first index whose key is below x (q < r) or not above x (q > r)
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const bool before = q < r ? run[mid] >= x : run[mid] > x;
+      if (before) lo = mid + 1;
+      else hi = mid;
     }
-    if (hit >= 0) {
-      pick = first + hit;
-      return hit;
-    }
-    return (cum == before && before > 0.0) ? 0 : -1;  // cum is final and r >= cum
-  });
-  if (threadIdx.x == 0) a.out[b] = static_cast<int>(key_id(sorted[pick]));
+    pos += lo;
+  }
+  out[pos] = x;
+}
+
+// The sampler after a split sort: the merged keys, every id kept unless top-k (above the LDS path)
+// keeps k.
+__global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
+  __shared__ double s_stage[kStage];
+  __shared__ int s_stop, s_keep;
+  __shared__ double s_sum;
+  const int b = blockIdx.x, V = a.vocab;
+  uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
+  double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));
+  const int keep = a.top_k > 0 && a.top_k < V ? a.top_k : V;
+  sample_tail(a, b, merged_of(a, b), keep, false, prob, nullptr, s_stage, s_stop, s_sum, s_keep);
 }
 
 }  // namespace
@@ -745,7 +809,7 @@ size_t sample_workspace_stride(int vocab) {
   size_t n2 = 1;
   while (n2 < static_cast<size_t>(vocab)) n2 <<= 1;
   const size_t v = static_cast<size_t>(vocab);
-  return ((v * 4 + 255) & ~size_t{255}) + ((v * 8 + 255) & ~size_t{255}) + ((n2 * 8 + 255) & ~size_t{255});
+  return ((v * 4 + 255) & ~size_t{255}) + ((v * 8 + 255) & ~size_t{255}) + 2 * ((n2 * 8 + 255) & ~size_t{255});
 }
 
 int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t s) {
@@ -799,7 +863,18 @@ int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_h
   int n2 = 1;
   while (n2 < vocab) n2 <<= 1;
   a.npow2 = n2;
-  hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  // A full sort of 8K+ keys (sampling without a top-k on the LDS path) runs across workgroups:
+  // the keys, each kChunk run sorted, the runs merged, then the rest of the sampler.
+  const bool topk_lds = cfg.top_k > 0 && cfg.top_k < vocab && cfg.top_k <= kMaxTopK;
+  if (cfg.temperature > 0.0f && !topk_lds && n2 >= 2 * kChunk) {
+    a.phase = 1;
+    hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(chunk_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(rank_merge_kernel, dim3(n2 / 256, batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(sample_tail_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+  }
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }
