@@ -506,15 +506,9 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
     if (threadIdx.x == 0) s_keep = n < keep && cum >= tp ? n + 1 : keep;  // cum < tp: every term
     __syncthreads();
     const int kp = s_keep > 1 ? s_keep : 1;
-    double s2 = 0.0;
-    serial_loop(prob, kp, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
-      const double before = s2;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u < cnt) s2 = s2 + v[u];
-      return (s2 == before && before > 0.0) ? 0 : -1;
-    });
-    if (threadIdx.x == 0) s_sum = s2;
+    // the reference's s2 (the kept terms summed from 0.0 in order, src/sampler.cpp:57-59) adds the
+    // same terms in the same order as cum did up to the cut, so it is cum, bit for bit
+    if (threadIdx.x == 0) s_sum = cum;
     __syncthreads();
     keep = kp;
     const double s2b = s_sum;
