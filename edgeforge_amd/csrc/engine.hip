@@ -52,6 +52,7 @@ struct ef_hip_engine_s {
   void* gemv_ws = nullptr;  // prepared activation fragments of the batched GEMVs (B > 1)
   size_t gemv_ws_bytes = 0;
   int32_t* stage = nullptr;  // pinned host staging
+  int32_t* tok_dev = nullptr;  // device staging of token ids ([batch][n] rows before they move into hist)
   std::vector<void*> allocs;
   std::map<int, hipGraphExec_t> graphs;
   ef_hip_sampler_config scfg{};
@@ -111,6 +112,16 @@ int check_matrix(ef_hip_weight w, size_t rows, size_t cols, const char* what) {
 
 
 int enqueue_tail(ef_hip_engine e, int mode);
+
+// hist[b][pos .. pos + n) = stage[b * n .. b * n + n) for every sequence b: one contiguous copy of
+// the pinned staging words (plus the 8 words after them) to the device, then a row-copy kernel into
+// the history rows.  The caller has filled e->stage and keeps it untouched until the stream syncs.
+int put_tokens(ef_hip_engine e, size_t pos, size_t n) {
+  const size_t words = n * static_cast<size_t>(e->B);
+  EFH_HIP(hipMemcpyAsync(e->tok_dev, e->stage, (words + 8) * 4, hipMemcpyHostToDevice, e->stream));
+  return launch_copy_rows(e->tok_dev, static_cast<long>(n), e->hist + pos, static_cast<long>(e->max_seq),
+                          static_cast<int>(n), e->B, e->stream);
+}
 
 int enqueue_step(ef_hip_engine e, int mode) {
   const ef_hip_model_config& c = e->c;
@@ -231,8 +242,9 @@ int enqueue_prefill(ef_hip_engine e, int n, int mode) {
     return launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, R, D, c.V, s, e->pf_ws, e->pf_ws_bytes);
   }
   if (n > 1) EFH_RC(launch_advance_by(e->pos, n - 1, s));
-  EFH_HIP(hipMemcpy2DAsync(e->x, D * sizeof(float), e->pf_x + (n - 1) * D, n * D * sizeof(float), D * sizeof(float),
-                           B, hipMemcpyDeviceToDevice, s));
+  // the last prompt row of every sequence becomes the decode state
+  EFH_RC(launch_copy_rows(e->pf_x + (n - 1) * D, static_cast<long>(n * D), e->x, static_cast<long>(D),
+                          static_cast<int>(D), B, s));
   return enqueue_tail(e, mode);
 }
 
@@ -466,7 +478,7 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
       (rc = dev_alloc(e, &e->next_tok, B)) || (rc = dev_alloc(e, &e->pos, 1)) ||
       (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S)) ||
       (rc = dev_alloc(e, &e->step_counter, 1)) || (rc = dev_alloc(e, &e->eos_cur, B)) ||
-      (rc = dev_alloc(e, &e->eos_out, B * S))) {
+      (rc = dev_alloc(e, &e->eos_out, B * S)) || (rc = dev_alloc(e, &e->tok_dev, B * S + 8))) {
     return cleanup_fail(rc);
   }
   void* ws = nullptr;
@@ -562,11 +574,11 @@ int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens, size_t pos, in
   if (pos > e->cached)
     return fail(EF_HIP_EINVAL, "forward: position " + std::to_string(pos) + " skips ahead of the " +
                                    std::to_string(e->cached) + " cached tokens");
+  EFH_HIP(hipStreamSynchronize(e->stream));  // the pinned staging buffer is reused below
   for (int b = 0; b < e->B; ++b) e->stage[b] = tokens[b];
   e->stage[e->B] = static_cast<int32_t>(pos);
-  const size_t S = e->max_seq;
-  EFH_HIP(hipMemcpy2DAsync(e->hist + pos, S * 4, e->stage, 4, 4, e->B, hipMemcpyHostToDevice, e->stream));
-  EFH_HIP(hipMemcpyAsync(e->pos, e->stage + e->B, 4, hipMemcpyHostToDevice, e->stream));
+  EFH_RC(put_tokens(e, pos, 1));
+  EFH_HIP(hipMemcpyAsync(e->pos, e->tok_dev + e->B, 4, hipMemcpyDeviceToDevice, e->stream));
   EFH_RC(run_step(e, compute_logits ? kLogits : 0));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->cached = pos + 1;
@@ -587,11 +599,10 @@ int ef_hip_engine_prefill(ef_hip_engine e, const int32_t* tokens, size_t n, size
   if (pos > e->cached)
     return fail(EF_HIP_EINVAL, "prefill: position " + std::to_string(pos) + " skips ahead of the " +
                                    std::to_string(e->cached) + " cached tokens");
-  const size_t S = e->max_seq;
   const int B = e->B;
   EFH_HIP(hipStreamSynchronize(e->stream));  // the pinned staging buffer is reused below
   for (size_t i = 0; i < n * static_cast<size_t>(B); ++i) e->stage[i] = tokens[i];
-  EFH_HIP(hipMemcpy2DAsync(e->hist + pos, S * 4, e->stage, n * 4, n * 4, B, hipMemcpyHostToDevice, e->stream));
+  EFH_RC(put_tokens(e, pos, n));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->stage[0] = static_cast<int32_t>(pos);
   EFH_HIP(hipMemcpyAsync(e->pos, e->stage, 4, hipMemcpyHostToDevice, e->stream));
@@ -641,10 +652,11 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
     pick = kSample;
   }
   // history <- prompt, hist_len <- n_prompt, position 0
+  EFH_HIP(hipStreamSynchronize(e->stream));  // the pinned staging buffer is reused below
   for (int b = 0; b < B; ++b) {
     for (size_t p = 0; p < n_prompt; ++p) e->stage[b * n_prompt + p] = prompt[b * n_prompt + p];
   }
-  EFH_HIP(hipMemcpy2DAsync(e->hist, S * 4, e->stage, n_prompt * 4, n_prompt * 4, B, hipMemcpyHostToDevice, e->stream));
+  EFH_RC(put_tokens(e, 0, n_prompt));
   EFH_HIP(hipStreamSynchronize(e->stream));
   for (int b = 0; b < B; ++b) e->stage[b] = static_cast<int32_t>(n_prompt);
   e->stage[B] = 0;
@@ -677,7 +689,10 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   for (size_t k = 1; k < n; ++k) EFH_HIP(hipGraphLaunch(g_dec, e->stream));
   EFH_HIP(hipStreamSynchronize(e->stream));
   const auto t2 = Clock::now();
-  EFH_HIP(hipMemcpy2DAsync(tokens_out, n * 4, e->out_tokens, S * 4, n * 4, B, hipMemcpyDeviceToHost, e->stream));
+  // [B][S] -> [B][n] on the device, then one contiguous copy to the caller
+  EFH_RC(launch_copy_rows(e->out_tokens, static_cast<long>(S), e->tok_dev, static_cast<long>(n), static_cast<int>(n),
+                          B, e->stream));
+  EFH_HIP(hipMemcpyAsync(tokens_out, e->tok_dev, n * B * 4, hipMemcpyDeviceToHost, e->stream));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->cached = n_prompt + n - 1;
   e->chat_ids.clear();

@@ -43,5 +43,8 @@ int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_
                        long out_ld, const int32_t* n_prompt_dev, int32_t* pos_dev, hipStream_t s,
                        const double* eos_p = nullptr, double* out_eos = nullptr);
 int launch_advance(int32_t* pos_dev, hipStream_t s);
+// dst[r][0..n) = src[r][0..n) for rows r (4-byte words; strides lds / ldd in words), as a kernel:
+// it touches only those words (a strided 2D runtime copy may treat pitch x height as its extent).
+int launch_copy_rows(const void* src, long lds, void* dst, long ldd, int n, int rows, hipStream_t s);
 
 }  // namespace efh

@@ -594,6 +594,16 @@ __global__ void finish_step_kernel(const int32_t* __restrict__ next, int batch, 
 
 __global__ void advance_kernel(int32_t* pos_dev) { *pos_dev += 1; }
 
+// dst[r][c] = src[r][c] for r < rows, c < n (4-byte words, row strides lds / ldd): touches exactly
+// the rows' n words, nothing of the stride gaps.
+__global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* __restrict__ src, long lds,
+                                                        uint32_t* __restrict__ dst, long ldd, int n, int rows) {
+  const int r = blockIdx.y;
+  if (r >= rows) return;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n; c += gridDim.x * blockDim.x)
+    dst[r * ldd + c] = src[r * lds + c];
+}
+
 }  // namespace
 
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
@@ -705,6 +715,15 @@ int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_
                        double* out_eos) {
   hipLaunchKernelGGL(finish_step_kernel, dim3(1), dim3(256), 0, s, next, batch, hist, hist_ld, hist_len, out, out_ld,
                      n_prompt_dev, pos_dev, eos_p, out_eos);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_copy_rows(const void* src, long lds, void* dst, long ldd, int n, int rows, hipStream_t s) {
+  if (n <= 0 || rows <= 0) return EF_HIP_OK;
+  const unsigned gx = static_cast<unsigned>(std::min(16, (n + 255) / 256));
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(gx, rows), dim3(256), 0, s, static_cast<const uint32_t*>(src), lds,
+                     static_cast<uint32_t*>(dst), ldd, n, rows);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }

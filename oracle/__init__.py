@@ -139,8 +139,13 @@ def lib():
     return _LIB
 
 
+def ref_available() -> bool:
+    """Whether the reference build exists, without loading it (test collection stays load-free)."""
+    return os.path.exists(os.path.join(HERE, "_ref", "libefref.so"))
+
+
 def ref():
-    """The reference build, or None when oracle/_ref/libefref.so is absent."""
+    """The reference build, or None when oracle/_ref/libefref.so is absent.  Loaded on first call."""
     global _REF
     if _REF is None:
         path = os.path.join(HERE, "_ref", "libefref.so")

@@ -20,8 +20,7 @@ from edgeforge_amd.qfile import QuantFile
 from oracle.efq import write_efq
 from oracle.model import HostModel
 
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference build) not present")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
 
 TINY32 = Config(D=32, F=64, H=4, KV=2, hd=8, V=40, L=2, max_pos=64)  # tests/test_qinfer.cpp:269-278
 NAMES = ["model.embed_tokens.weight"] + [
@@ -46,7 +45,7 @@ def ours(buf: bytes):
 
 def theirs(buf: bytes):
     err = C.create_string_buffer(1024)
-    n = REF.ref_efq_parse(bytes(buf), len(buf), err, 1024)
+    n = O.ref().ref_efq_parse(bytes(buf), len(buf), err, 1024)
     return (n, None) if n >= 0 else (None, err.value.decode())
 
 
@@ -85,9 +84,9 @@ def test_reader_indexes_a_written_file():
         assert (pol["layers"], pol["lm_head"], pol["embed"], pol["n_overrides"], pol["name"]) == \
             (O.Q4_0, O.Q8_0, O.BF16, 2, "custom")
         f.close()
-        if REF is not None:
+        if O.ref_available():
             bpt, desc = C.c_uint64(), C.create_string_buffer(512)
-            assert REF.ref_model_load_efq(path.encode(), C.byref(bpt), desc, 512) == 0
+            assert O.ref().ref_model_load_efq(path.encode(), C.byref(bpt), desc, 512) == 0
             assert bpt.value == want
             assert desc.value.decode() == "efq, policy custom: 12 Q4_0 + 3 Q8_0 matrices, embedding BF16"
 
@@ -170,7 +169,7 @@ def test_glob_overrides(patterns, msg):
             assert ov and all(x.type == O.Q8_0 for x in ov)
         else:
             assert got[0] is None and msg in got[1]
-        if REF is not None:
+        if O.ref_available():
             assert theirs(buf) == got
 
 
@@ -192,7 +191,7 @@ def test_tied_embeddings_and_bf16_fallback():
         g = QuantFile.open(p2)
         q = g.at("model.layers.0.self_attn.q_proj.weight")
         assert q.type == O.BF16 and q.rule == "fallback-bf16"
-        if REF is not None:
+        if O.ref_available():
             for p in (path, p2):
                 buf = open(p, "rb").read()
                 assert theirs(buf) == ours(buf)
@@ -223,7 +222,7 @@ def test_header_edits_match_the_reference(edit):
             bad = _swap(good, old, new)
         got = ours(bad)
         assert got[0] is None, edit
-        if REF is not None:
+        if O.ref_available():
             want = theirs(bad)
             assert want[0] is None
             if not want[1].startswith("invalid .efq header"):

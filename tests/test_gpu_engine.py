@@ -27,6 +27,29 @@ def _top2_margin(l):
     return float(s[-1] - s[-2])
 
 
+# The reference's near-tie rule for greedy parity (README.md:603-607, src/verify_chat.cpp:193-216):
+# token sequences must be identical, and a difference is tolerated only where the checker's own
+# top-1 / top-2 logit margin at the first differing step is below 1e-3.
+NEAR_TIE = 1e-3
+
+
+def assert_greedy_identical(got, want, want_logits, label=""):
+    """Identical greedy ids, or a first difference at a near-tie of the oracle's logits (then the
+    rest of the sequence is not comparable).  Returns (minimum top-2 margin over the compared steps,
+    first differing step or None)."""
+    got = [int(v) for v in got]
+    want = [int(v) for v in want]
+    margins = [_top2_margin(l) for l in want_logits[:len(want)]]
+    k = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+    if k is None:
+        print(f"{label} greedy ids identical over {len(want)} steps; min top-2 margin {min(margins):.3e}", flush=True)
+        return min(margins), None
+    assert margins[k] < NEAR_TIE, (f"{label} greedy ids differ at step {k} ({got[k]} vs {want[k]}) where the "
+                                   f"oracle's top-2 margin {margins[k]:.3e} is not a near-tie (< {NEAR_TIE})")
+    print(f"{label} near-tie flip at step {k}: margin {margins[k]:.3e} (tolerated, README.md:603-607)", flush=True)
+    return min(margins[:k + 1]), k
+
+
 @pytest.mark.parametrize("cfg,q8", [(SMALL, {(0, "wk"), (1, "wv"), (2, "w_down")}), (ODD, {(1, "wq")}),
                                     (WIDE, {(0, "wo")})])
 def test_forward_logits_match_oracle_each_position(hip, cfg, q8):
@@ -77,9 +100,9 @@ def test_config5_greedy_32_steps_identical(tinyllama):
     want, want_logits, _, _ = om.run_once(prompt, 32)
     eng = Engine(dm, max_seq=23 + 32)
     got, pre, dec = eng.generate([prompt], 32)
-    margins = [_top2_margin(l) for l in want_logits]
-    print(f"greedy tokens {got[0].tolist()}\nmin top-2 margin {min(margins):.3e}", flush=True)
-    assert got[0].tolist() == want.tolist()
+    print(f"greedy tokens {got[0].tolist()}", flush=True)
+    _, flip = assert_greedy_identical(got[0], want, want_logits, "config 5 B=1:")
+    assert flip is None or flip > 0
     # logits of every decode step (teacher-forced on the same tokens)
     seq = prompt + want.tolist()
     for p in range(len(prompt) + 31):
@@ -126,6 +149,81 @@ def test_config5_sampled_generation_replays_on_cpu(tinyllama, hip):
             assert tok == int(got[0][k]), k
             seq.append(tok)
     eng.close()
+
+
+# Sequences checked against the oracle in the batched config-5 runs: spread over the batch,
+# including the first and the last.
+def _checked(B):
+    return sorted({0, B - 1, *range(0, B, max(1, B // 8))})
+
+
+def _teacher_forced_logits(eng, toks_by_pos, first):
+    """Logits of every sequence at positions first .. len(toks_by_pos)-1, each position run through
+    the engine's one-position batched step on the given tokens: {position: [B][V]}."""
+    out = {}
+    for p, t in enumerate(toks_by_pos):
+        eng.forward(t, p, compute_logits=p >= first)
+        if p >= first:
+            out[p] = eng.logits()
+    return out
+
+
+@pytest.mark.parametrize("B", [16, 64])
+def test_config5_batched_greedy_32_steps_match_oracle(tinyllama, B):
+    """Config 5 at B=16 and B=64 (config 4's shapes: the matrix-core GEMV with the K split, the
+    KV-group attention, the batched argmax): independent prompts, 32 greedy steps.  Spread sequences
+    (first and last included) match the oracle's run_once token for token (src/bench_decode.cpp:30-49,
+    src/model.cpp:184-276), and their logits at every decode step are within 1e-4 relative."""
+    dm, om = tinyllama
+    n = 32
+    prompts = D.rng(500 + B).integers(0, 32000, size=(B, 23)).astype(np.int32)
+    print(f"[case] config-5 greedy decode at B={B}", flush=True)
+    eng = Engine(dm, max_seq=23 + n, batch=B)
+    got, _, _ = eng.generate(prompts, n)
+    check = _checked(B)
+    want = {}
+    for b in check:
+        toks, logits, _, _ = om.run_once(prompts[b], n)
+        want[b] = (toks, logits)
+        _, flip = assert_greedy_identical(got[b], toks, logits, f"config 5 B={B} seq {b}:")
+        assert flip is None or flip > 0, b
+    # every decode step's logits on the generated tokens (teacher forced, all sequences at once)
+    seqs = np.concatenate([prompts, got], axis=1)
+    tf = _teacher_forced_logits(eng, [seqs[:, p] for p in range(23 + n - 1)], 22)
+    worst = 0.0
+    for b in check:
+        toks, logits = want[b]
+        if got[b].tolist() != toks.tolist():
+            continue  # a tolerated near-tie: the oracle followed another sequence
+        for k in range(n):
+            e = _logit_err(tf[22 + k][b], logits[k])
+            worst = max(worst, e)
+            assert e < 1e-4, (b, k, e)
+    print(f"B={B}: worst relative logit error over {len(check)} sequences x {n} steps {worst:.2e}", flush=True)
+    eng.close()
+
+
+def test_config5_batched_sampled_replays_on_cpu(tinyllama, hip):
+    """Config 5 at B=64 with config 3's sampler (T 0.8, top-k 40, top-p 0.95, penalty 1.1 over the
+    context), one seed per sequence: every id of every sequence equals the CPU Sampler's pick
+    (src/sampler.cpp:13-70, one Sampler per sequence) on the device's own logits of that step."""
+    dm, _ = tinyllama
+    B, n = 64, 32
+    cfg = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
+    prompts = D.rng(700).integers(0, 32000, size=(B, 23)).astype(np.int32)
+    seeds = [9000 + 31 * b for b in range(B)]
+    print("[case] config-5 sampled decode at B=64", flush=True)
+    eng = Engine(dm, max_seq=23 + n, batch=B)
+    got, _, _ = eng.generate(prompts, n, sampler=cfg, rng=hip.RngStates(seeds))
+    seqs = np.concatenate([prompts, got], axis=1)
+    tf = _teacher_forced_logits(eng, [seqs[:, p] for p in range(23 + n - 1)], 22)
+    eng.close()
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    for k in range(n):
+        for b in range(B):
+            hist = seqs[b, :23 + k]
+            tok = cpu[b].sample(tf[22 + k][b], hist)
+            assert tok == int(got[b][k]), (b, k)
 
 
 def test_engine_rejects_bad_tokens_and_positions(tinyllama):

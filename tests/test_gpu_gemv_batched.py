@@ -32,6 +32,12 @@ def _batch_x(seed, batch, cols):
     (O.Q4_0, 96, 512, 300),      # 19 sequence tiles in one launch
     (O.Q8_0, 37, 256, 1100),     # two launches (1024 + 76 sequences)
     (O.Q8_0, 64, 512, 2),
+    (O.Q4_0, 5632, 2048, 16),    # config 4 at B = 16: gate / up shape
+    (O.Q4_0, 2048, 5632, 16),    # down shape (K = 5632)
+    (O.Q8_0, 256, 2048, 16),     # a Q8_0 k / v override
+    (O.Q4_0, 2048, 2048, 16),    # q / o shape
+    (O.Q4_0, 5632, 2048, 64),    # config 4 at B = 64
+    (O.Q8_0, 256, 2048, 64),
 ])
 def test_batched_gemv_each_sequence_meets_the_gates(hip, qtype, rows, cols, batch):
     print(f"[case] batched gemv qtype={qtype} {rows}x{cols} B={batch}", flush=True)

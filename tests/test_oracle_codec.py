@@ -15,8 +15,7 @@ import pytest
 import oracle as O
 
 L = O.lib()
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference build) not present")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "fixtures.json")))
 
 
@@ -94,13 +93,13 @@ def test_bf16_round_trip_and_rounding():  # tests/test_fp16.cpp:17-60
 @needs_ref
 def test_fp16_bf16_match_reference_build():
     h, got = f16_all()
-    ref = np.array([REF.ref_fp16_to_f32(int(v)) for v in h], np.float32)
+    ref = np.array([O.ref().ref_fp16_to_f32(int(v)) for v in h], np.float32)
     assert np.array_equal(np.isnan(got), np.isnan(ref))
     ok = ~np.isnan(ref)
     assert np.array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
     f = np.random.default_rng(3).integers(0, 2 ** 32, 20000, dtype=np.uint64).astype(np.uint32).view(np.float32)
-    assert [REF.ref_f32_to_fp16(float(v)) for v in f] == to_fp16(f).tolist()
-    assert [REF.ref_f32_to_bf16(float(v)) for v in f] == to_bf16(f).tolist()
+    assert [O.ref().ref_f32_to_fp16(float(v)) for v in f] == to_fp16(f).tolist()
+    assert [O.ref().ref_f32_to_bf16(float(v)) for v in f] == to_bf16(f).tolist()
 
 
 # ---------------------------------------------------------------------------------- block codec
@@ -220,7 +219,7 @@ def test_quantizer_bytes_match_reference_build(qtype, search):
         got = O.quantize(qtype, w, search=search)
         want = np.empty_like(got)
         for r in range(w.shape[0]):
-            assert REF.ref_quantize_row(qtype, O.ptr(w[r], O._f32p), 256, O.ptr(want[r]), int(search)) == 0
+            assert O.ref().ref_quantize_row(qtype, O.ptr(w[r], O._f32p), 256, O.ptr(want[r]), int(search)) == 0
         assert np.array_equal(got, want), seed
 
 

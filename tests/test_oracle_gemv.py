@@ -16,8 +16,7 @@ import oracle as O
 from tests import _data as D
 
 L = O.lib()
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference build) not present")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "fixtures.json")))
 
 
@@ -116,7 +115,7 @@ def test_gemv_bit_identical_to_reference_build(threads):
                 ref = O.ref_matvec_jobs([(qt, W, x)], backend=backend, threads=threads)[0]
                 assert np.array_equal(mine.view(np.uint32), ref.view(np.uint32)), (qt, n, backend)
             for r in (0, 39):
-                f = REF.ref_dot_q4_0 if qt == O.Q4_0 else REF.ref_dot_q8_0
+                f = O.ref().ref_dot_q4_0 if qt == O.Q4_0 else O.ref().ref_dot_q8_0
                 assert np.float32(f(O.ptr(W[r], O._u8p), O.ptr(x, O._f32p), n)) == np.float32(dot(qt, W[r], x, 0))
 
 

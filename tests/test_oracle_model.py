@@ -20,8 +20,7 @@ from oracle.efq import write_efq
 from oracle.model import HostModel, OracleModel
 
 L = O.lib()
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference build) not present")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "fixtures.json")))
 F = O._f32p
 
@@ -122,18 +121,18 @@ def test_glue_kernels_bit_identical_to_reference_build():
     w = (1 + 0.1 * g.standard_normal(2048)).astype(np.float32)
     a, b = np.empty_like(x), np.empty_like(x)
     L.efo_rmsnorm(O.ptr(a, F), O.ptr(x, F), O.ptr(w, F), 2048, 1e-5)
-    REF.ref_rmsnorm(O.ptr(b, F), O.ptr(x, F), O.ptr(w, F), 2048, 1e-5)
+    O.ref().ref_rmsnorm(O.ptr(b, F), O.ptr(x, F), O.ptr(w, F), 2048, 1e-5)
     assert np.array_equal(a, b)
     for v in g.standard_normal(200).astype(np.float32) * 20:
-        assert np.float32(L.efo_silu(float(v))) == np.float32(REF.ref_silu(float(v)))
+        assert np.float32(L.efo_silu(float(v))) == np.float32(O.ref().ref_silu(float(v)))
     inv, c, s = rope_tables(64, 64, 10000.0)
     inv2, c2, s2 = np.empty_like(inv), np.empty_like(c), np.empty_like(s)
-    REF.ref_rope_table(O.ptr(inv2, F), O.ptr(c2, F), O.ptr(s2, F), 64, 64, 10000.0)
+    O.ref().ref_rope_table(O.ptr(inv2, F), O.ptr(c2, F), O.ptr(s2, F), 64, 64, 10000.0)
     assert np.array_equal(inv, inv2) and np.array_equal(c, c2) and np.array_equal(s, s2)
     H, KV, hd, T = 32, 4, 64, 40
     q, k, v = (g.standard_normal(n).astype(np.float32) for n in (H * hd, T * KV * hd, T * KV * hd))
     out_ref, sc = np.empty(H * hd, np.float32), np.empty(T, np.float32)
-    REF.ref_attention(O.ptr(out_ref, F), O.ptr(q, F), O.ptr(k, F), O.ptr(v, F), T, H, KV, hd, O.ptr(sc, F))
+    O.ref().ref_attention(O.ptr(out_ref, F), O.ptr(q, F), O.ptr(k, F), O.ptr(v, F), T, H, KV, hd, O.ptr(sc, F))
     assert np.array_equal(attention(q, k, v, T, H, KV, hd), out_ref)
 
 
@@ -148,19 +147,19 @@ def test_transformer_logits_bit_identical_to_reference_engine(backend):
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "tiny.efq")
         write_efq(path, TINY, hm.efq_tensors())
-        e = REF.ref_engine_open(path.encode(), 16, 3, backend)
+        e = O.ref().ref_engine_open(path.encode(), 16, 3, backend)
         assert e, "reference engine rejected the .efq file"
-        bpt = REF.ref_engine_bytes_per_token(e)
+        bpt = O.ref().ref_engine_bytes_per_token(e)
         ot = om.transformer(16, threads=2, backend=backend)
         ids = [1, 5, 9, 33, 2, 17, 17, 4, 30, 12]
         for p, t in enumerate(ids):
             want = np.empty(TINY.V, np.float32)
-            assert REF.ref_engine_forward(e, t, p, 1, O.ptr(want, F)) == 0
+            assert O.ref().ref_engine_forward(e, t, p, 1, O.ptr(want, F)) == 0
             got = ot.forward(t, p)
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), p
-        assert REF.ref_engine_forward(e, TINY.V, 0, 1, None) == -1  # token out of range throws
-        assert REF.ref_engine_forward(e, 1, 12, 1, None) == -1  # skipping ahead throws
-        REF.ref_engine_close(e)
+        assert O.ref().ref_engine_forward(e, TINY.V, 0, 1, None) == -1  # token out of range throws
+        assert O.ref().ref_engine_forward(e, 1, 12, 1, None) == -1  # skipping ahead throws
+        O.ref().ref_engine_close(e)
         ot.close()
     assert bpt == sum(hm.host_bytes(k).nbytes for k in hm.weights if k != "embed") + (2 * TINY.L + 1) * TINY.D * 4
 

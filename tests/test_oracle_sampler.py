@@ -17,8 +17,7 @@ import pytest
 import oracle as O
 
 L = O.lib()
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference build) not present")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "fixtures.json")))
 
 
@@ -51,10 +50,10 @@ def test_canonical_double_closed_form():
 def test_rng_matches_the_library():
     n = 5000
     ref_w = np.empty(n, np.uint64)
-    REF.ref_mt64_words(42, n, O.ptr(ref_w, O._u64p))
+    O.ref().ref_mt64_words(42, n, O.ptr(ref_w, O._u64p))
     assert words(42, n) == ref_w.tolist()
     ref_u = np.empty(n, np.float64)
-    REF.ref_uniform_doubles(42, n, O.ptr(ref_u, O._f64p))
+    O.ref().ref_uniform_doubles(42, n, O.ptr(ref_u, O._f64p))
     g = Mt()
     L.efo_mt64_seed(C.byref(g), 42)
     assert [L.efo_canonical_double(C.byref(g)) for _ in range(n)] == ref_u.tolist()
