@@ -121,6 +121,8 @@ SIGNATURES = {
     "ef_hip_sample_workspace_bytes": (_sz, [_sz, C.c_int]),
     "ef_hip_sample": (C.c_int, [_P, _sz, C.c_int, _sz, C.POINTER(ef_hip_sampler_config), _P, _P, _sz, _P, _P, _P,
                                 _P]),
+    "ef_hip_sample_noalloc": (C.c_int, [_P, _sz, C.c_int, _sz, C.POINTER(ef_hip_sampler_config), _P, _P, _sz, _P,
+                                        _P, _P]),
     "ef_hip_argmax": (C.c_int, [_P, _sz, C.c_int, _sz, _P, _P]),
     "ef_hip_profile_matvec": (C.c_int, [C.c_int, C.POINTER(_P), C.POINTER(_P), _sz, _P, _P, C.c_float, _P, C.c_int,
                                         C.c_int, _P, _f32p]),

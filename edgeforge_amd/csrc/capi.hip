@@ -15,6 +15,16 @@ namespace efh {
 namespace {
 thread_local std::string t_last_error;
 Context g_ctx;
+
+// Scratch of the no-allocation sampler entry point (ef_hip_sample_noalloc): a file-scope device
+// array, one copy per GPU the library runs on, held until the process ends.  Host code never uses
+// the array's name as an address (on the host it is only a stand-in for the symbol): ef_hip_init
+// resolves each device's own copy with hipGetSymbolAddress and every later use goes through that
+// pointer.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+void* g_scratch_dev[kMaxScratchDevices] = {};
 }  // namespace
 
 void set_error(const std::string& msg) { t_last_error = msg; }
@@ -78,6 +88,11 @@ int ef_hip_init(int device) {
     return fail(EF_HIP_ENODEV, std::string("this build targets gfx950 (MI355X); device is ") + prop.gcnArchName);
   }
   EFH_HIP(hipSetDevice(device));
+  if (device < kMaxScratchDevices && g_scratch_dev[device] == nullptr) {  // once per device, device current
+    void* p = nullptr;
+    EFH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_dev[device] = p;
+  }
   EFH_HIP(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   g_ctx.device = device;
   g_ctx.cu_count = prop.multiProcessorCount;
@@ -482,16 +497,24 @@ void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
 }  // namespace
 
-int ef_hip_sample(const float* logits, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
-                  const int32_t* hist, const int32_t* hist_len, size_t hist_ld, void* rng, int32_t* out, void* ws,
-                  void* stream) {
-  EFH_READY();
+namespace {
+int check_sample_args(const float* logits, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
+                      const int32_t* hist, const int32_t* hist_len, void* rng, int32_t* out) {
   EFH_CHECK(logits && cfg && out, "sample: null pointer");
   if (vocab == 0) return fail(EF_HIP_EINVAL, "sampler: empty vocabulary");  // src/sampler.cpp:14
   EFH_CHECK(vocab <= (1u << 24), "sample: vocab above 2^24");
   EFH_CHECK(batch >= 1 && batch <= 65535 && (batch == 1 || ld >= vocab), "sample: bad batch / ld");
   EFH_CHECK(cfg->temperature <= 0.0f || rng != nullptr, "sample: temperature > 0 needs an rng state");
   EFH_CHECK(cfg->repetition_penalty == 1.0f || (hist && hist_len), "sample: penalty needs a history");
+  return EF_HIP_OK;
+}
+}  // namespace
+
+int ef_hip_sample(const float* logits, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
+                  const int32_t* hist, const int32_t* hist_len, size_t hist_ld, void* rng, int32_t* out, void* ws,
+                  void* stream) {
+  EFH_READY();
+  EFH_RC(check_sample_args(logits, vocab, batch, ld, cfg, hist, hist_len, rng, out));
   hipStream_t s = pick(stream);
   if (ws == nullptr) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -508,6 +531,28 @@ int ef_hip_sample(const float* logits, size_t vocab, int batch, size_t ld, const
   }
   return launch_sample(logits, static_cast<int>(vocab), batch, static_cast<long>(ld), *cfg, hist, hist_len,
                        static_cast<long>(hist_ld), rng, out, ws, s);
+}
+
+// ef_hip_sample over the library's fixed device scratch: no allocation of any kind.  The kernels
+// write every workspace word they later read, so the scratch needs no clearing between calls.
+int ef_hip_sample_noalloc(const float* logits, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
+                          const int32_t* hist, const int32_t* hist_len, size_t hist_ld, void* rng, int32_t* out,
+                          void* stream) {
+  EFH_READY();
+  EFH_RC(check_sample_args(logits, vocab, batch, ld, cfg, hist, hist_len, rng, out));
+  const size_t need = ef_hip_sample_workspace_bytes(vocab, batch);
+  if (need > kScratchBytes) {
+    const size_t per = ef_hip_sample_workspace_bytes(vocab, 1);
+    return fail(EF_HIP_EINVAL, "sample_noalloc: " + std::to_string(batch) + " sequences of vocab " +
+                                   std::to_string(vocab) + " need " + std::to_string(need) +
+                                   " bytes of scratch, above the fixed " + std::to_string(kScratchBytes) +
+                                   " (at most " + std::to_string(kScratchBytes / per) +
+                                   " sequences of this vocab); use ef_hip_sample with a workspace");
+  }
+  void* ws = g_ctx.device < kMaxScratchDevices ? g_scratch_dev[g_ctx.device] : nullptr;
+  EFH_CHECK(ws != nullptr, "sample_noalloc: no scratch on this device (device index above 63)");
+  return launch_sample(logits, static_cast<int>(vocab), batch, static_cast<long>(ld), *cfg, hist, hist_len,
+                       static_cast<long>(hist_ld), rng, out, ws, pick(stream));
 }
 
 }  // extern "C"

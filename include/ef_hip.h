@@ -141,6 +141,15 @@ size_t ef_hip_sample_workspace_bytes(size_t vocab, int batch);
 int ef_hip_sample(const float* logits_dev, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
                   const int32_t* hist_dev, const int32_t* hist_len_dev, size_t hist_ld, void* rng_dev,
                   int32_t* out_dev, void* ws_dev, void* stream);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): ef_hip_sample with the
+ * library's own fixed scratch, a 16 MiB device array per GPU held until the process ends, and no
+ * allocation of any kind.  Sizes whose workspace (ef_hip_sample_workspace_bytes) exceeds 16 MiB are
+ * rejected with EF_HIP_EINVAL (at vocab 32000: at most 18 sequences per call).  Every call on one
+ * GPU shares that scratch: calls that overlap on one GPU (other streams, other threads) race. */
+int ef_hip_sample_noalloc(const float* logits_dev, size_t vocab, int batch, size_t ld, const ef_hip_sampler_config* cfg,
+                          const int32_t* hist_dev, const int32_t* hist_len_dev, size_t hist_ld, void* rng_dev,
+                          int32_t* out_dev, void* stream);
 /* kern::argmax (src/kernels.cpp:105-111): first maximum wins. */
 int ef_hip_argmax(const float* x_dev, size_t n, int batch, size_t ld, int32_t* out_dev, void* stream);
 
