@@ -94,6 +94,41 @@ def profile_plain(H, L, model, key, qtype, block, batch: int, launches: int = 40
     return avg.value, gemv_bytes(w0.rows, w0.cols, block, batch=batch)
 
 
+def group_weight_bytes(cfg) -> dict:
+    """Packed weight bytes each kernel group streams per step (run_profile's bytes[],
+    src/bench_decode.cpp:170-179)."""
+    from edgeforge_amd.model import TINYLLAMA_Q8, _packed_row_bytes
+    import edgeforge_amd._lib as EL
+
+    def mat(l, name):
+        r, c = cfg.shape(name)
+        return r * _packed_row_bytes(EL.Q8_0 if (l, name) in TINYLLAMA_Q8 else EL.Q4_0, c)
+
+    b = {"qkv": 0, "o_proj": 0, "gate_up": 0, "down": 0}
+    for l in range(cfg.L):
+        b["qkv"] += mat(l, "wq") + mat(l, "wk") + mat(l, "wv")
+        b["o_proj"] += mat(l, "wo")
+        b["gate_up"] += mat(l, "w_gate") + mat(l, "w_up")
+        b["down"] += mat(l, "w_down")
+    b["lm_head"] = cfg.V * _packed_row_bytes(EL.Q8_0, cfg.D)
+    return b
+
+
+def step_profile(eng, ms_per_step: float, cfg, sampler=None, rng=None, reps: int = 20) -> dict:
+    """Per-group decode-step breakdown (ef_hip_engine_profile): microseconds per step of each group,
+    their sum against the timed step, and the weight GB/s of each GEMV group."""
+    prof = eng.profile(reps=reps, sampler=sampler, rng=rng)
+    wb = group_weight_bytes(cfg)
+    total = sum(prof.values())
+    out = {"us": {g: round(v * 1e3, 2) for g, v in prof.items()},
+           "sum_ms": round(total, 4), "step_ms": round(ms_per_step, 4),
+           "sum_over_step": round(total / ms_per_step, 4),
+           "weight_gbs": {g: round(wb[g] / (prof[g] * 1e-3) / 1e9, 1) for g in wb}}
+    log(f"[bench] step profile: " + ", ".join(f"{g} {v * 1e3:.1f}us" for g, v in prof.items()) +
+        f"; sum {total:.4f} ms vs step {ms_per_step:.4f} ms")
+    return out
+
+
 CPU_RUNS = {"threads": 7, "one": 3}  # timed runs per thread count; the medians are reported
 
 
@@ -212,12 +247,14 @@ def main() -> int:
     eng = Engine(model, max_seq=23 + max(K, W) + 1)
     eng.generate([prompt], W + 1)
     toks, pre_s, dec_s = eng.generate([prompt], K + 1)
+    prof_b1 = step_profile(eng, dec_s / K * 1e3, TINYLLAMA)
     eng.close()
     tps = K / dec_s
     log(f"[bench] B=1 decode: {K} steps in {dec_s * 1e3:.2f} ms -> {tps:.1f} tok/s "
         f"({tps * wbytes / 1e9:.1f} GB/s of weights)")
 
-    extra = {"prefill_b1_ms": round(pre_s * 1e3, 3), "prefill_b1_tok_s": round(len(prompt) / pre_s, 1)}
+    extra = {"prefill_b1_ms": round(pre_s * 1e3, 3), "prefill_b1_tok_s": round(len(prompt) / pre_s, 1),
+             "step_profile_b1": prof_b1}
     log(f"[bench] B=1 prefill (23 positions, batched, incl. the first pick): {pre_s * 1e3:.3f} ms")
     # config 5's sampled decode (config 3's sampler: T 0.8, top-k 40, top-p 0.95, penalty 1.1)
     samp = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
@@ -233,6 +270,7 @@ def main() -> int:
         eng = Engine(model, max_seq=23 + max(K, W) + 1, batch=B)
         eng.generate(prompts, W + 1)
         _, pre64, dec64 = eng.generate(prompts, K + 1)
+        extra["step_profile_b64"] = step_profile(eng, dec64 / K * 1e3, TINYLLAMA)
         seeds = list(range(100, 100 + B))
         eng.generate(prompts, W + 1, sampler=samp, rng=H.RngStates(seeds))
         _, _, sdec64 = eng.generate(prompts, K + 1, sampler=samp, rng=H.RngStates(seeds))

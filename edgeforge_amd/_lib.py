@@ -129,6 +129,8 @@ SIGNATURES = {
     "ef_hip_engine_create": (C.c_int, [C.POINTER(ef_hip_model_config), C.POINTER(ef_hip_layer), _P, _P, _P, _sz,
                                        C.c_int, C.POINTER(_P)]),
     "ef_hip_engine_destroy": (C.c_int, [_P]),
+    "ef_hip_engine_profile": (C.c_int, [_P, C.POINTER(ef_hip_sampler_config), _P, C.c_int,
+                                        C.POINTER(C.c_double)]),
     "ef_hip_engine_forward": (C.c_int, [_P, _i32p, _sz, C.c_int]),
     "ef_hip_engine_prefill": (C.c_int, [_P, _i32p, _sz, _sz, C.c_int]),
     "ef_hip_engine_logits": (C.c_int, [_P, C.POINTER(_P)]),

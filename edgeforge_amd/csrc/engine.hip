@@ -30,6 +30,20 @@
 namespace {
 constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
 enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32, kAllLogits = 64 };
+// Kernel groups of a decode step (the reference's ForwardProfile buckets, include/ef/model.h:89-94,
+// merged where this build fuses them): a step enqueues the groups its mask selects, so a profile
+// can capture and time each group's launches on their own.
+enum StepGroup : unsigned {
+  kGEmbed = 1u << EF_HIP_PROF_EMBED,
+  kGQkv = 1u << EF_HIP_PROF_QKV,
+  kGAttn = 1u << EF_HIP_PROF_ATTENTION,
+  kGOproj = 1u << EF_HIP_PROF_OPROJ,
+  kGGateUp = 1u << EF_HIP_PROF_GATE_UP,
+  kGDown = 1u << EF_HIP_PROF_DOWN,
+  kGLmHead = 1u << EF_HIP_PROF_LM_HEAD,
+  kGPick = 1u << EF_HIP_PROF_PICK,
+  kAllGroups = (1u << EF_HIP_PROF_GROUPS) - 1u,
+};
 // Rows (sequences x positions) of one batched prefill launch; longer prompts go in chunks.
 constexpr size_t kPrefillRows = 4096;
 }  // namespace
@@ -111,7 +125,7 @@ int check_matrix(ef_hip_weight w, size_t rows, size_t cols, const char* what) {
 }
 
 
-int enqueue_tail(ef_hip_engine e, int mode);
+int enqueue_tail(ef_hip_engine e, int mode, unsigned groups = kAllGroups);
 
 // hist[b][pos .. pos + n) = stage[b * n .. b * n + n) for every sequence b: one contiguous copy of
 // the pinned staging words (plus the 8 words after them) to the device, then a row-copy kernel into
@@ -123,12 +137,13 @@ int put_tokens(ef_hip_engine e, size_t pos, size_t n) {
                           static_cast<int>(n), e->B, e->stream);
 }
 
-int enqueue_step(ef_hip_engine e, int mode) {
+int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   const ef_hip_model_config& c = e->c;
   const int B = e->B;
   const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
   hipStream_t s = e->stream;
-  EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s));
+  if (groups & kGEmbed)
+    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s));
   AttnArgs a{};
   a.q = e->q;
   a.knew = e->knew;
@@ -148,31 +163,36 @@ int enqueue_step(ef_hip_engine e, int mode) {
     const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, D, D},
                             {w.wk, nullptr, e->x, e->knew, D, kvd},
                             {w.wv, nullptr, e->x, e->vnew, D, kvd}};
-    EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
+    if (groups & kGQkv)
+      EFH_RC(launch_gemv(qkv, 3, kEpiStore, w.attn_norm_dev, c.eps, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
     a.kcache = e->kc + l * B * S * kvd;
     a.vcache = e->vc + l * B * S * kvd;
-    EFH_RC(launch_attention(a, B, s));
+    if (groups & kGAttn) EFH_RC(launch_attention(a, B, s));
     const GemvJob o{w.wo, nullptr, e->ctx, e->x, D, D};
-    EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
+    if (groups & kGOproj)
+      EFH_RC(launch_gemv(&o, 1, kEpiResidual, nullptr, 0.0f, B, D, D, s, e->gemv_ws, e->gemv_ws_bytes));
     const GemvJob gu{w.w_gate, w.w_up, e->x, e->act, D, F};
-    EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, B, D, F, s, e->gemv_ws, e->gemv_ws_bytes));
+    if (groups & kGGateUp)
+      EFH_RC(launch_gemv(&gu, 1, kEpiSwiglu, w.ffn_norm_dev, c.eps, B, D, F, s, e->gemv_ws, e->gemv_ws_bytes));
     const GemvJob dn{w.w_down, nullptr, e->act, e->x, F, D};
-    EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s, e->gemv_ws, e->gemv_ws_bytes));
+    if (groups & kGDown)
+      EFH_RC(launch_gemv(&dn, 1, kEpiResidual, nullptr, 0.0f, B, F, D, s, e->gemv_ws, e->gemv_ws_bytes));
   }
-  return enqueue_tail(e, mode);
+  return enqueue_tail(e, mode, groups);
 }
 
 // After the layers: final RMSNorm + lm_head, then the token pick and the step bookkeeping, or
 // only the position advance (a prompt position whose logits are not needed).
-int enqueue_tail(ef_hip_engine e, int mode) {
+int enqueue_tail(ef_hip_engine e, int mode, unsigned groups) {
   const ef_hip_model_config& c = e->c;
   const int B = e->B;
   const size_t D = c.D, V = c.V, S = e->max_seq;
   hipStream_t s = e->stream;
-  if (mode & kLogits) {
+  if ((mode & kLogits) && (groups & kGLmHead)) {
     const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, D, V};
     EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s, e->gemv_ws, e->gemv_ws_bytes));
   }
+  if (!(groups & kGPick)) return EF_HIP_OK;
   if (mode & (kGreedy | kSample)) {
     if (mode & kGreedy) {
       StepArgs f{e->next_tok, e->hist, static_cast<long>(S), e->hist_len, e->out_tokens, static_cast<long>(S),
@@ -699,6 +719,75 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
   if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
   return EF_HIP_OK;
+}
+
+int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, void* rng, int reps, double* ms_out) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(ms_out != nullptr && reps >= 1 && reps <= 100000, "engine_profile: null output or reps not in [1, 1e5]");
+  EFH_CHECK(e->cached >= 1, "engine_profile: no cached position (run forward, prefill or generate first)");
+  int pick = kGreedy;
+  if (cfg != nullptr && cfg->temperature > 0.0f) {
+    EFH_CHECK(rng != nullptr, "engine_profile: sampling needs rng states");
+    EFH_RC(set_sampler(e, *cfg, rng));
+    pick = kSample;
+  }
+  const int mode = kLogits | pick;
+  // every group runs at position P (its token and cache rows are in bounds); only the pick group
+  // moves the position, and it is put back after each group
+  const int32_t P = static_cast<int32_t>(std::min(e->cached, e->max_seq - 1));
+  auto set_pos = [&]() -> int {
+    EFH_HIP(hipStreamSynchronize(e->stream));
+    e->stage[0] = P;
+    EFH_HIP(hipMemcpyAsync(e->pos, e->stage, 4, hipMemcpyHostToDevice, e->stream));
+    EFH_HIP(hipStreamSynchronize(e->stream));
+    return EF_HIP_OK;
+  };
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  EFH_HIP(hipEventCreate(&ev0));
+  if (hipEventCreate(&ev1) != hipSuccess) {
+    (void)hipEventDestroy(ev0);
+    return fail(EF_HIP_ERUNTIME, "engine_profile: hipEventCreate");
+  }
+  int rc = EF_HIP_OK;
+  for (int g = 0; g < EF_HIP_PROF_GROUPS && rc == EF_HIP_OK; ++g) {
+    hipGraphExec_t ex = nullptr;
+    rc = set_pos();
+    if (rc != EF_HIP_OK) break;
+    if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      rc = fail(EF_HIP_ERUNTIME, "engine_profile: hipStreamBeginCapture");
+      break;
+    }
+    // the group's launches kInGraph times in one graph, so one graph launch's host-side cost is
+    // spread over as many steps' worth of work (a step graph pays it once per step)
+    constexpr int kInGraph = 8;
+    for (int k = 0; k < kInGraph && rc == EF_HIP_OK; ++k) rc = enqueue_step(e, mode, 1u << g);
+    hipGraph_t gr = nullptr;
+    const hipError_t ec = hipStreamEndCapture(e->stream, &gr);
+    if (rc == EF_HIP_OK && ec != hipSuccess) rc = fail_hip(ec, "hipStreamEndCapture");
+    if (rc == EF_HIP_OK) {
+      const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+      if (ei != hipSuccess) rc = fail_hip(ei, "hipGraphInstantiate");
+    }
+    if (gr) (void)hipGraphDestroy(gr);
+    float ms = 0.0f;
+    if (rc == EF_HIP_OK) {
+      hipError_t he = hipSuccess;
+      for (int w = 0; w < 3 && he == hipSuccess; ++w) he = hipGraphLaunch(ex, e->stream);  // warm-up
+      if (he == hipSuccess) he = hipEventRecord(ev0, e->stream);
+      for (int r = 0; r < reps && he == hipSuccess; ++r) he = hipGraphLaunch(ex, e->stream);
+      if (he == hipSuccess) he = hipEventRecord(ev1, e->stream);
+      if (he == hipSuccess) he = hipEventSynchronize(ev1);
+      if (he == hipSuccess) he = hipEventElapsedTime(&ms, ev0, ev1);
+      if (he != hipSuccess) rc = fail_hip(he, "engine_profile: timed launches");
+    }
+    if (ex) (void)hipGraphExecDestroy(ex);
+    ms_out[g] = static_cast<double>(ms) / (static_cast<double>(reps) * kInGraph);
+  }
+  (void)hipEventDestroy(ev0);
+  (void)hipEventDestroy(ev1);
+  if (rc == EF_HIP_OK) rc = set_pos();
+  e->chat_ids.clear();
+  return rc;
 }
 
 int ef_hip_engine_reset(ef_hip_engine e) {

@@ -167,7 +167,7 @@ void throw_if_error() {
 
 void matvec(float* y, const WeightView& W, const float* x, ThreadPool*) noexcept {
   const kern::MatvecJob j{y, &W, x};
-  matvec_jobs(&j, 1, nullptr);
+  hip::matvec_jobs(&j, 1, nullptr);  // qualified: argument-dependent lookup also finds ef::kern's
 }
 
 // kern::matvec_jobs (src/qkernels.cpp:280-297): jobs of equal width share one launch; jobs are

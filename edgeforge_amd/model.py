@@ -194,6 +194,20 @@ class Engine:
                peos.ctypes.data_as(C.POINTER(C.c_double)), C.byref(st))
         return out[:st.generated].copy(), peos[:st.steps].copy(), st
 
+    PROFILE_GROUPS = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "pick")
+
+    def profile(self, reps: int = 20, sampler: dict | None = None, rng: H.RngStates | None = None) -> dict:
+        """Milliseconds per step of each kernel group of a decode step (ef_hip_engine_profile)."""
+        out = (C.c_double * len(self.PROFILE_GROUPS))()
+        cfg = None
+        if sampler is not None:
+            cfg = EL.ef_hip_sampler_config(sampler.get("temperature", 0.0), sampler.get("top_k", 0),
+                                          sampler.get("top_p", 1.0), sampler.get("repetition_penalty", 1.0),
+                                          sampler.get("seed", 0))
+        EL.call("ef_hip_engine_profile", self.h, C.byref(cfg) if cfg is not None else None,
+               rng.buf.ptr if rng else None, reps, out)
+        return {g: float(out[i]) for i, g in enumerate(self.PROFILE_GROUPS)}
+
     def reset(self) -> None:
         EL.call("ef_hip_engine_reset", self.h)
 

@@ -225,6 +225,26 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n
                            const ef_hip_sampler_config* cfg, void* rng_dev, int32_t* tokens_out,
                            double* prefill_s, double* decode_s);
 
+/* Where the time of a decode step goes (the reference's ForwardProfile and run_profile,
+ * include/ef/model.h:89-94, src/bench_decode.cpp:164-231; its 13 buckets merged where this build
+ * fuses the ops into one kernel).  Each group's launches of one step (every layer's, in step order,
+ * the same kernels and arguments as the step graph) are captured as their own HIP graph and
+ * replayed `reps` times between HIP events on the engine's stream, at the last cached position;
+ * ms_out[g] gets the mean milliseconds per step of group g.  cfg / rng_dev as in generate: the
+ * pick group is the sampler (cfg with temperature > 0) or argmax.  The position is restored after
+ * each group; the RNG states advance and history entries past the cached positions are
+ * overwritten.  Needs at least one cached position (forward, prefill or generate first). */
+#define EF_HIP_PROF_EMBED 0     /* Embed */
+#define EF_HIP_PROF_QKV 1       /* AttnNorm + QKV (+ the batched path's activation preparation) */
+#define EF_HIP_PROF_ATTENTION 2 /* Rope + Attention (cache write included) */
+#define EF_HIP_PROF_OPROJ 3     /* OProj + Residual */
+#define EF_HIP_PROF_GATE_UP 4   /* FfnNorm + GateUp + SwiGLU */
+#define EF_HIP_PROF_DOWN 5      /* Down + Residual */
+#define EF_HIP_PROF_LM_HEAD 6   /* FinalNorm + LmHead */
+#define EF_HIP_PROF_PICK 7      /* argmax or the sampler, and the step bookkeeping */
+#define EF_HIP_PROF_GROUPS 8
+int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, void* rng_dev, int reps, double* ms_out);
+
 /* ---- quality of a quantized model (eval-quant, src/eval_quant.cpp) ---------------------------------
  * compare_dist (src/eval_quant.cpp:48-96) over n positions of device logits: KL(P_ref || P_ours) in
  * double, top-1 agreement, the reference confident (its top-1 probability >= 0.5), ours finite;

@@ -310,3 +310,24 @@ def test_long_context_group_and_head_attention_identical(hip, monkeypatch):
         eng.close()
     assert np.array_equal(out["head"][0], out["group"][0])
     assert np.array_equal(out["head"][1], out["group"][1])
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_engine_profile_groups_and_state(hip, B):
+    """ef_hip_engine_profile times every kernel group of a step and puts the position back: each
+    group has a positive time, the groups add up to about one step, and decoding afterwards from
+    the same state gives the same tokens as before."""
+    print(f"[case] engine profile B={B}", flush=True)
+    dm = DeviceModel.synthetic(SMALL, seed=29)
+    prompts = D.rng(47).integers(0, SMALL.V, size=(B, 9)).astype(np.int32)
+    eng = Engine(dm, max_seq=9 + 12, batch=B)
+    first, _, dec = eng.generate(prompts, 12)
+    prof = eng.profile(reps=5)
+    assert set(prof) == set(Engine.PROFILE_GROUPS)
+    assert all(v > 0.0 and np.isfinite(v) for v in prof.values()), prof
+    again, _, _ = eng.generate(prompts, 12)
+    assert np.array_equal(first, again)
+    prof_s = eng.profile(reps=5, sampler=dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
+                         rng=hip.RngStates(list(range(B))))
+    assert prof_s["pick"] > 0.0
+    eng.close()
