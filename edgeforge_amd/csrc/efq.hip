@@ -418,58 +418,11 @@ std::string shape_str(const std::vector<uint64_t>& s) {
   return out + "]";
 }
 
-// ---- config.json fields (src/model_config.cpp:18-70 semantics)
-const Json* field(const Json& root, const char* key) {
-  const Json* v = root.find(key);
-  return v == nullptr || v->kind == Json::Null ? nullptr : v;
-}
-
-int64_t int_field(const Json& root, const char* key, int64_t lo, int64_t hi, const int64_t* def) {
-  const Json* v = field(root, key);
-  if (v == nullptr) {
-    if (def != nullptr) return *def;
-    throw Error(std::string("config.json: missing required field '") + key + "'");
-  }
-  if (v->kind != Json::Number || !v->is_int)
-    throw Error(std::string("config.json: '") + key + "' must be an integer, got " +
-                (v->kind == Json::Number ? v->text : std::string(kind_name(v->kind))));
-  if (v->integer < lo || v->integer > hi) {
-    throw Error(std::string("config.json: '") + key + "' = " + std::to_string(v->integer) + " is outside [" +
-                std::to_string(lo) + ", " + std::to_string(hi) + "]");
-  }
-  return v->integer;
-}
-
-double num_field(const Json& root, const char* key, const double* def) {
-  const Json* v = field(root, key);
-  if (v == nullptr) {
-    if (def != nullptr) return *def;
-    throw Error(std::string("config.json: missing required field '") + key + "'");
-  }
-  if (v->kind != Json::Number)
-    throw Error(std::string("config.json: '") + key + "' must be a number, got " + kind_name(v->kind));
-  return v->number;
-}
-
-bool bool_field(const Json& root, const char* key, bool def) {
-  const Json* v = field(root, key);
-  if (v == nullptr) return def;
-  if (v->kind != Json::Bool) throw Error(std::string("config.json: '") + key + "' must be true or false");
-  return v->boolean;
-}
-
-std::string str_field(const Json& root, const char* key, const std::string& def) {
-  const Json* v = field(root, key);
-  if (v == nullptr) return def;
-  if (v->kind != Json::String) throw Error(std::string("config.json: '") + key + "' must be a string");
-  return v->text;
-}
-
 }  // namespace
 
 Json parse_json(const char* text, size_t n) { return JsonReader(text, n).document(); }
 
-// ---------------------------------------------------------------- types, policy, config
+// ---------------------------------------------------------------- types
 
 const char* qtype_name(int t) {
   switch (t) {
@@ -496,6 +449,245 @@ uint64_t row_bytes(int t, uint64_t cols) {  // src/quant.cpp:136-149
   }
 }
 
+// ---------------------------------------------------------------- config.json as a rule table
+//
+// The model-config fields are validated by walking one ordered table (src/model_config.cpp:72-131
+// gives the semantics: which fields, their ranges and defaults, the accepted values, and which
+// failure a file with several problems reports first).  A field row reads and checks one key; a
+// constraint row checks fields read by earlier rows.  Reading follows the table's order, so the
+// first failing row decides the message.
+
+namespace {
+
+struct ConfigState {
+  const Json* root = nullptr;
+  std::unordered_map<std::string, int64_t> ints;
+  std::unordered_map<std::string, double> reals;
+  std::unordered_map<std::string, bool> flags;
+  std::unordered_map<std::string, std::string> texts;
+};
+
+enum class Row : uint8_t { Text, Int, Real, Flag, Constraint };
+// How an absent (or null) key is treated.
+enum class Absent : uint8_t { Required, Constant, SameAs, Quotient };
+
+struct ConfigRow {
+  Row kind;
+  const char* key;            // the config.json key (Constraint rows: a label only)
+  Absent absent;
+  int64_t lo, hi;             // Int rows: accepted range
+  double constant;            // Absent::Constant numeric default
+  const char* text;           // Text default (Constant), or the key whose value is the default (SameAs),
+                              // or the dividend key of a quotient default (Quotient)
+  const char* text2;          // Quotient: the divisor key
+  bool (*ok)(const ConfigState&);                 // Constraint rows, and Text rows with one accepted value
+  std::string (*why)(const ConfigState&);         // message when ok() fails
+};
+
+const Json* present(const Json& root, const char* key) {
+  const Json* v = root.find(key);
+  return v == nullptr || v->kind == Json::Null ? nullptr : v;
+}
+
+std::string quoted(const char* key) { return std::string("config.json: '") + key + "'"; }
+
+void read_row(const ConfigRow& r, ConfigState& st) {
+  // an optional key given as null takes its default; a required key must be there, null or not,
+  // and a null one fails its type check
+  const Json* v = r.absent == Absent::Required ? st.root->find(r.key) : present(*st.root, r.key);
+  const bool have = v != nullptr;
+  if (!have && r.absent == Absent::Required) throw Error(std::string("config.json: missing required field '") + r.key + "'");
+  switch (r.kind) {
+    case Row::Text: {
+      std::string val;
+      if (have) {
+        if (v->kind != Json::String) throw Error(quoted(r.key) + " must be a string");
+        val = v->text;
+      } else {
+        val = r.absent == Absent::SameAs ? st.texts[r.text] : std::string(r.text ? r.text : "");
+      }
+      st.texts[r.key] = val;
+      break;
+    }
+    case Row::Int: {
+      int64_t val = 0;
+      if (have) {
+        if (v->kind != Json::Number || !v->is_int)
+          throw Error(quoted(r.key) + " must be an integer, got " +
+                      (v->kind == Json::Number ? v->text : std::string(kind_name(v->kind))));
+        val = v->integer;
+        if (val < r.lo || val > r.hi)
+          throw Error(quoted(r.key) + " = " + std::to_string(val) + " is outside [" + std::to_string(r.lo) + ", " +
+                      std::to_string(r.hi) + "]");
+      } else if (r.absent == Absent::SameAs) {
+        val = st.ints[r.text];
+      } else if (r.absent == Absent::Quotient) {
+        val = st.ints[r.text] / st.ints[r.text2];
+      } else {
+        val = static_cast<int64_t>(r.constant);
+      }
+      st.ints[r.key] = val;
+      break;
+    }
+    case Row::Real: {
+      double val = r.constant;
+      if (have) {
+        if (v->kind != Json::Number) throw Error(quoted(r.key) + " must be a number, got " + kind_name(v->kind));
+        val = v->number;
+      }
+      st.reals[r.key] = val;
+      break;
+    }
+    case Row::Flag: {
+      bool val = r.constant != 0.0;
+      if (have) {
+        if (v->kind != Json::Bool) throw Error(quoted(r.key) + " must be true or false");
+        val = v->boolean;
+      }
+      st.flags[r.key] = val;
+      break;
+    }
+    case Row::Constraint: break;
+  }
+  if (r.ok != nullptr && !r.ok(st)) throw Error("config.json: " + r.why(st));
+}
+
+int64_t I(const ConfigState& s, const char* k) { return s.ints.at(k); }
+double R(const ConfigState& s, const char* k) { return s.reals.at(k); }
+bool positive_finite(double v) { return v > 0.0 && std::isfinite(v); }
+
+constexpr int64_t kMaxDim = int64_t{1} << 20;
+constexpr int64_t kMaxId = int64_t{1} << 24;
+
+const ConfigRow kConfigRows[] = {
+    {Row::Text, "model_type", Absent::Constant, 0, 0, 0.0, "", nullptr,
+     [](const ConfigState& s) { return s.texts.at("model_type") == "llama"; },
+     [](const ConfigState& s) {
+       return "model_type '" + s.texts.at("model_type") + "' is not supported (EdgeForge targets 'llama')";
+     }},
+    {Row::Text, "hidden_act", Absent::Constant, 0, 0, 0.0, "silu", nullptr,
+     [](const ConfigState& s) { return s.texts.at("hidden_act") == "silu"; },
+     [](const ConfigState& s) { return "hidden_act '" + s.texts.at("hidden_act") + "' is not supported (expected 'silu')"; }},
+    // informational strings: only their JSON type is checked ("torch_dtype" defaults to "dtype")
+    {Row::Text, "dtype", Absent::Constant, 0, 0, 0.0, "", nullptr, nullptr, nullptr},
+    {Row::Text, "torch_dtype", Absent::SameAs, 0, 0, 0.0, "dtype", nullptr, nullptr, nullptr},
+    {Row::Int, "hidden_size", Absent::Required, 1, kMaxDim, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "intermediate_size", Absent::Required, 1, kMaxDim, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "num_hidden_layers", Absent::Required, 1, 4096, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "num_attention_heads", Absent::Required, 1, 4096, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "num_key_value_heads", Absent::SameAs, 1, 4096, 0.0, "num_attention_heads", nullptr, nullptr, nullptr},
+    {Row::Int, "vocab_size", Absent::Required, 1, kMaxId, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "max_position_embeddings", Absent::Constant, 1, kMaxId, 2048.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Real, "rms_norm_eps", Absent::Required, 0, 0, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Real, "rope_theta", Absent::Constant, 0, 0, 10000.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Flag, "tie_word_embeddings", Absent::Constant, 0, 0, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Flag, "attention_bias", Absent::Constant, 0, 0, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Flag, "mlp_bias", Absent::Constant, 0, 0, 0.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "bos_token_id", Absent::Constant, -1, kMaxId, -1.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Int, "eos_token_id", Absent::Constant, -1, kMaxId, -1.0, nullptr, nullptr, nullptr, nullptr},
+    {Row::Constraint, "heads divide hidden", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return I(s, "hidden_size") % I(s, "num_attention_heads") == 0; },
+     [](const ConfigState& s) {
+       return "hidden_size " + std::to_string(I(s, "hidden_size")) + " is not divisible by num_attention_heads " +
+              std::to_string(I(s, "num_attention_heads"));
+     }},
+    {Row::Int, "head_dim", Absent::Quotient, 1, kMaxDim, 0.0, "hidden_size", "num_attention_heads", nullptr, nullptr},
+    {Row::Constraint, "head_dim x heads", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return I(s, "head_dim") * I(s, "num_attention_heads") == I(s, "hidden_size"); },
+     [](const ConfigState&) { return std::string("head_dim * num_attention_heads must equal hidden_size"); }},
+    {Row::Constraint, "even head_dim", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return I(s, "head_dim") % 2 == 0; },
+     [](const ConfigState&) { return std::string("head_dim must be even for RoPE"); }},
+    {Row::Constraint, "kv heads divide heads", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return I(s, "num_attention_heads") % I(s, "num_key_value_heads") == 0; },
+     [](const ConfigState& s) {
+       return "num_attention_heads " + std::to_string(I(s, "num_attention_heads")) +
+              " is not divisible by num_key_value_heads " + std::to_string(I(s, "num_key_value_heads"));
+     }},
+    {Row::Constraint, "eps", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return positive_finite(R(s, "rms_norm_eps")); },
+     [](const ConfigState&) { return std::string("rms_norm_eps must be a positive finite number"); }},
+    {Row::Constraint, "theta", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return positive_finite(R(s, "rope_theta")); },
+     [](const ConfigState&) { return std::string("rope_theta must be a positive finite number"); }},
+    {Row::Constraint, "rope scaling", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return present(*s.root, "rope_scaling") == nullptr; },
+     [](const ConfigState&) { return std::string("rope_scaling is set; scaled RoPE is not supported yet"); }},
+    {Row::Constraint, "attention bias", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return !s.flags.at("attention_bias"); },
+     [](const ConfigState&) { return std::string("attention_bias=true is not supported"); }},
+    {Row::Constraint, "mlp bias", Absent::Constant, 0, 0, 0.0, nullptr, nullptr,
+     [](const ConfigState& s) { return !s.flags.at("mlp_bias"); },
+     [](const ConfigState&) { return std::string("mlp_bias=true is not supported"); }},
+};
+
+}  // namespace
+
+Config parse_config(const Json& root) {
+  if (root.kind != Json::Object) throw Error("config.json: top level must be a JSON object");
+  ConfigState st;
+  st.root = &root;
+  for (const ConfigRow& r : kConfigRows) read_row(r, st);
+  Config c;
+  c.hidden_size = I(st, "hidden_size");
+  c.intermediate_size = I(st, "intermediate_size");
+  c.num_hidden_layers = I(st, "num_hidden_layers");
+  c.num_attention_heads = I(st, "num_attention_heads");
+  c.num_key_value_heads = I(st, "num_key_value_heads");
+  c.head_dim = I(st, "head_dim");
+  c.vocab_size = I(st, "vocab_size");
+  c.max_position_embeddings = I(st, "max_position_embeddings");
+  c.bos_token_id = I(st, "bos_token_id");
+  c.eos_token_id = I(st, "eos_token_id");
+  c.rms_norm_eps = R(st, "rms_norm_eps");
+  c.rope_theta = R(st, "rope_theta");
+  c.tie_word_embeddings = st.flags.at("tie_word_embeddings");
+  return c;
+}
+
+// ---------------------------------------------------------------- tensors the config implies
+
+namespace {
+// A tensor slot: name (a per-layer suffix or a whole name) and its shape in model dimensions
+// ('D' hidden, 'F' intermediate, 'K' KV width, 'V' vocabulary, 0 for the second dim of a 1-D norm).
+struct Slot {
+  const char* name;
+  char rows, cols;
+};
+constexpr Slot kLayerSlots[] = {
+    {"self_attn.q_proj.weight", 'D', 'D'}, {"self_attn.k_proj.weight", 'K', 'D'},
+    {"self_attn.v_proj.weight", 'K', 'D'}, {"self_attn.o_proj.weight", 'D', 'D'},
+    {"mlp.gate_proj.weight", 'F', 'D'},    {"mlp.up_proj.weight", 'F', 'D'},
+    {"mlp.down_proj.weight", 'D', 'F'},    {"input_layernorm.weight", 'D', 0},
+    {"post_attention_layernorm.weight", 'D', 0},
+};
+}  // namespace
+
+// Forward order: the embedding, each layer's slots, the final norm, then the lm_head unless tied
+// to the embedding (src/model_config.cpp:145-167 lists the same set).
+std::vector<Expected> expected_tensors(const Config& c) {
+  auto dim = [&](char d) -> uint64_t {
+    switch (d) {
+      case 'D': return static_cast<uint64_t>(c.hidden_size);
+      case 'F': return static_cast<uint64_t>(c.intermediate_size);
+      case 'K': return static_cast<uint64_t>(c.kv_dim());
+      default: return static_cast<uint64_t>(c.vocab_size);
+    }
+  };
+  auto shape = [&](const Slot& s) {
+    return s.cols ? std::vector<uint64_t>{dim(s.rows), dim(s.cols)} : std::vector<uint64_t>{dim(s.rows)};
+  };
+  std::vector<Expected> out;
+  out.reserve(static_cast<size_t>(c.num_hidden_layers) * std::size(kLayerSlots) + 3);
+  out.push_back({"model.embed_tokens.weight", shape({nullptr, 'V', 'D'})});
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l)
+    for (const Slot& s : kLayerSlots)
+      out.push_back({"model.layers." + std::to_string(l) + "." + s.name, shape(s)});
+  out.push_back({"model.norm.weight", shape({nullptr, 'D', 0})});
+  if (!c.tie_word_embeddings) out.push_back({"lm_head.weight", shape({nullptr, 'V', 'D'})});
+  return out;
+}
+
 // '*' matches any run of characters (including none); every other character matches itself.
 // Dynamic programming over pattern prefixes: reach[j] = the first j pattern characters can
 // match the text consumed so far.
@@ -519,93 +711,151 @@ bool glob_match(const std::string& p, const std::string& s) {
   return reach[p.size()] != 0;
 }
 
-Choice policy_choice(const Policy& p, const std::string& name, uint64_t cols) {  // src/qfile.cpp:66-78
+// The storage type a file's policy assigns to a tensor (src/qfile.cpp:66-78 semantics): norms are
+// always F32; otherwise the last override whose pattern matches wins over the tensor's role
+// (embedding, lm_head, or a layer matrix); a block type on rows that are not whole blocks falls
+// back to BF16.
+Choice policy_choice(const Policy& p, const std::string& name, uint64_t cols) {
   if (is_norm(name)) return {EF_QTYPE_F32, "norm"};
-  Choice c{p.layers, "layers"};
-  if (name == "model.embed_tokens.weight") c = {p.embed, "embed"};
-  if (name == "lm_head.weight") c = {p.lm_head, "lm_head"};
-  for (const Override& o : p.overrides)
-    if (glob_match(o.pattern, name)) c = {o.qtype, "override"};
-  if ((c.qtype == EF_QTYPE_Q4_0 || c.qtype == EF_QTYPE_Q8_0) && cols % 32 != 0) c = {EF_QTYPE_BF16, "fallback-bf16"};
-  return c;
-}
-
-std::vector<Expected> expected_tensors(const Config& c) {
-  const auto D = static_cast<uint64_t>(c.hidden_size), F = static_cast<uint64_t>(c.intermediate_size);
-  const auto V = static_cast<uint64_t>(c.vocab_size), KV = static_cast<uint64_t>(c.kv_dim());
-  std::vector<Expected> out;
-  out.push_back({"model.embed_tokens.weight", {V, D}});
-  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
-    const std::string p = "model.layers." + std::to_string(l) + ".";
-    out.push_back({p + "self_attn.q_proj.weight", {D, D}});
-    out.push_back({p + "self_attn.k_proj.weight", {KV, D}});
-    out.push_back({p + "self_attn.v_proj.weight", {KV, D}});
-    out.push_back({p + "self_attn.o_proj.weight", {D, D}});
-    out.push_back({p + "mlp.gate_proj.weight", {F, D}});
-    out.push_back({p + "mlp.up_proj.weight", {F, D}});
-    out.push_back({p + "mlp.down_proj.weight", {D, F}});
-    out.push_back({p + "input_layernorm.weight", {D}});
-    out.push_back({p + "post_attention_layernorm.weight", {D}});
-  }
-  out.push_back({"model.norm.weight", {D}});
-  if (!c.tie_word_embeddings) out.push_back({"lm_head.weight", {V, D}});
-  return out;
-}
-
-Config parse_config(const Json& root) {
-  if (root.kind != Json::Object) throw Error("config.json: top level must be a JSON object");
-  Config c;
-  const std::string model_type = str_field(root, "model_type", "");
-  if (model_type != "llama")
-    throw Error("config.json: model_type '" + model_type + "' is not supported (EdgeForge targets 'llama')");
-  const std::string act = str_field(root, "hidden_act", "silu");
-  if (act != "silu") throw Error("config.json: hidden_act '" + act + "' is not supported (expected 'silu')");
-  constexpr int64_t kMaxDim = int64_t{1} << 20;
-  c.hidden_size = int_field(root, "hidden_size", 1, kMaxDim, nullptr);
-  c.intermediate_size = int_field(root, "intermediate_size", 1, kMaxDim, nullptr);
-  c.num_hidden_layers = int_field(root, "num_hidden_layers", 1, 4096, nullptr);
-  c.num_attention_heads = int_field(root, "num_attention_heads", 1, 4096, nullptr);
-  c.num_key_value_heads = int_field(root, "num_key_value_heads", 1, 4096, &c.num_attention_heads);
-  c.vocab_size = int_field(root, "vocab_size", 1, int64_t{1} << 24, nullptr);
-  const int64_t def_pos = 2048, def_id = -1;
-  c.max_position_embeddings = int_field(root, "max_position_embeddings", 1, int64_t{1} << 24, &def_pos);
-  c.rms_norm_eps = num_field(root, "rms_norm_eps", nullptr);
-  const double def_theta = 10000.0;
-  c.rope_theta = num_field(root, "rope_theta", &def_theta);
-  c.tie_word_embeddings = bool_field(root, "tie_word_embeddings", false);
-  const bool attention_bias = bool_field(root, "attention_bias", false);
-  const bool mlp_bias = bool_field(root, "mlp_bias", false);
-  c.bos_token_id = int_field(root, "bos_token_id", -1, int64_t{1} << 24, &def_id);
-  c.eos_token_id = int_field(root, "eos_token_id", -1, int64_t{1} << 24, &def_id);
-  if (c.hidden_size % c.num_attention_heads != 0)
-    throw Error("config.json: hidden_size " + std::to_string(c.hidden_size) + " is not divisible by num_attention_heads " +
-                std::to_string(c.num_attention_heads));
-  const int64_t def_hd = c.hidden_size / c.num_attention_heads;
-  c.head_dim = int_field(root, "head_dim", 1, kMaxDim, &def_hd);
-  if (c.head_dim * c.num_attention_heads != c.hidden_size)
-    throw Error("config.json: head_dim * num_attention_heads must equal hidden_size");
-  if (c.head_dim % 2 != 0) throw Error("config.json: head_dim must be even for RoPE");
-  if (c.num_attention_heads % c.num_key_value_heads != 0)
-    throw Error("config.json: num_attention_heads " + std::to_string(c.num_attention_heads) +
-                " is not divisible by num_key_value_heads " + std::to_string(c.num_key_value_heads));
-  if (!(c.rms_norm_eps > 0.0) || !std::isfinite(c.rms_norm_eps))
-    throw Error("config.json: rms_norm_eps must be a positive finite number");
-  if (!(c.rope_theta > 0.0) || !std::isfinite(c.rope_theta))
-    throw Error("config.json: rope_theta must be a positive finite number");
-  if (field(root, "rope_scaling") != nullptr)
-    throw Error("config.json: rope_scaling is set; scaled RoPE is not supported yet");
-  if (attention_bias) throw Error("config.json: attention_bias=true is not supported");
-  if (mlp_bias) throw Error("config.json: mlp_bias=true is not supported");
+  const auto hit = std::find_if(p.overrides.rbegin(), p.overrides.rend(),
+                                [&](const Override& o) { return glob_match(o.pattern, name); });
+  Choice c = hit != p.overrides.rend()              ? Choice{hit->qtype, "override"}
+             : name == "lm_head.weight"             ? Choice{p.lm_head, "lm_head"}
+             : name == "model.embed_tokens.weight"  ? Choice{p.embed, "embed"}
+                                                    : Choice{p.layers, "layers"};
+  const bool block = c.qtype == EF_QTYPE_Q4_0 || c.qtype == EF_QTYPE_Q8_0;
+  if (block && cols % 32 != 0) c = {EF_QTYPE_BF16, "fallback-bf16"};
   return c;
 }
 
 // ---------------------------------------------------------------- the file
 
+namespace {
+
+// One header tensor entry, decoded in key order with each key's own check right after it (a
+// malformed entry reports the first problem in that order).
+Tensor decode_entry(const Json& e) {
+  Tensor t;
+  t.name = e.at("name").str();
+  const std::string& type = e.at("type").str();
+  t.qtype = qtype_from(type);
+  if (t.qtype < 0) throw Error("tensor '" + t.name + "': unknown type " + type);
+  if (const Json* r = e.find("rule")) t.rule = r->str();
+  for (const Json& d : e.at("shape").list()) t.shape.push_back(d.u64());
+  if (t.shape.empty() || t.shape.size() > 2) throw Error("tensor '" + t.name + "': shape must be 1-D or 2-D");
+  t.offset = e.at("offset").u64();
+  t.bytes = e.at("bytes").u64();
+  if (const Json* r = e.find("rel_rmse")) t.rel_rmse = r->dbl();
+  if (const Json* r = e.find("max_abs_err")) t.max_abs_err = r->dbl();
+  return t;
+}
+
+// Checks of one decoded entry against the file, in the order a file with several problems reports
+// them: size arithmetic, declared bytes, alignment, placement after the header, bounds.
+struct Placement {
+  uint64_t data_start, file_size;
+};
+struct EntryRule {
+  bool (*bad)(const Tensor&, const Placement&, uint64_t need, bool overflow);
+  std::string (*why)(const Tensor&, uint64_t need);
+};
+const EntryRule kEntryRules[] = {
+    {[](const Tensor&, const Placement&, uint64_t, bool overflow) { return overflow; },
+     [](const Tensor&, uint64_t) { return std::string("size overflows"); }},
+    {[](const Tensor& t, const Placement&, uint64_t need, bool) { return need != t.bytes; },
+     [](const Tensor& t, uint64_t need) {
+       return std::string(qtype_name(t.qtype)) + " " + shape_str(t.shape) + " needs " + std::to_string(need) +
+              " bytes, header says " + std::to_string(t.bytes);
+     }},
+    {[](const Tensor& t, const Placement&, uint64_t, bool) { return t.offset % 64 != 0; },
+     [](const Tensor&, uint64_t) { return std::string("offset is not 64-byte aligned"); }},
+    {[](const Tensor& t, const Placement& p, uint64_t, bool) { return t.offset < p.data_start; },
+     [](const Tensor&, uint64_t) { return std::string("data overlaps the header"); }},
+    {[](const Tensor& t, const Placement& p, uint64_t, bool) {
+       return t.offset > p.file_size || t.bytes > p.file_size - t.offset;
+     },
+     [](const Tensor&, uint64_t) { return std::string("data runs past the end of the file (truncated?)"); }},
+};
+
+void check_entry(const Tensor& t, const Placement& where) {
+  const uint64_t rb = row_bytes(t.qtype, t.cols());
+  const bool overflow = t.rows() != 0 && rb > std::numeric_limits<uint64_t>::max() / t.rows();
+  const uint64_t need = overflow ? 0 : rb * t.rows();
+  for (const EntryRule& r : kEntryRules)
+    if (r.bad(t, where, need, overflow)) throw Error("tensor '" + t.name + "': " + r.why(t, need));
+}
+
+// No two tensors' byte ranges intersect: walked in offset order (ties in header order), the first
+// range that starts before its predecessor ends is reported with that predecessor.
+void check_disjoint(const std::vector<Tensor>& ts) {
+  std::vector<std::pair<uint64_t, size_t>> by_offset;
+  by_offset.reserve(ts.size());
+  for (size_t i = 0; i < ts.size(); ++i) by_offset.emplace_back(ts[i].offset, i);
+  std::sort(by_offset.begin(), by_offset.end());
+  uint64_t end = 0;
+  const Tensor* prev = nullptr;
+  for (const auto& [off, i] : by_offset) {
+    if (prev != nullptr && off < end) throw Error("tensors '" + prev->name + "' and '" + ts[i].name + "' overlap");
+    prev = &ts[i];
+    end = off + ts[i].bytes;
+  }
+}
+
+// Exactly the tensors the configuration implies, each once, with the implied shapes.
+void check_names_and_shapes(const std::vector<Tensor>& ts, const std::vector<Expected>& want) {
+  std::unordered_map<std::string, const Tensor*> seen;
+  for (const Tensor& t : ts)
+    if (!seen.emplace(t.name, &t).second) throw Error("duplicate tensor '" + t.name + "'");
+  for (const Expected& e : want) {
+    const auto it = seen.find(e.name);
+    if (it == seen.end()) throw Error("missing tensor '" + e.name + "'");
+    if (it->second->shape != e.shape)
+      throw Error("tensor '" + e.name + "' has shape " + shape_str(it->second->shape) + ", config needs " +
+                  shape_str(e.shape));
+  }
+  if (seen.size() != want.size()) throw Error(".efq file has tensors the config does not use");
+}
+
+// The header's quantization policy: the three role types, F32 norms, the override list (each must
+// name at least one tensor of this model and no norm; src/qfile.cpp:80-93 semantics).
+Policy read_policy(const Json& qs, const std::vector<Expected>& want) {
+  const Json* table = qs.find("overrides");
+  if (table == nullptr)
+    throw Error(".efq header has no \"overrides\" table: written by an older pre-release build, re-run "
+                "edgeforge quantize");
+  auto type_of = [](const Json& v, const char* what) {
+    const int t = qtype_from(v.str());
+    if (t < 0) throw Error(std::string(".efq header: unknown ") + what + " type " + v.str());
+    return t;
+  };
+  Policy p;
+  p.layers = type_of(qs.at("layers"), "layers");
+  p.lm_head = type_of(qs.at("lm_head"), "lm_head");
+  p.embed = type_of(qs.at("embed"), "embed");
+  if (qs.at("norms").str() != "F32") throw Error(".efq header: norms must be F32");
+  if (const Json* n = qs.find("policy")) p.name = n->str();
+  for (const Json& o : table->list()) p.overrides.push_back({o.at("pattern").str(), type_of(o.at("type"), "override")});
+  for (const Override& o : p.overrides) {
+    if (o.pattern.empty()) throw Error("override with an empty tensor pattern");
+    auto matches = [&](const Expected& e) { return glob_match(o.pattern, e.name); };
+    const auto norm = std::find_if(want.begin(), want.end(), [&](const Expected& e) { return matches(e) && is_norm(e.name); });
+    if (norm != want.end())
+      throw Error("override '" + o.pattern + "' matches norm tensor '" + norm->name + "' (norms are always F32)");
+    if (std::none_of(want.begin(), want.end(), matches))
+      throw Error("override '" + o.pattern + "' matches no tensor of this model");
+  }
+  return p;
+}
+
+}  // namespace
+
+// parse_efq (src/qfile.cpp:125-223 semantics): the fixed preamble, the JSON header, the config,
+// every tensor entry, then the cross-entry checks and the policy, each stage reporting its first
+// problem with the reference's wording.
 Layout parse(const uint8_t* file, uint64_t size) {
   if (size < 16) throw Error("file too small to be an .efq model (" + std::to_string(size) + " bytes)");
   if (std::memcmp(file, "EFQ1", 4) != 0) throw Error("not an EdgeForge .efq file (bad magic)");
-  const uint64_t version = le(file + 4, 4);
-  if (version != 1)
+  if (const uint64_t version = le(file + 4, 4); version != 1)
     throw Error("unsupported .efq version " + std::to_string(version) + " (this build reads 1)");
   Layout L;
   L.header_len = le(file + 8, 8);
@@ -619,82 +869,15 @@ Layout parse(const uint8_t* file, uint64_t size) {
   }
   if (h.at("format").str() != "edgeforge-quant") throw Error(".efq header: wrong \"format\"");
   L.cfg = parse_config(h.at("config"));
-  const uint64_t data_start = 16 + L.header_len;
-
+  const Placement where{16 + L.header_len, size};
   for (const Json& e : h.at("tensors").list()) {
-    Tensor t;
-    t.name = e.at("name").str();
-    t.qtype = qtype_from(e.at("type").str());
-    if (t.qtype < 0) throw Error("tensor '" + t.name + "': unknown type " + e.at("type").str());
-    if (const Json* r = e.find("rule")) t.rule = r->str();
-    for (const Json& d : e.at("shape").list()) t.shape.push_back(d.u64());
-    if (t.shape.empty() || t.shape.size() > 2) throw Error("tensor '" + t.name + "': shape must be 1-D or 2-D");
-    t.offset = e.at("offset").u64();
-    t.bytes = e.at("bytes").u64();
-    if (const Json* r = e.find("rel_rmse")) t.rel_rmse = r->dbl();
-    if (const Json* r = e.find("max_abs_err")) t.max_abs_err = r->dbl();
-    const uint64_t rb = row_bytes(t.qtype, t.cols());
-    if (t.rows() != 0 && rb > std::numeric_limits<uint64_t>::max() / t.rows())
-      throw Error("tensor '" + t.name + "': size overflows");
-    if (rb * t.rows() != t.bytes)
-      throw Error("tensor '" + t.name + "': " + qtype_name(t.qtype) + " " + shape_str(t.shape) + " needs " +
-                  std::to_string(rb * t.rows()) + " bytes, header says " + std::to_string(t.bytes));
-    if (t.offset % 64 != 0) throw Error("tensor '" + t.name + "': offset is not 64-byte aligned");
-    if (t.offset < data_start) throw Error("tensor '" + t.name + "': data overlaps the header");
-    if (t.offset > size || t.bytes > size - t.offset)
-      throw Error("tensor '" + t.name + "': data runs past the end of the file (truncated?)");
-    L.tensors.push_back(std::move(t));
+    L.tensors.push_back(decode_entry(e));
+    check_entry(L.tensors.back(), where);
   }
-  std::vector<size_t> order(L.tensors.size());
-  std::iota(order.begin(), order.end(), size_t{0});
-  std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return L.tensors[a].offset < L.tensors[b].offset; });
-  for (size_t i = 1; i < order.size(); ++i) {
-    const Tensor& p = L.tensors[order[i - 1]];
-    const Tensor& c = L.tensors[order[i]];
-    if (c.offset < p.offset + p.bytes) throw Error("tensors '" + p.name + "' and '" + c.name + "' overlap");
-  }
-
-  std::unordered_map<std::string, const Tensor*> by_name;
-  for (const Tensor& t : L.tensors)
-    if (!by_name.emplace(t.name, &t).second) throw Error("duplicate tensor '" + t.name + "'");
-  const std::vector<Expected> expected = expected_tensors(L.cfg);
-  for (const Expected& e : expected) {
-    const auto it = by_name.find(e.name);
-    if (it == by_name.end()) throw Error("missing tensor '" + e.name + "'");
-    if (it->second->shape != e.shape)
-      throw Error("tensor '" + e.name + "' has shape " + shape_str(it->second->shape) + ", config needs " +
-                  shape_str(e.shape));
-  }
-  if (by_name.size() != expected.size()) throw Error(".efq file has tensors the config does not use");
-
-  const Json& qs = h.at("quant");
-  const Json* ov = qs.find("overrides");
-  if (ov == nullptr)
-    throw Error(".efq header has no \"overrides\" table: written by an older pre-release build, re-run "
-                "edgeforge quantize");
-  auto type_field = [](const Json& v, const char* what) {
-    const int t = qtype_from(v.str());
-    if (t < 0) throw Error(std::string(".efq header: unknown ") + what + " type " + v.str());
-    return t;
-  };
-  L.policy.layers = type_field(qs.at("layers"), "layers");
-  L.policy.lm_head = type_field(qs.at("lm_head"), "lm_head");
-  L.policy.embed = type_field(qs.at("embed"), "embed");
-  if (qs.at("norms").str() != "F32") throw Error(".efq header: norms must be F32");
-  if (const Json* n = qs.find("policy")) L.policy.name = n->str();
-  for (const Json& o : ov->list())
-    L.policy.overrides.push_back({o.at("pattern").str(), type_field(o.at("type"), "override")});
-  for (const Override& o : L.policy.overrides) {  // check_overrides (src/qfile.cpp:80-93)
-    if (o.pattern.empty()) throw Error("override with an empty tensor pattern");
-    size_t hits = 0;
-    for (const Expected& e : expected) {
-      if (!glob_match(o.pattern, e.name)) continue;
-      if (is_norm(e.name))
-        throw Error("override '" + o.pattern + "' matches norm tensor '" + e.name + "' (norms are always F32)");
-      ++hits;
-    }
-    if (hits == 0) throw Error("override '" + o.pattern + "' matches no tensor of this model");
-  }
+  check_disjoint(L.tensors);
+  const std::vector<Expected> want = expected_tensors(L.cfg);
+  check_names_and_shapes(L.tensors, want);
+  L.policy = read_policy(h.at("quant"), want);
   for (const Tensor& t : L.tensors) {
     const Choice c = policy_choice(L.policy, t.name, t.cols());
     if (t.qtype != c.qtype || t.rule != c.rule)
@@ -705,12 +888,17 @@ Layout parse(const uint8_t* file, uint64_t size) {
   return L;
 }
 
+// Name -> index over the validated table, and the bytes one decoded token streams: every tensor but
+// the embedding (one row of it is read per token), plus the embedding when it doubles as the lm_head.
 void File::index() {
-  for (size_t i = 0; i < L_.tensors.size(); ++i) {
-    index_.emplace(L_.tensors[i].name, i);
-    if (L_.tensors[i].name != "model.embed_tokens.weight") bytes_per_token_ += L_.tensors[i].bytes;
-  }
-  if (L_.cfg.tie_word_embeddings) bytes_per_token_ += at("model.embed_tokens.weight").bytes;
+  index_.reserve(L_.tensors.size());
+  for (size_t i = 0; i < L_.tensors.size(); ++i) index_.emplace(L_.tensors[i].name, i);
+  const bool tied = L_.cfg.tie_word_embeddings;
+  bytes_per_token_ = std::accumulate(L_.tensors.begin(), L_.tensors.end(), uint64_t{0},
+                                     [&](uint64_t acc, const Tensor& t) {
+                                       const bool embed = t.name == "model.embed_tokens.weight";
+                                       return acc + (!embed || tied ? t.bytes : 0);
+                                     });
 }
 
 std::unique_ptr<File> File::open(const std::string& path) {
@@ -758,8 +946,9 @@ const Tensor* File::find(const std::string& name) const {
 }
 
 const Tensor& File::at(const std::string& name) const {
-  if (const Tensor* t = find(name)) return *t;
-  throw Error("tensor '" + name + "' not found in '" + path_ + "'");
+  const Tensor* t = find(name);
+  if (t == nullptr) throw Error("tensor '" + name + "' not found in '" + path_ + "'");
+  return *t;
 }
 
 }  // namespace efh::efq

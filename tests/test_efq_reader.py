@@ -250,3 +250,58 @@ def test_single_byte_corruptions_agree_with_the_reference():
             else:
                 assert got[0] == want[0]
         assert agree_reject > 50
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_double_byte_corruptions_agree_with_the_reference(seed):
+    """500 seeded two-byte edits of the header per seed (printable ASCII): the first failing check,
+    and so the message, is the same as the reference reader's."""
+    with tempfile.TemporaryDirectory() as d:
+        _, _, good = written(d, q8={(0, "wv")})
+        hlen = int.from_bytes(good[8:16], "little")
+        g = np.random.default_rng(seed)
+        for k in range(500):
+            bad = bytearray(good)
+            for _ in range(2):
+                bad[16 + int(g.integers(0, hlen))] = int(g.integers(0x20, 0x7F))
+            got, want = ours(bytes(bad)), theirs(bytes(bad))
+            assert (got[0] is None) == (want[0] is None), (k, got, want)
+            if got[0] is None and not want[1].startswith("invalid .efq header"):
+                assert got[1] == want[1], (k, got, want)
+
+
+CONFIG_KEYS = ["model_type", "hidden_act", "hidden_size", "intermediate_size", "num_hidden_layers",
+               "num_attention_heads", "num_key_value_heads", "vocab_size", "max_position_embeddings",
+               "rms_norm_eps", "rope_theta", "tie_word_embeddings", "bos_token_id", "eos_token_id"]
+VALUES = ['null', '"x"', '7', '-3', '0', '1.5', 'true', '[]', '{}', '1048577', '16777217', '1e400', '2']
+
+
+@needs_ref
+@pytest.mark.parametrize("key", CONFIG_KEYS + ["head_dim", "rope_scaling", "attention_bias", "mlp_bias", "dtype",
+                                               "torch_dtype"])
+def test_config_field_values_agree_with_the_reference(key):
+    """Every config field set to each of a set of values (absent, wrong JSON type, out of range,
+    inconsistent with the other fields): accepted or rejected with the same message as the
+    reference's config parser (src/model_config.cpp:72-131)."""
+    import json
+    import re
+    with tempfile.TemporaryDirectory() as d:
+        _, _, good = written(d)
+        hlen = int.from_bytes(good[8:16], "little")
+        header = json.loads(good[16:16 + hlen].decode())
+        for v in VALUES + ["DELETE"]:
+            h = json.loads(json.dumps(header))
+            if v == "DELETE":
+                h["config"].pop(key, None)
+            else:
+                h["config"][key] = "__V__"
+            text = json.dumps(h, separators=(",", ":")).replace('"__V__"', v)
+            if len(text) > hlen:
+                continue
+            text = text + " " * (hlen - len(text))
+            bad = good[:16] + text.encode() + good[16 + hlen:]
+            got, want = ours(bad), theirs(bad)
+            assert (got[0] is None) == (want[0] is None), (key, v, got, want)
+            if got[0] is None and not want[1].startswith("invalid .efq header"):
+                assert got[1] == want[1], (key, v, got, want)
