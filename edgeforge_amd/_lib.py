@@ -106,6 +106,7 @@ SIGNATURES = {
     "ef_hip_weight_register_host": (C.c_int, [_P, C.c_int, _sz, _sz, C.POINTER(_P)]),
     "ef_hip_weight_register_device": (C.c_int, [_P, C.c_int, _sz, _sz, C.POINTER(_P)]),
     "ef_hip_weight_release": (C.c_int, [_P]),
+    "ef_hip_weight_refresh": (C.c_int, [_P, _P]),
     "ef_hip_weight_info": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_P)]),
     "ef_hip_row_bytes": (C.c_int, [C.c_int, _sz, C.POINTER(_sz)]),
     "ef_hip_matvec": (C.c_int, [_P, _P, _P, C.c_int, _sz, _sz, _P]),

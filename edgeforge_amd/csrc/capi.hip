@@ -307,6 +307,12 @@ int ef_hip_weight_release(ef_hip_weight w) {
   return EF_HIP_OK;
 }
 
+int ef_hip_weight_refresh(ef_hip_weight w, void* stream) {
+  EFH_READY();
+  EFH_RC(check_weight(w));
+  return refresh_tiled(w, pick(stream));
+}
+
 int ef_hip_weight_info(ef_hip_weight w, int* qtype, size_t* rows, size_t* cols, const void** dev) {
   EFH_RC(check_weight(w));
   if (qtype) *qtype = w->qtype;

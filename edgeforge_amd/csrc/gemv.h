@@ -37,8 +37,11 @@ size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int b
 int gemv_mfma_max_rows();
 // The batched path reads Q4_0 / Q8_0 matrices from a tile-order copy (w->tiled, tiled_bytes(w)
 // bytes).  ensure_tiled makes it when missing (allocates; refused while `s` is capturing a graph).
+// refresh_tiled rewrites an existing copy from the handle's current bytes, in place and
+// stream-ordered on `s` (no allocation, so graphs that read the copy stay valid); no-op without one.
 size_t tiled_bytes(const ef_hip_weight_s* w);
 int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s);
+int refresh_tiled(const ef_hip_weight_s* w, hipStream_t s);
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 

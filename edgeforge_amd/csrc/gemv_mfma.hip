@@ -895,6 +895,23 @@ size_t tiled_bytes(const ef_hip_weight_s* w) {
   return tiles * nb * (w->qtype == EF_QTYPE_Q4_0 ? kTileBlockQ4 : kTileBlockQ8);
 }
 
+namespace {
+void launch_tile_layout(const ef_hip_weight_s* w, uint8_t* out, hipStream_t s) {
+  const size_t tiles = (w->rows + kTileRows - 1) / kTileRows, nb = w->cols / 32;
+  const size_t threads = tiles * nb * kWave;
+  hipLaunchKernelGGL(tile_layout_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s, w->dev,
+                     static_cast<int>(w->rows), static_cast<int>(nb), static_cast<int>(w->row_bytes),
+                     w->qtype == EF_QTYPE_Q4_0 ? 1 : 0, out);
+}
+}  // namespace
+
+int refresh_tiled(const ef_hip_weight_s* w, hipStream_t s) {
+  if (w->tiled == nullptr) return EF_HIP_OK;
+  launch_tile_layout(w, w->tiled, s);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
 int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s) {
   if (w->tiled != nullptr) return EF_HIP_OK;
   EFH_CHECK(w->qtype == EF_QTYPE_Q4_0 || w->qtype == EF_QTYPE_Q8_0, "tile layout: packed types only");
@@ -908,11 +925,7 @@ int ensure_tiled(const ef_hip_weight_s* w, hipStream_t s) {
   EFH_CHECK(bytes < (size_t(1) << 32), "tile layout: matrix too large for one buffer resource");
   uint8_t* out = nullptr;
   EFH_HIP(hipMalloc(&out, bytes));
-  const size_t tiles = (w->rows + kTileRows - 1) / kTileRows, nb = w->cols / 32;
-  const size_t threads = tiles * nb * kWave;
-  hipLaunchKernelGGL(tile_layout_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s, w->dev,
-                     static_cast<int>(w->rows), static_cast<int>(nb), static_cast<int>(w->row_bytes),
-                     w->qtype == EF_QTYPE_Q4_0 ? 1 : 0, out);
+  launch_tile_layout(w, out, s);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {

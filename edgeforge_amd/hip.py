@@ -145,6 +145,10 @@ class Weight:
             call("ef_hip_weight_register_device", device.ptr, qtype, rows, cols, C.byref(h))
         self.handle = h.value
 
+    def refresh(self, stream=None) -> None:
+        """Rewrite the batched path's tile-order copy from the current bytes (after they changed)."""
+        call("ef_hip_weight_refresh", self.handle, _s(stream))
+
     def release(self) -> None:
         if getattr(self, "handle", None):
             call("ef_hip_weight_release", self.handle)

@@ -64,11 +64,18 @@ int ef_hip_event_elapsed_ms(void* start, void* stop, float* ms);
  * Replaces ef::WeightView (include/ef/qkernels.h:28-34): a row-major [rows][cols] matrix in one of
  * the storage types above (row bytes as src/quant.cpp:136-149; Q4_0/Q8_0 need cols % 32 == 0).
  * register_host uploads the bytes once; register_device wraps device bytes the caller owns (no
- * copy).  The handle is what the GEMV entry points take. */
+ * copy).  The handle is what the GEMV entry points take.
+ * Batched products (batch >= 2) of a Q4_0 / Q8_0 handle read a tile-order copy of its bytes, made
+ * on the handle's first batched call (or at engine creation) and freed with the handle; batch 1
+ * reads the bytes in place.  A caller that rewrites a handle's bytes after its first batched use
+ * (ef_hip_quantize into the same buffer, a copy) calls ef_hip_weight_refresh, which rewrites the
+ * copy in place on `stream`, stream-ordered after the write, without allocating (graphs captured
+ * over the handle stay valid); without it batched products keep using the former bytes. */
 typedef struct ef_hip_weight_s* ef_hip_weight;
 int ef_hip_weight_register_host(const void* host_bytes, int qtype, size_t rows, size_t cols, ef_hip_weight* out);
 int ef_hip_weight_register_device(const void* dev_bytes, int qtype, size_t rows, size_t cols, ef_hip_weight* out);
 int ef_hip_weight_release(ef_hip_weight w);
+int ef_hip_weight_refresh(ef_hip_weight w, void* stream);
 int ef_hip_weight_info(ef_hip_weight w, int* qtype, size_t* rows, size_t* cols, const void** dev_bytes);
 int ef_hip_row_bytes(int qtype, size_t cols, size_t* out); /* src/quant.cpp:136-149 */
 
@@ -77,7 +84,8 @@ int ef_hip_row_bytes(int qtype, size_t cols, size_t* out); /* src/quant.cpp:136-
  * Replaces kern::matvec (include/ef/qkernels.h:66, src/qkernels.cpp:275-278) and, with batch > 1,
  * the loop over independent sequences the reference would run.  ldx / ldy are the row strides
  * (in floats) of x and y.  All five storage types, as kern::matvec_rows (src/qkernels.cpp:213-269):
- * Q4_0 / Q8_0 read the 18 / 34-byte blocks in place (cols % 32 == 0, cols <= 14336); F32 / F16 /
+ * Q4_0 / Q8_0 read the 18 / 34-byte blocks (in place at batch 1, from the handle's tile-order copy
+ * at batch >= 2; cols % 32 == 0, cols <= 14336); F32 / F16 /
  * BF16 rows take any cols up to 16320.  Results agree with
  * the reference's FP32 kernels to the rounding of a different summation order (the dot products
  * are reproducible: the same inputs give the same bits on every call). */

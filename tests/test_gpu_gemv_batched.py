@@ -148,3 +148,33 @@ def test_batched_norm_long_rows(hip):
         h = np.empty(cols, np.float32)
         L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), cols, 1e-5)
         assert np.abs(out.numpy()[b] - O.matvec(O.Q4_0, packed.reshape(-1), h)).max() <= ABS_TOL, b
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0])
+def test_refresh_after_rewriting_device_bytes(hip, qtype):
+    """Batched products read a tile-order copy made on first use; ef_hip_weight_refresh rewrites it
+    from the handle's current bytes, so a caller that rewrites the bytes sees the new matrix."""
+    rows, cols, batch = 96, 512, 16
+    print(f"[case] refresh qtype={qtype} {rows}x{cols} B={batch}", flush=True)
+    first = D.random_rows(qtype, rows, cols, seed=11)
+    second = D.random_rows(qtype, rows, cols, seed=12)
+    buf = hip.DeviceArray.from_host(first.reshape(-1))
+    W = hip.Weight(qtype, rows, cols, device=buf)
+    X = _batch_x(77, batch, cols)
+    dx = hip.DeviceArray.from_host(X)
+    dy = hip.DeviceArray((batch, rows))
+    hip.matvec(W, dx, dy, batch=batch)
+    y_first = dy.numpy()
+    buf.upload(second.reshape(-1))
+    hip.matvec(W, dx, dy, batch=batch)
+    assert np.array_equal(dy.numpy(), y_first)  # the copy still holds the former bytes
+    W.refresh()
+    hip.matvec(W, dx, dy, batch=batch)
+    got = dy.numpy()
+    w64 = D.dequant_exact(qtype, second, cols)
+    for b in range(batch):
+        assert D.rel_dot_error(w64, X[b], got[b]).max() < REL_TOL, b
+    # batch 1 reads the bytes in place: the same matrix either way
+    y1 = hip.DeviceArray((rows,))
+    hip.matvec(W, hip.DeviceArray.from_host(X[0]), y1, batch=1)
+    assert np.abs(y1.numpy() - got[0]).max() <= ABS_TOL + 1e-5 * np.abs(got[0]).max()
