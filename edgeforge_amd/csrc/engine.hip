@@ -59,6 +59,7 @@ struct ef_hip_engine_s {
   hipStream_t stream = nullptr;
   float *x = nullptr, *q = nullptr, *knew = nullptr, *vnew = nullptr, *ctx = nullptr, *act = nullptr;
   float *logits = nullptr, *hidden = nullptr, *kc = nullptr, *vc = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+  float* rope_now = nullptr;  // RoPE's cos / sin rows at the step's position (written by embed_at)
   int32_t *hist = nullptr, *hist_len = nullptr, *next_tok = nullptr, *pos = nullptr, *n_prompt = nullptr;
   uint32_t* step_counter = nullptr;  // zero between steps (argmax_finish re-arms it)
   int32_t* out_tokens = nullptr;
@@ -143,7 +144,8 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
   hipStream_t s = e->stream;
   if (groups & kGEmbed)
-    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s));
+    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
+                           e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now));
   AttnArgs a{};
   a.q = e->q;
   a.knew = e->knew;
@@ -151,6 +153,7 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   a.cos_t = e->cos_t;
   a.sin_t = e->sin_t;
   a.pos_dev = e->pos;
+  a.rope_now = e->rope_now;
   a.ctx = e->ctx;
   a.ldq = static_cast<long>(D);
   a.H = static_cast<int>(c.H);
@@ -494,6 +497,7 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
       (rc = dev_alloc(e, &e->logits, B * c.V)) || (rc = dev_alloc(e, &e->hidden, B * c.D)) ||
       (rc = dev_alloc(e, &e->kc, c.L * B * S * kvd)) || (rc = dev_alloc(e, &e->vc, c.L * B * S * kvd)) ||
       (rc = dev_alloc(e, &e->cos_t, S * c.hd / 2)) || (rc = dev_alloc(e, &e->sin_t, S * c.hd / 2)) ||
+      (rc = dev_alloc(e, &e->rope_now, c.hd)) ||
       (rc = dev_alloc(e, &e->hist, B * S)) || (rc = dev_alloc(e, &e->hist_len, B)) ||
       (rc = dev_alloc(e, &e->next_tok, B)) || (rc = dev_alloc(e, &e->pos, 1)) ||
       (rc = dev_alloc(e, &e->n_prompt, 1)) || (rc = dev_alloc(e, &e->out_tokens, B * S)) ||

@@ -14,6 +14,7 @@ struct AttnArgs {
   const float* cos_t;   // [max_seq][hd / 2]
   const float* sin_t;
   const int32_t* pos_dev;
+  const float* rope_now;  // cos then sin rows (hd / 2 each) at *pos_dev, or null (decode only)
   float* ctx;           // [batch][ldq]
   long ldq;
   int H, KV, hd, max_seq;
@@ -33,8 +34,10 @@ int launch_embed_rows(const ef_hip_weight_s* W, const int32_t* hist, long hist_l
                       int rows, float* out, long ldo, hipStream_t s);
 int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s);
 
+// With rope_now, also copies the cos / sin table rows at *pos_dev there (half floats each).
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
-                    float* out, long ldo, hipStream_t s);
+                    float* out, long ldo, hipStream_t s, const float* cos_t = nullptr, const float* sin_t = nullptr,
+                    int half = 0, float* rope_now = nullptr);
 size_t attention_lds_bytes(int hd, int max_seq);
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, int batch, float* out, hipStream_t s);

@@ -38,11 +38,21 @@ __device__ __forceinline__ float decode_elem(const uint8_t* row, int qtype, long
   return static_cast<float>(static_cast<int8_t>(p[2 + j])) * d;
 }
 
-// x[b] = row hist[b][pos] of the embedding table (kern::row_f32 / embedding_bf16).
+// x[b] = row hist[b][pos] of the embedding table (kern::row_f32 / embedding_bf16).  With rope_now,
+// workgroup (0, 0) also copies RoPE's cos and sin rows at pos into rope_now[0, half) and
+// [half, 2 half), so the step's attention launches read them without first reading the position.
 __global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long rows, long cols, long rb,
                                 const int32_t* __restrict__ hist, long hist_ld, const int32_t* __restrict__ pos_dev,
-                                float* __restrict__ out, long ldo) {
+                                float* __restrict__ out, long ldo, const float* __restrict__ cos_t,
+                                const float* __restrict__ sin_t, int half, float* __restrict__ rope_now) {
   const int b = blockIdx.y;
+  if (rope_now != nullptr && blockIdx.x == 0 && b == 0) {
+    const long base = static_cast<long>(*pos_dev) * half;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      rope_now[i] = cos_t[base + i];
+      rope_now[half + i] = sin_t[base + i];
+    }
+  }
   const int32_t id = hist[b * hist_ld + *pos_dev];
   const bool ok = id >= 0 && id < rows;
   const uint8_t* row = W + (ok ? id : 0) * rb;
@@ -316,6 +326,156 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     attend<false>(qs, rows, sc, red, kc, vc, kvd, kn, vn, pos, n_pos, hd, a.scale,
                   a.ctx + static_cast<long>(b) * a.ldq + h * hd, nullptr);
   }
+}
+
+// One wave per (query head h, sequence b) for hd = 64 (the small-batch decode): lane l owns
+// dimension l for RoPE and p.v, and position c0 + l of each 64-position chunk for the scores.
+// Every load that does not need the position is issued at entry: this step's q / k / v, the
+// step's RoPE row (rope_now, required), the first chunk's cached K
+// rows (one row per lane) and V values (one column per lane).  The first 64 rows are in bounds
+// whatever the position (rows past it are never used), so a single memory round trip precedes
+// the arithmetic; softmax and p.v stay inside the wave (DPP reductions, p broadcast by readlane),
+// with no workgroup barrier.  Operation order as attention_kernel: kern::dot_f32's partials and
+// tree per score, float exp(s - max), a double sum, p = e * inv, and p * v accumulated per
+// dimension over positions in increasing order (src/kernels.cpp:27-43,77-92,153-174); the double
+// sum adds lane partials by a DPP tree, so its last bits can differ from the per-head kernel's.
+constexpr int kWaveHd = 64;
+
+__device__ __forceinline__ float dot64_regs(const float* qv, const float4 (&kr)[16]) {
+  float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float4 qa = *reinterpret_cast<const float4*>(qv + 8 * m), qb = *reinterpret_cast<const float4*>(qv + 8 * m + 4);
+    const float4 ka = kr[2 * m], kb = kr[2 * m + 1];
+    p0 += qa.x * ka.x;
+    p1 += qa.y * ka.y;
+    p2 += qa.z * ka.z;
+    p3 += qa.w * ka.w;
+    p4 += qb.x * kb.x;
+    p5 += qb.y * kb.y;
+    p6 += qb.z * kb.z;
+    p7 += qb.w * kb.w;
+  }
+  return ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7));
+}
+
+__global__ __launch_bounds__(kWave) void attention_wave_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  float* qs = sm;                // [64] roped query
+  float* kn = sm + kWaveHd;      // [64] roped new key
+  float* sc = sm + 2 * kWaveHd;  // [max_seq]: scores, then exp, of positions >= 64
+  const int h = blockIdx.x, b = blockIdx.y, l = threadIdx.x;
+  const int hpg = a.H / a.KV, g = h / hpg, kvd = a.KV * kWaveHd;
+  const float* qr = a.q + static_cast<long>(b) * a.ldq + h * kWaveHd;
+  const float* knr = a.knew + static_cast<long>(b) * kvd + g * kWaveHd;
+  const float* vnr = a.vnew + static_cast<long>(b) * kvd + g * kWaveHd;
+  const long seq0 = static_cast<long>(b) * a.max_seq * kvd + g * kWaveHd;
+  // one buffer resource over this (sequence, KV head)'s rows of the layer's cache
+  const uint32_t span = static_cast<uint32_t>(a.max_seq - 1) * static_cast<uint32_t>(kvd) * 4u + kWaveHd * 4u;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kcache + seq0, span);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vcache + seq0, span);
+  const uint32_t row_bytes = static_cast<uint32_t>(kvd) * 4u;
+  const int n0 = min(kWaveHd, a.max_seq);
+
+  // 1. loads, in the order they are consumed (vector-memory loads return in order).  The position
+  //    is a vector load: as a scalar load its wait would also hold back the loads issued after it.
+  const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.pos_dev, 4u), 0u, 0u, 0);
+  const float q0 = qr[l], q1 = qr[l ^ 32], k0 = knr[l], k1 = knr[l ^ 32], vnew = vnr[l];
+  const float cs = a.rope_now[l & 31], sn = a.rope_now[32 + (l & 31)];
+  float4 kr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kr[i] = buf_f4(rk, static_cast<uint32_t>(l) * row_bytes + 16u * i);
+  __builtin_amdgcn_sched_barrier(0);  // the K rows (consumed first) are issued before the V values
+  float vr[kWaveHd];
+#pragma unroll
+  for (int r = 0; r < kWaveHd; ++r)
+    vr[r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, static_cast<uint32_t>(l) * 4u,
+                                                                static_cast<uint32_t>(r) * row_bytes, 0));
+
+  // 2. RoPE on q and the new k (half-split pairs, src/kernels.cpp:133-146); the group's first head
+  //    publishes k / v at pos for later steps
+  const int pos = __builtin_amdgcn_readfirstlane(pos_v);
+  float qrot, krot;
+  if (l < 32) {
+    qrot = q0 * cs - q1 * sn;
+    krot = k0 * cs - k1 * sn;
+  } else {
+    qrot = q0 * cs + q1 * sn;
+    krot = k0 * cs + k1 * sn;
+  }
+  qs[l] = qrot;
+  kn[l] = krot;
+  if (h % hpg == 0) {
+    a.kcache[seq0 + static_cast<long>(pos) * kvd + l] = krot;
+    a.vcache[seq0 + static_cast<long>(pos) * kvd + l] = vnew;
+  }
+  __syncthreads();
+
+  // 3. scores: the first chunk from registers (row pos from kn), later chunks loaded per chunk
+  const int n_pos = pos + 1, c0n = min(n_pos, n0);
+  float s0 = -INFINITY;
+  if (l < c0n) {
+    if (l == pos) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) kr[i] = reinterpret_cast<const float4*>(kn)[i];
+    }
+    s0 = dot64_regs(qs, kr) * a.scale;
+  }
+  float mx = s0;
+  for (int c0 = kWaveHd; c0 < n_pos; c0 += kWaveHd) {
+    const int r = c0 + l;
+    if (r < n_pos) {
+      float4 k4[16];
+      if (r == pos) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) k4[i] = reinterpret_cast<const float4*>(kn)[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) k4[i] = buf_f4(rk, static_cast<uint32_t>(r) * row_bytes + 16u * i);
+      }
+      const float s = dot64_regs(qs, k4) * a.scale;
+      sc[r] = s;
+      mx = fmaxf(mx, s);
+    }
+  }
+
+  // 4. softmax_inplace: max, float exp(s - max), double sum, inv = float(1 / sum)
+  mx = wave_max_dpp(mx);
+  const float e0 = l < c0n ? expf(s0 - mx) : 0.0f;
+  double ssum = static_cast<double>(e0);
+  for (int r = kWaveHd + l; r < n_pos; r += kWaveHd) {
+    const float e = expf(sc[r] - mx);
+    sc[r] = e;
+    ssum += static_cast<double>(e);
+  }
+  const float inv = static_cast<float>(1.0 / wave_sum_d_dpp(ssum));
+  __syncthreads();  // sc[] exps visible to every lane
+
+  // 5. out[l] = sum_t p_t v_t[l], positions in increasing order
+  float o = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kWaveHd; ++r) {
+    if (r < c0n) {
+      const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), r)) * inv;
+      o += p * (r == pos ? vnew : vr[r]);
+    }
+  }
+  for (int c0 = kWaveHd; c0 < n_pos; c0 += kWaveHd) {
+    const int n = min(kWaveHd, n_pos - c0);
+#pragma unroll
+    for (int r = 0; r < kWaveHd; ++r)
+      if (r < n)
+        vr[r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rv, static_cast<uint32_t>(l) * 4u, static_cast<uint32_t>(c0 + r) * row_bytes, 0));
+#pragma unroll
+    for (int r = 0; r < kWaveHd; ++r) {
+      if (r < n) {
+        const float p = sc[c0 + r] * inv;
+        o += p * (c0 + r == pos ? vnew : vr[r]);
+      }
+    }
+  }
+  a.ctx[static_cast<long>(b) * a.ldq + h * kWaveHd + l] = o;
 }
 
 // One (KV group g, sequence b) per workgroup of kGroupThreads: the group's hpg query heads share
@@ -607,10 +767,12 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* __restri
 }  // namespace
 
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
-                    float* out, long ldo, hipStream_t s) {
+                    float* out, long ldo, hipStream_t s, const float* cos_t, const float* sin_t, int half,
+                    float* rope_now) {
   const unsigned gx = static_cast<unsigned>(std::min<size_t>((W->cols + 255) / 256, 16));
   hipLaunchKernelGGL(embed_at_kernel, dim3(gx, batch), dim3(256), 0, s, W->dev, W->qtype, static_cast<long>(W->rows),
-                     static_cast<long>(W->cols), static_cast<long>(W->row_bytes), hist, hist_ld, pos_dev, out, ldo);
+                     static_cast<long>(W->cols), static_cast<long>(W->row_bytes), hist, hist_ld, pos_dev, out, ldo,
+                     cos_t, sin_t, half, rope_now);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }
@@ -657,6 +819,7 @@ int attention_choice() {
   if (v == nullptr) return 0;
   if (std::strcmp(v, "head") == 0) return 1;
   if (std::strcmp(v, "group") == 0) return 2;
+  if (std::strcmp(v, "wave") == 0) return 3;
   return 0;
 }
 
@@ -673,6 +836,15 @@ int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
     hipLaunchKernelGGL(attention_group_kernel, dim3(a.KV, batch), dim3(kGroupThreads), glds, s, a);
     EFH_HIP(hipGetLastError());
     return EF_HIP_OK;
+  }
+  // hd = 64 with the step's RoPE row: one wave per (head, sequence), unless another kernel is forced
+  if (a.hd == kWaveHd && a.rope_now != nullptr && a.H % a.KV == 0 && choice != 1 && choice != 2) {
+    const size_t wlds = (2 * static_cast<size_t>(kWaveHd) + static_cast<size_t>(a.max_seq)) * sizeof(float);
+    if (wlds <= lim) {
+      hipLaunchKernelGGL(attention_wave_kernel, dim3(a.H, batch), dim3(kWave), wlds, s, a);
+      EFH_HIP(hipGetLastError());
+      return EF_HIP_OK;
+    }
   }
   // With few workgroups (latency-bound: a small batch) the decode kernel prefetches the first
   // chunk's K / V rows, stages the V rows in a second LDS buffer and stages every later chunk with

@@ -295,6 +295,41 @@ def test_long_context_decode_matches_oracle(hip):
     eng.close()
 
 
+@pytest.mark.parametrize("kind", ["wave", "head"])
+def test_decode_attention_across_the_first_chunk_matches_oracle(hip, kind, monkeypatch):
+    """Greedy decode from a 58-token prompt through positions 58..69, across the 64-position
+    boundary where the one-wave kernel moves from the rows it loads at entry to loaded chunks;
+    forced per kernel, tokens and every step's logits match the oracle."""
+    print(f"[case] decode across position 64, attention={kind}", flush=True)
+    monkeypatch.setenv("EF_HIP_ATTENTION", kind)
+    dm = DeviceModel.synthetic(LONG, seed=31)
+    om = OracleModel(dm)
+    prompt = [int(v) for v in D.rng(12).integers(0, LONG.V, 58)]
+    want, want_logits, _, _ = om.run_once(prompt, 12)
+    eng = Engine(dm, max_seq=80)
+    got, _, _ = eng.generate([prompt], 12)
+    assert got[0].tolist() == want.tolist()
+    assert _logit_err(eng.logits()[0], want_logits[-1]) < 1e-4
+    eng.close()
+
+
+def test_wave_attention_short_cache_matches_oracle(hip, monkeypatch):
+    """max_seq below 64: the one-wave kernel's entry loads past the cache's last row read zeros
+    through the buffer range and are never used; every position's logits match the oracle."""
+    print("[case] wave attention, max_seq 12", flush=True)
+    monkeypatch.setenv("EF_HIP_ATTENTION", "wave")
+    dm = DeviceModel.synthetic(SMALL, seed=37)
+    om = OracleModel(dm)
+    ids = [int(v) for v in D.rng(10).integers(0, SMALL.V, 12)]
+    eng = Engine(dm, max_seq=len(ids))
+    ot = om.transformer(len(ids))
+    for p, t in enumerate(ids):
+        eng.forward([t], p)
+        assert _logit_err(eng.logits()[0], ot.forward(t, p)) < 1e-4, p
+    ot.close()
+    eng.close()
+
+
 def test_long_context_group_and_head_attention_identical(hip, monkeypatch):
     """Positions 250..261: the per-head kernel (large LDS-DMA chunks) and the KV-group kernel
     (64-row chunks) give identical logits and tokens."""
