@@ -14,6 +14,7 @@
 #include <utility>
 
 #include "glue.h"
+#include "qdot.h"
 
 #pragma clang fp contract(off)
 
@@ -21,22 +22,6 @@ namespace efh {
 namespace {
 
 constexpr int kAttnThreads = 256;
-
-__device__ __forceinline__ float decode_elem(const uint8_t* row, int qtype, long c) {
-  if (qtype == EF_QTYPE_F32) return reinterpret_cast<const float*>(row)[c];
-  if (qtype == EF_QTYPE_BF16) return __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(row)[c]) << 16);
-  if (qtype == EF_QTYPE_F16) return half_bits_to_float(reinterpret_cast<const uint16_t*>(row)[c]);
-  const long blk = c >> 5, j = c & 31;
-  if (qtype == EF_QTYPE_Q4_0) {
-    const uint8_t* p = row + blk * 18;
-    const float d = half_bits_to_float(static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8));
-    const int code = j < 16 ? (p[2 + j] & 15) : (p[2 + j - 16] >> 4);
-    return static_cast<float>(code - 8) * d;
-  }
-  const uint8_t* p = row + blk * 34;
-  const float d = half_bits_to_float(static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8));
-  return static_cast<float>(static_cast<int8_t>(p[2 + j])) * d;
-}
 
 // x[b] = row hist[b][pos] of the embedding table (kern::row_f32 / embedding_bf16).  With rope_now,
 // workgroup (0, 0) also copies RoPE's cos and sin rows at pos into rope_now[0, half) and
@@ -340,24 +325,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 // dimension over positions in increasing order (src/kernels.cpp:27-43,77-92,153-174); the double
 // sum adds lane partials by a DPP tree, so its last bits can differ from the per-head kernel's.
 constexpr int kWaveHd = 64;
-
-__device__ __forceinline__ float dot64_regs(const float* qv, const float4 (&kr)[16]) {
-  float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const float4 qa = *reinterpret_cast<const float4*>(qv + 8 * m), qb = *reinterpret_cast<const float4*>(qv + 8 * m + 4);
-    const float4 ka = kr[2 * m], kb = kr[2 * m + 1];
-    p0 += qa.x * ka.x;
-    p1 += qa.y * ka.y;
-    p2 += qa.z * ka.z;
-    p3 += qa.w * ka.w;
-    p4 += qb.x * kb.x;
-    p5 += qb.y * kb.y;
-    p6 += qb.z * kb.z;
-    p7 += qb.w * kb.w;
-  }
-  return ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7));
-}
 
 __global__ __launch_bounds__(kWave) void attention_wave_kernel(AttnArgs a) {
   extern __shared__ float sm[];

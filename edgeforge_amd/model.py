@@ -196,6 +196,12 @@ class Engine:
 
     PROFILE_GROUPS = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "pick")
 
+    def persistent(self) -> tuple[bool, str]:
+        """Whether decode steps run as one persistent launch, and why not (ef_hip_engine_persistent)."""
+        on, why = C.c_int(0), C.c_char_p()
+        EL.call("ef_hip_engine_persistent", self.h, C.byref(on), C.byref(why))
+        return bool(on.value), (why.value or b"").decode()
+
     def profile(self, reps: int = 20, sampler: dict | None = None, rng: H.RngStates | None = None) -> dict:
         """Milliseconds per step of each kernel group of a decode step (ef_hip_engine_profile)."""
         out = (C.c_double * len(self.PROFILE_GROUPS))()
