@@ -254,8 +254,9 @@ __device__ __forceinline__ void lds_pair(const uint8_t* p, uint32_t (&d)[RR][Pai
 
 // q . k over 64 values, q in LDS and k in registers, in kern::dot_f32's order: partial j sums the
 // products i = j mod 8 in increasing i, then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
-// (src/kernels.cpp:27-43).  Callers compile with contraction off.
+// (src/kernels.cpp:27-43), multiplies and adds kept apart (no contraction into FMA).
 __device__ __forceinline__ float dot64_regs(const float* qv, const float4 (&kr)[16]) {
+#pragma clang fp contract(off)
   float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
