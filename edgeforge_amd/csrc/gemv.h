@@ -45,6 +45,31 @@ int refresh_tiled(const ef_hip_weight_s* w, hipStream_t s);
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 
+// Block-scaled A tables of the matrix-core GEMV, staged by the kernel that produces its input
+// (or by launch_stage_tables): t4 / t8 in the Q4_0 / Q8_0 column orders
+// ([sequence tile][block][hi, lo][64 lanes][16 B], stage_table_bytes each), a power-of-two scale
+// per (block, sequence) at bscale[block * bpad + sequence] (bpad >= stage_bpad(batch)), and for a
+// product with an input RMSNorm n_ssp partial sums of squares of the un-normed input per sequence
+// at ssp[p * bpad + sequence] (the tables then hold norm_w * x; 1 / rms scales the results).
+struct MfmaStage {
+  const uint8_t* t4 = nullptr;
+  const uint8_t* t8 = nullptr;
+  const float* bscale = nullptr;
+  int bpad = 0;
+  const double* ssp = nullptr;
+  int n_ssp = 0;
+  float eps = 0.0f;
+};
+size_t stage_table_bytes(int K, int batch);
+int stage_bpad(int batch);
+// The tables from x [batch][ldx] (one partial sum per sequence; norm_w may be null).
+int launch_stage_tables(const float* x, size_t ldx, int K, int batch, const float* norm_w, const MfmaStage& st,
+                        hipStream_t stream);
+// The batched product over staged tables (one launch of <= 1024 sequences; ws as for launch_gemv,
+// gemv_mfma_workspace_bytes of the same jobs).
+int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const MfmaStage& st, int batch, size_t ldy,
+                            void* ws, size_t ws_bytes, hipStream_t stream);
+
 // F32 / F16 / BF16 weights (gemv_dense.hip): same jobs, epilogues and fused RMSNorm, any cols up to
 // kMaxDenseCols; all jobs of one launch share the type.  launch_gemv routes these types here.
 constexpr size_t kMaxDenseCols = 16320;

@@ -42,6 +42,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 
 #include "gemv.h"
 
@@ -81,6 +82,16 @@ struct MArgs {
   const float* post;    // [B] 2^e_s
   int ksplit, blocks_per_split;   // split-K: workgroups per row group and blocks each
   float* part;          // [group][split][B][rows of the group][matrices] partial sums (ksplit > 1)
+  // Block-scaled tables (staged by the producing kernel): every (sequence, block) has its own power
+  // of two, bscale[block * bpad + sequence], by which the block's products are multiplied; the
+  // epilogue factor is 1 / rms from ssp[p * bpad + sequence] (n_ssp partial sums of squares of the
+  // un-normed input, eps) or 1 without ssp.  post_out gets those factors for finalize_kernel.
+  const float* bscale;
+  int bpad;
+  const double* ssp;
+  int n_ssp;
+  float eps;
+  float* post_out;
 };
 
 struct PrepArgs {
@@ -433,6 +444,114 @@ __global__ __launch_bounds__(kSeqPrepThreads) void xfrag_seq_kernel(PrepArgs a) 
   }
 }
 
+// Block-scaled tables from activations in memory (no kernel staged them): one workgroup per
+// sequence, thread t owns pairs t + 256 j (pair = block kb, k group g), so the four threads of a
+// block hold its 32 values.  Each (sequence, block) gets its own power of two 2^e (|v| 2^-e < 2^15
+// for v = norm_w * x, or x), written to bscale[kb * bpad + seq]; the fragments hold v 2^-e split
+// into fp16 hi + lo in the tables' slot orders; ssp[seq] (one partial per sequence) is the double
+// sum of x^2, kern::rmsnorm's statistic, applied by the GEMV's epilogue as 1 / rms.
+__global__ __launch_bounds__(kSeqPrepThreads) void xfrag_block_kernel(PrepArgs a, float* bscale, int bpad,
+                                                                       double* ssp) {
+  __shared__ double s_ss[kSeqPrepThreads / kWave];
+  const int sq = blockIdx.x, tile = sq / kSeqTile, i = sq % kSeqTile;
+  const int K = a.K, nb = K >> 5, npairs = nb * 4;
+  const int t = threadIdx.x, wave = t / kWave, lane = t & (kWave - 1);
+  const bool has_norm = a.norm_w != nullptr, live = sq < a.B;
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 4u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (live ? sq : 0) * a.ldx, live ? row_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, has_norm ? row_bytes : 0u);
+  auto offs = [&](int pr, bool q4, uint32_t (&o)[2]) {
+    const uint32_t kb = static_cast<uint32_t>(pr >> 2), g = static_cast<uint32_t>(pr & 3);
+    const uint32_t base = pr < npairs ? kb * 128u : row_bytes;
+    o[0] = base + (q4 ? 16u * g : 32u * g);
+    o[1] = base + (q4 ? 64u + 16u * g : 32u * g + 16u);
+  };
+  f4v xv[kSeqPrepPairs][2], wv[kSeqPrepPairs][2];
+#pragma unroll
+  for (int j = 0; j < kSeqPrepPairs; ++j) {
+    uint32_t o[2];
+    offs(t + kSeqPrepThreads * j, true, o);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rx, o[h], 0, 0));
+      wv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rw, o[h], 0, 0));
+    }
+  }
+  double ss = 0.0;
+  float pre[kSeqPrepPairs];
+#pragma unroll
+  for (int j = 0; j < kSeqPrepPairs; ++j) {
+    float m = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = xv[j][h][e];
+        ss += static_cast<double>(x) * static_cast<double>(x);
+        m = fmaxf(m, fabsf(has_norm ? wv[j][h][e] * x : x));
+      }
+    // the block's four threads (pairs 4 kb .. 4 kb + 3 are threads of one quad)
+    m = fmaxf(m, dpp_self_f<0xB1>(m));
+    m = fmaxf(m, dpp_self_f<0x4E>(m));
+    const float bound = m * 1.0001f;
+    int ex = 0;
+    if (bound > 0.0f && bound <= 3.0e38f) ex = ilogbf(bound) - 14;  // bound * 2^-ex < 2^15
+    pre[j] = ldexpf(1.0f, -ex);
+    const int pr = t + kSeqPrepThreads * j;
+    if ((pr & 3) == 0 && pr < npairs && live) bscale[static_cast<size_t>(pr >> 2) * bpad + sq] = ldexpf(1.0f, ex);
+  }
+  ss = wave_sum_d_dpp(ss);
+  if (lane == 0) s_ss[wave] = ss;
+  __syncthreads();
+  if (t == 0 && live) {
+    double tot = 0.0;
+    for (int w = 0; w < kSeqPrepThreads / kWave; ++w) tot += s_ss[w];
+    ssp[sq] = tot;
+  }
+  auto emit = [&](uint8_t* table, int pr, const f4v (&x2)[2], const f4v (&w2)[2], float pscale, bool q4) {
+    if (pr >= npairs) return;
+    float v[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * h + e] = (has_norm ? w2[h][e] * x2[h][e] : x2[h][e]) * pscale;
+    constexpr int ord4[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    constexpr int ord8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    h8 hi, lo;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float xp = v[q4 ? ord4[u] : ord8[u]];
+      const _Float16 hh = static_cast<_Float16>(xp);
+      const _Float16 ll = static_cast<_Float16>(xp - static_cast<float>(hh));
+      const _Float16 qs = static_cast<_Float16>(q4 && (u & 2) ? 0.0625f : 1.0f);
+      hi[u] = hh * qs;
+      lo[u] = ll * qs;
+    }
+    const int kb = pr >> 2, g = pr & 3;
+    uint8_t* f = table + ((static_cast<size_t>(tile) * nb + kb) * 2 * kWave + (16 * g + i)) * 16;
+    *reinterpret_cast<h8*>(f) = hi;
+    *reinterpret_cast<h8*>(f + kWave * 16) = lo;
+  };
+  if (a.t4 != nullptr) {
+#pragma unroll
+    for (int j = 0; j < kSeqPrepPairs; ++j) emit(a.t4, t + kSeqPrepThreads * j, xv[j], wv[j], pre[j], true);
+  }
+  if (a.t8 != nullptr) {  // the Q8_0 order's values
+#pragma unroll
+    for (int j = 0; j < kSeqPrepPairs; ++j) {
+      uint32_t o[2];
+      offs(t + kSeqPrepThreads * j, false, o);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        xv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rx, o[h], 0, 0));
+        wv[j][h] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rw, o[h], 0, 0));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kSeqPrepPairs; ++j) emit(a.t8, t + kSeqPrepThreads * j, xv[j], wv[j], pre[j], false);
+  }
+}
+
 // Weights in tile order: for every 16-row tile T and block b, the 16 rows' codes in the order the
 // B fragment's lanes use them (lane l = 16 g + j: row j's code bytes 4g .. 4g + 3 of a Q4_0 block,
 // 8g .. 8g + 7 of a Q8_0 block), then the 16 rows' fp16 scales: 288 (Q4_0) or 544 (Q8_0) bytes at
@@ -489,9 +608,9 @@ __device__ __forceinline__ WRegs<Q4> load_w(__amdgpu_buffer_rsrc_t r, uint32_t v
 // the matrix core, the vector ALU converts unit u + 1's codes and applies unit u - 1's scales, so
 // neither pipe waits on the other (each stage is kept together by a scheduling barrier, and inside
 // it products and vector instructions alternate).
-template <int RT, int NM, int NS, bool Q4>
+template <int RT, int NM, int NS, bool Q4, bool BS = false>
 __device__ __forceinline__ void block_products(const WRegs<Q4> (&W)[RT][NM], const h8 (&Ax)[NS][2],
-                                               f4v (&acc)[RT][NM][NS]) {
+                                               f4v (&acc)[RT][NM][NS], const f4v (&Sc)[NS]) {
   constexpr int U = RT * NM;
   const f4v Z = {0.0f, 0.0f, 0.0f, 0.0f};
   auto operand = [&](int u) -> h8 {
@@ -514,7 +633,7 @@ __device__ __forceinline__ void block_products(const WRegs<Q4> (&W)[RT][NM], con
 #pragma unroll
       for (int t = 0; t < NS; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(d, Dp[t][r], acc[rt][mt][t][r]);
+        for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(BS ? d * Sc[t][r] : d, Dp[t][r], acc[rt][mt][t][r]);
     }
     if (u + 1 < U) b = operand(u + 1);
 #pragma unroll
@@ -533,17 +652,18 @@ __device__ __forceinline__ void block_products(const WRegs<Q4> (&W)[RT][NM], con
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(d, Dp[t][r], acc[rt][mt][t][r]);
+      for (int r = 0; r < 4; ++r) acc[rt][mt][t][r] = fmaf(BS ? d * Sc[t][r] : d, Dp[t][r], acc[rt][mt][t][r]);
   }
 }
 
 // The wave's blocks b = kb0 + wave + 8 i < kb1: the weights two blocks ahead and the A fragments
 // one block ahead are loaded while the current block's products run.  Prefetches past the row
 // read its last block instead, so they need no bounds test.
-template <int RT, int NM, int NS, bool Q4>
+template <int RT, int NM, int NS, bool Q4, bool BS = false>
 __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, int kb0, int kb1, int wave, int lane,
                                        __amdgpu_buffer_rsrc_t tab, uint32_t tile0, uint32_t tstride,
-                                       f4v (&acc)[RT][NM][NS]) {
+                                       f4v (&acc)[RT][NM][NS], __amdgpu_buffer_rsrc_t bsr, uint32_t bpad,
+                                       uint32_t seq0) {
   const uint32_t bb = Q4 ? kTileBlockQ4 : kTileBlockQ8;
   const int last_tile = static_cast<int>(jb.bytes / (static_cast<uint32_t>(nb) * bb)) - 1;
   const __amdgpu_buffer_rsrc_t r1 = make_rsrc(jb.W, jb.bytes);
@@ -578,19 +698,35 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
   // unconditionally (a block past this workgroup's range is read and never used), so every path
   // has the same loads in flight and the wait before each block's products covers only that
   // block's loads.
+  // block scales of the lane's four sequences (4 (l / 16) .. + 3 of each tile) with the A fragments
+  auto load_s = [&](f4v (&dst)[NS], int kb) {
+    if constexpr (BS) {
+      kb = min(kb, nb - 1);
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        const uint32_t off = (static_cast<uint32_t>(kb) * bpad + seq0 + t * kSeqTile + 4u * (lane >> 4)) * 4u;
+        dst[t] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(bsr, off, 0, 0));
+      }
+    }
+  };
   WRegs<Q4> W[kMaxBlocksPerWave][RT][NM];
   h8 A[2][NS][2];
+  f4v Sc[2][NS];
   const int kb = kb0 + wave;
   load_wb(W[0], kb);
   load_wb(W[1], kb + kWavesM);
   load_a(A[0], kb);
+  load_s(Sc[0], kb);
 #pragma unroll
   for (int i = 0; i < kMaxBlocksPerWave; ++i) {
     const int b = kb + i * kWavesM;
     if (b >= kb1) break;
-    if (i + 1 < kMaxBlocksPerWave) load_a(A[(i + 1) & 1], b + kWavesM);
+    if (i + 1 < kMaxBlocksPerWave) {
+      load_a(A[(i + 1) & 1], b + kWavesM);
+      load_s(Sc[(i + 1) & 1], b + kWavesM);
+    }
     if (i + 2 < kMaxBlocksPerWave) load_wb(W[i + 2], b + 2 * kWavesM);
-    block_products<RT, NM, NS, Q4>(W[i], A[i & 1], acc);
+    block_products<RT, NM, NS, Q4, BS>(W[i], A[i & 1], acc, Sc[i & 1]);
   }
 }
 
@@ -602,7 +738,8 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
 template <int EPI, int RT, int NS>
 __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb, uint8_t* lb,
                                                   const f4v (&acc)[RT][EPI == kEpiSwiglu ? 2 : 1][NS], int wave,
-                                                  int lane, int row0, int grp, int ks, int s0) {
+                                                  int lane, int row0, int grp, int ks, int s0, const float* post_p,
+                                                  int post_base) {
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
   constexpr int F = RT * NS;                       // fragments per matrix
@@ -641,7 +778,7 @@ __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb
         continue;
       }
       if (row >= jb.rows) continue;
-      const float post = a.post[sq];
+      const float post = post_p[sq - post_base];
       float* y = jb.y + sq * jb.ldy + row;
       if (EPI == kEpiResidual) {
         *y = *y + v[0][r] * post;
@@ -655,9 +792,11 @@ __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb
 }
 
 // RT row tiles of 16 rows per workgroup, NS sequence tiles of 16 sequences per workgroup.
-template <int EPI, int RT, int NS>
+// BS: block-scaled tables staged by the producing kernel (no preparation launch).
+template <int EPI, int RT, int NS, bool BS>
 __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lb[];
+  __shared__ float s_post[BS ? NS * kSeqTile : 1];
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int ROWS = RT * kTileRows;
   const int nb = a.K >> 5;
@@ -682,13 +821,39 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
 #pragma unroll
       for (int t = 0; t < NS; ++t) acc[rt][mt][t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
   const int tile_row0 = row0 / kTileRows;
-  if (q4) {
-    k_loop<RT, NM, NS, true>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc);
+  if constexpr (BS) {
+    // the epilogue factor of each of this workgroup's sequences: 1 / rms from the producer's
+    // partial sums (in index order), or 1; the first row group's first split also hands them to
+    // finalize_kernel
+    if (threadIdx.x < NS * kSeqTile) {
+      const int sq = s0 + threadIdx.x;
+      float f = 1.0f;
+      if (a.ssp != nullptr && sq < a.B) {
+        double tot = 0.0;
+        for (int p = 0; p < a.n_ssp; ++p) tot += a.ssp[static_cast<size_t>(p) * a.bpad + sq];
+        f = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(a.K) + static_cast<double>(a.eps)));
+      }
+      s_post[threadIdx.x] = f;
+      if (a.post_out != nullptr && blockIdx.x == 0 && sq < a.B) a.post_out[sq] = f;
+    }
+    const __amdgpu_buffer_rsrc_t bsr =
+        make_rsrc(a.bscale, static_cast<uint32_t>(nb) * static_cast<uint32_t>(a.bpad) * 4u);
+    if (q4) {
+      k_loop<RT, NM, NS, true, true>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc, bsr,
+                                     static_cast<uint32_t>(a.bpad), static_cast<uint32_t>(s0));
+    } else {
+      k_loop<RT, NM, NS, false, true>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc, bsr,
+                                      static_cast<uint32_t>(a.bpad), static_cast<uint32_t>(s0));
+    }
+    combine_and_store<EPI, RT, NS>(a, jb, lb, acc, wave, lane, row0, grp, ks, s0, s_post, s0);
   } else {
-    k_loop<RT, NM, NS, false>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc);
+    if (q4) {
+      k_loop<RT, NM, NS, true>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc, tab, 0u, 0u);
+    } else {
+      k_loop<RT, NM, NS, false>(jb, tile_row0, nb, kb0, kb1, wave, lane, tab, tile0, tstride, acc, tab, 0u, 0u);
+    }
+    combine_and_store<EPI, RT, NS>(a, jb, lb, acc, wave, lane, row0, grp, ks, s0, a.post, 0);
   }
-
-  combine_and_store<EPI, RT, NS>(a, jb, lb, acc, wave, lane, row0, grp, ks, s0);
 }
 
 struct FinArgs {
@@ -738,22 +903,22 @@ struct Shape {
 constexpr Shape kShapesStore[] = {{2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {4, 4}, {8, 1}, {8, 2}};
 constexpr Shape kShapesSwiglu[] = {{2, 1}, {2, 2}, {2, 4}, {3, 1}, {3, 2}, {4, 1}, {4, 2}};
 
-template <int EPI, int RT, int NS>
+template <int EPI, int RT, int NS, bool BS>
 void* kfn() {
-  return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, NS>);
+  return reinterpret_cast<void*>(&gemv_mfma_kernel<EPI, RT, NS, BS>);
 }
 
 // The instantiated kernel of shape (rt, ns): one of kShapesStore / kShapesSwiglu.
-template <int EPI>
+template <int EPI, bool BS = false>
 void* pick_mfma(int rt, int ns) {
   if constexpr (EPI == kEpiSwiglu) {
-    if (rt == 4) return ns == 2 ? kfn<EPI, 4, 2>() : kfn<EPI, 4, 1>();
-    if (rt == 3) return ns == 2 ? kfn<EPI, 3, 2>() : kfn<EPI, 3, 1>();
-    return ns == 4 ? kfn<EPI, 2, 4>() : (ns == 2 ? kfn<EPI, 2, 2>() : kfn<EPI, 2, 1>());
+    if (rt == 4) return ns == 2 ? kfn<EPI, 4, 2, BS>() : kfn<EPI, 4, 1, BS>();
+    if (rt == 3) return ns == 2 ? kfn<EPI, 3, 2, BS>() : kfn<EPI, 3, 1, BS>();
+    return ns == 4 ? kfn<EPI, 2, 4, BS>() : (ns == 2 ? kfn<EPI, 2, 2, BS>() : kfn<EPI, 2, 1, BS>());
   } else {
-    if (rt == 8) return ns == 2 ? kfn<EPI, 8, 2>() : kfn<EPI, 8, 1>();
-    if (rt == 4) return ns == 4 ? kfn<EPI, 4, 4>() : (ns == 2 ? kfn<EPI, 4, 2>() : kfn<EPI, 4, 1>());
-    return ns == 4 ? kfn<EPI, 2, 4>() : (ns == 2 ? kfn<EPI, 2, 2>() : kfn<EPI, 2, 1>());
+    if (rt == 8) return ns == 2 ? kfn<EPI, 8, 2, BS>() : kfn<EPI, 8, 1, BS>();
+    if (rt == 4) return ns == 4 ? kfn<EPI, 4, 4, BS>() : (ns == 2 ? kfn<EPI, 4, 2, BS>() : kfn<EPI, 4, 1, BS>());
+    return ns == 4 ? kfn<EPI, 2, 4, BS>() : (ns == 2 ? kfn<EPI, 2, 2, BS>() : kfn<EPI, 2, 1, BS>());
   }
 }
 
@@ -943,11 +1108,71 @@ size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int b
   return p.ok ? p.bytes : 0;
 }
 
+namespace {
+// EF_HIP_MFMA_TABLES=block: batched products go through block-scaled tables made by
+// launch_stage_tables (the path producer-staged inputs take), for testing that path on any input.
+bool block_tables_forced() {
+  const char* v = std::getenv("EF_HIP_MFMA_TABLES");
+  return v != nullptr && std::strcmp(v, "block") == 0;
+}
+}  // namespace
+
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken) {
   *taken = false;
   const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, ldx);
   if (!pl.ok) return EF_HIP_OK;
+  if (block_tables_forced() && jobs[0].W->cols <= static_cast<size_t>(kSeqPrepMaxK)) {
+    const int K = static_cast<int>(jobs[0].W->cols);
+    const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
+    int rc = EF_HIP_OK;
+    for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += pl.chunk) {
+      const int nb = std::min(pl.chunk, batch - b0);
+      const int bpad = stage_bpad(nb);
+      const size_t tb = stage_table_bytes(K, nb);
+      const size_t need = (pl.q4 ? tb : 0) + (pl.q8 ? tb : 0) + static_cast<size_t>(K / 32) * bpad * 4 + bpad * 8 + 256 +
+                          pl.bytes;
+      uint8_t* buf = nullptr;
+      EFH_HIP(hipMallocAsync(reinterpret_cast<void**>(&buf), need, stream));
+      MfmaStage st{};
+      size_t off = 0;
+      if (pl.q4) {
+        st.t4 = buf + off;
+        off += tb;
+      }
+      if (pl.q8) {
+        st.t8 = buf + off;
+        off += tb;
+      }
+      st.bscale = reinterpret_cast<float*>(buf + off);
+      off += static_cast<size_t>(K / 32) * bpad * 4;
+      off = (off + 15) & ~size_t(15);
+      st.ssp = reinterpret_cast<double*>(buf + off);  // written by the preparation either way
+      off += static_cast<size_t>(bpad) * 8;
+      off = (off + 255) & ~size_t(255);
+      st.bpad = bpad;
+      st.n_ssp = 1;
+      st.eps = eps;
+      MfmaStage mk = st;
+      if (norm_w == nullptr) {  // the product has no RMSNorm: its epilogue factor is 1
+        st.ssp = nullptr;
+        st.n_ssp = 0;
+      }
+      rc = launch_stage_tables(jobs[0].x + b0 * xld, xld, K, nb, norm_w, mk, stream);
+      GemvJob cj[kMaxJobsM];
+      for (int j = 0; j < n_jobs; ++j) {
+        cj[j] = jobs[j];
+        const size_t yld = jobs[j].ldy ? jobs[j].ldy : ldy;
+        cj[j].y = jobs[j].y + b0 * yld;
+        cj[j].ldy = yld;
+      }
+      if (rc == EF_HIP_OK) rc = launch_gemv_mfma_staged(cj, n_jobs, epi, st, nb, ldy, buf + off, pl.bytes, stream);
+      const hipError_t e = hipFreeAsync(buf, stream);
+      if (e != hipSuccess && rc == EF_HIP_OK) rc = fail_hip(e, "hipFreeAsync");
+    }
+    if (rc == EF_HIP_OK) *taken = true;
+    return rc;
+  }
   if (norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 != 0) return EF_HIP_OK;
   for (int j = 0; j < n_jobs; ++j) {
     EFH_RC(ensure_tiled(jobs[j].W, stream));
@@ -1048,6 +1273,106 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
   }
   if (rc == EF_HIP_OK) *taken = true;
   return rc;
+}
+
+
+size_t stage_table_bytes(int K, int batch) {
+  const size_t tiles = (static_cast<size_t>(batch) + kSeqTile - 1) / kSeqTile;
+  return tiles * static_cast<size_t>(K / 32) * 2 * kWave * 16;
+}
+int stage_bpad(int batch) { return ((batch + kSeqTile - 1) / kSeqTile) * kSeqTile; }
+
+int launch_stage_tables(const float* x, size_t ldx, int K, int batch, const float* norm_w, const MfmaStage& st,
+                        hipStream_t stream) {
+  EFH_CHECK(K % 32 == 0 && K <= kSeqPrepMaxK && batch >= 1 && batch <= kMaxTiles * kSeqTile,
+            "stage_tables: K must be a multiple of 32 up to 8192, batch in [1, 1024]");
+  EFH_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0, "stage_tables: x rows must be 16-byte aligned");
+  EFH_CHECK(st.bpad >= stage_bpad(batch) && st.bscale && st.ssp && (st.t4 || st.t8), "stage_tables: outputs");
+  PrepArgs p{};
+  p.x = x;
+  p.ldx = static_cast<long>(ldx);
+  p.K = K;
+  p.B = batch;
+  p.norm_w = norm_w;
+  p.t4 = const_cast<uint8_t*>(st.t4);
+  p.t8 = const_cast<uint8_t*>(st.t8);
+  hipLaunchKernelGGL(xfrag_block_kernel, dim3(batch), dim3(kSeqPrepThreads), 0, stream, p,
+                     const_cast<float*>(st.bscale), st.bpad, const_cast<double*>(st.ssp));
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const MfmaStage& st, int batch, size_t ldy,
+                            void* ws, size_t ws_bytes, hipStream_t stream) {
+  const size_t K = jobs[0].W->cols;
+  const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, K);
+  EFH_CHECK(pl.ok, "gemv_mfma_staged: no matrix-core plan for this launch");
+  EFH_CHECK(batch <= pl.chunk, "gemv_mfma_staged: more sequences than one launch covers");
+  EFH_CHECK((!pl.q4 || st.t4) && (!pl.q8 || st.t8), "gemv_mfma_staged: a table of the launch's column order is missing");
+  EFH_CHECK(st.bscale != nullptr && st.bpad >= stage_bpad(batch), "gemv_mfma_staged: block scales");
+  EFH_CHECK(ws != nullptr && ws_bytes >= pl.bytes, "gemv_mfma_staged: workspace too small");
+  for (int j = 0; j < n_jobs; ++j) {
+    EFH_RC(ensure_tiled(jobs[j].W, stream));
+    if (jobs[j].W2 != nullptr) EFH_RC(ensure_tiled(jobs[j].W2, stream));
+  }
+  uint8_t* base = static_cast<uint8_t*>(ws);
+  float* post = reinterpret_cast<float*>(base + (pl.q4 ? pl.tab : 0) + (pl.q8 ? pl.tab : 0));
+  MArgs a{};
+  a.ksplit = pl.S;
+  a.blocks_per_split = pl.bps;
+  a.part = reinterpret_cast<float*>(base + pl.part_off);
+  a.n_jobs = n_jobs;
+  a.K = static_cast<int>(K);
+  a.B = batch;
+  a.n_tiles = pl.NT;
+  a.t4 = st.t4;
+  a.t8 = st.t8;
+  a.tab_bytes = static_cast<uint32_t>(stage_table_bytes(static_cast<int>(K), batch));
+  a.post = post;
+  a.bscale = st.bscale;
+  a.bpad = st.bpad;
+  a.ssp = st.ssp;
+  a.n_ssp = st.n_ssp;
+  a.eps = st.eps;
+  a.post_out = pl.S > 1 ? post : nullptr;
+  const int rows_wg = pl.RT * kTileRows;
+  int tiles = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    MJob& d = a.job[j];
+    const size_t yld = jobs[j].ldy ? jobs[j].ldy : ldy;
+    d.W = jobs[j].W->tiled;
+    d.W2 = jobs[j].W2 ? jobs[j].W2->tiled : nullptr;
+    d.y = jobs[j].y;
+    d.rows = static_cast<int>(jobs[j].W->rows);
+    d.qtype = jobs[j].W->qtype;
+    d.bytes = static_cast<uint32_t>(tiled_bytes(jobs[j].W));
+    d.ldy = static_cast<long>(yld);
+    d.tile_begin = tiles;
+    tiles += (d.rows + rows_wg - 1) / rows_wg;
+  }
+  void* fn = epi == kEpiStore ? pick_mfma<kEpiStore, true>(pl.RT, pl.NS)
+                              : (epi == kEpiResidual ? pick_mfma<kEpiResidual, true>(pl.RT, pl.NS)
+                                                     : pick_mfma<kEpiSwiglu, true>(pl.RT, pl.NS));
+  void* params[] = {&a};
+  const int sg = std::min(pl.SG, (batch + pl.NS * kSeqTile - 1) / (pl.NS * kSeqTile));
+  EFH_HIP(hipLaunchKernel(fn, dim3(tiles * pl.S, sg), dim3(kT), params, pl.lds, stream));
+  if (pl.S > 1) {
+    FinArgs f{};
+    for (int j = 0; j < n_jobs; ++j) f.job[j] = a.job[j];
+    f.n_jobs = n_jobs;
+    f.B = batch;
+    f.rows_wg = rows_wg;
+    f.S = pl.S;
+    f.total = tiles * rows_wg * batch;
+    f.part = a.part;
+    f.post = post;
+    void* fin = epi == kEpiStore ? reinterpret_cast<void*>(&finalize_kernel<kEpiStore>)
+                                 : (epi == kEpiResidual ? reinterpret_cast<void*>(&finalize_kernel<kEpiResidual>)
+                                                        : reinterpret_cast<void*>(&finalize_kernel<kEpiSwiglu>));
+    void* fparams[] = {&f};
+    EFH_HIP(hipLaunchKernel(fin, dim3((f.total + 255) / 256), dim3(256), fparams, 0, stream));
+  }
+  return EF_HIP_OK;
 }
 
 }  // namespace efh
