@@ -133,6 +133,7 @@ SIGNATURES = {
     "ef_hip_engine_profile": (C.c_int, [_P, C.POINTER(ef_hip_sampler_config), _P, C.c_int,
                                         C.POINTER(C.c_double)]),
     "ef_hip_engine_persistent": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
+    "ef_hip_engine_tables": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
     "ef_hip_engine_forward": (C.c_int, [_P, _i32p, _sz, C.c_int]),
     "ef_hip_engine_prefill": (C.c_int, [_P, _i32p, _sz, _sz, C.c_int]),
     "ef_hip_engine_logits": (C.c_int, [_P, C.POINTER(_P)]),

@@ -18,6 +18,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <vector>
 
@@ -95,6 +96,15 @@ struct ef_hip_engine_s {
   unsigned* step_sync = nullptr;
   bool step_on = false;
   std::string step_why;  // why the persistent step is off (empty when on)
+  // several-sequence step over producer-staged tables (afrag.h): table set a holds the inputs of
+  // q/k/v, gate/up and lm_head (K = D, with the RMSNorm's per-block partial sums), set b those of
+  // o_proj and down; each set has both column orders
+  bool staged = false;
+  std::string staged_why;  // why the staged step is off (empty when on)
+  uint8_t *ta4 = nullptr, *ta8 = nullptr, *tb4 = nullptr, *tb8 = nullptr;
+  float *ta_s = nullptr, *tb_s = nullptr;
+  double *ta_ssp = nullptr, *tb_ssp = nullptr;
+  int bpad = 0;
 };
 
 namespace efh {
@@ -133,7 +143,7 @@ int check_matrix(ef_hip_weight w, size_t rows, size_t cols, const char* what) {
 }
 
 
-int enqueue_tail(ef_hip_engine e, int mode, unsigned groups = kAllGroups);
+int enqueue_tail(ef_hip_engine e, int mode, unsigned groups = kAllGroups, bool staged_in = false);
 
 // hist[b][pos .. pos + n) = stage[b * n .. b * n + n) for every sequence b: one contiguous copy of
 // the pinned staging words (plus the 8 words after them) to the device, then a row-copy kernel into
@@ -285,18 +295,8 @@ int build_step(ef_hip_engine e) {
   return EF_HIP_OK;
 }
 
-int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
+AttnArgs attn_args(ef_hip_engine e) {
   const ef_hip_model_config& c = e->c;
-  const int B = e->B;
-  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
-  hipStream_t s = e->stream;
-  if (e->step_on && groups == kAllGroups) {  // the embedding and every layer in one launch
-    EFH_RC(launch_step(step_args(e), s));
-    return enqueue_tail(e, mode, groups);
-  }
-  if (groups & kGEmbed)
-    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
-                           e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now));
   AttnArgs a{};
   a.q = e->q;
   a.knew = e->knew;
@@ -306,12 +306,201 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   a.pos_dev = e->pos;
   a.rope_now = e->rope_now;
   a.ctx = e->ctx;
-  a.ldq = static_cast<long>(D);
+  a.ldq = static_cast<long>(c.D);
   a.H = static_cast<int>(c.H);
   a.KV = static_cast<int>(c.KV);
   a.hd = static_cast<int>(c.hd);
-  a.max_seq = static_cast<int>(S);
+  a.max_seq = static_cast<int>(e->max_seq);
   a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.hd)));  // src/kernels.cpp:158
+  return a;
+}
+
+// Staging of a product's input tables: set a (with the norm's partial sums, norm weights nw) or
+// set b, in the column orders of the consuming matrices.
+AEmit table_emit(ef_hip_engine e, bool set_a, std::initializer_list<ef_hip_weight> consumers, const float* nw,
+                 size_t K) {
+  AEmit m{};
+  bool q4 = false, q8 = false;
+  for (ef_hip_weight w : consumers) {
+    q4 = q4 || w->qtype == EF_QTYPE_Q4_0;
+    q8 = q8 || w->qtype == EF_QTYPE_Q8_0;
+  }
+  m.t4 = q4 ? (set_a ? e->ta4 : e->tb4) : nullptr;
+  m.t8 = q8 ? (set_a ? e->ta8 : e->tb8) : nullptr;
+  m.bscale = set_a ? e->ta_s : e->tb_s;
+  m.ssp = set_a ? e->ta_ssp : nullptr;
+  m.nw = nw;
+  m.nb = static_cast<int>(K / 32);
+  m.bpad = e->bpad;
+  return m;
+}
+
+MfmaStage table_set(ef_hip_engine e, bool set_a) {
+  MfmaStage st{};
+  st.t4 = set_a ? e->ta4 : e->tb4;
+  st.t8 = set_a ? e->ta8 : e->tb8;
+  st.bscale = set_a ? e->ta_s : e->tb_s;
+  st.bpad = e->bpad;
+  if (set_a) {
+    st.ssp = e->ta_ssp;
+    st.n_ssp = static_cast<int>(e->c.D / 32);
+    st.eps = e->c.eps;
+  }
+  return st;
+}
+
+// The step's product jobs of layer l (q/k/v, o, gate/up, down) and lm_head.
+struct LayerJobs {
+  GemvJob qkv[3], o, gu, dn;
+};
+LayerJobs layer_jobs(ef_hip_engine e, size_t l) {
+  const ef_hip_layer& w = e->layers[l];
+  const size_t D = e->c.D, F = e->c.F, kvd = e->kvd;
+  return LayerJobs{{{w.wq, nullptr, e->x, e->q, D, D}, {w.wk, nullptr, e->x, e->knew, D, kvd},
+                    {w.wv, nullptr, e->x, e->vnew, D, kvd}},
+                   {w.wo, nullptr, e->ctx, e->x, D, D},
+                   {w.w_gate, w.w_up, e->x, e->act, D, F},
+                   {w.w_down, nullptr, e->act, e->x, F, D}};
+}
+GemvJob lm_job(ef_hip_engine e) { return GemvJob{e->lm_head, nullptr, e->x, e->logits, e->c.D, e->c.V}; }
+
+// Whether the several-sequence step runs over producer-staged tables: the embedding lookup, the
+// KV-group attention and the o / gate-up / down products write the next product's input tables as
+// they store their outputs (afrag.h), so no product runs a preparation launch (the o projection
+// gets one when the attention kernel is not the KV-group one).  Needs packed matrices with a
+// matrix-core plan for every product; EF_HIP_DECODE_TABLES=prep keeps the per-product preparation.
+// Allocates the table sets and grows the GEMV workspace to the staged plans.
+int build_staged(ef_hip_engine e) {
+  const ef_hip_model_config& c = e->c;
+  e->staged = false;
+  const char* env = std::getenv("EF_HIP_DECODE_TABLES");
+  if (env != nullptr && std::strcmp(env, "prep") == 0) {
+    e->staged_why = "off: EF_HIP_DECODE_TABLES=prep";
+    return EF_HIP_OK;
+  }
+  if (e->B < 2) {
+    e->staged_why = "one sequence";
+    return EF_HIP_OK;
+  }
+  if (c.D > static_cast<size_t>(kStageMaxK)) {
+    e->staged_why = "D above the table preparation's limit";
+    return EF_HIP_OK;
+  }
+  const int B = e->B;
+  size_t need = 0;
+  auto plan = [&](const GemvJob* j, int n, int epi, bool emit) {
+    const size_t b = gemv_mfma_staged_workspace_bytes(j, n, epi, B, emit);
+    need = std::max(need, b);
+    return b > 0;
+  };
+  bool ok = true;
+  for (size_t l = 0; l < c.L && ok; ++l) {
+    const LayerJobs j = layer_jobs(e, l);
+    ok = plan(j.qkv, 3, kEpiStore, false) && plan(&j.o, 1, kEpiResidual, true) &&
+         plan(&j.gu, 1, kEpiSwiglu, true) && plan(&j.dn, 1, kEpiResidual, true);
+  }
+  const GemvJob lm = lm_job(e);
+  ok = ok && plan(&lm, 1, kEpiStore, false);
+  if (!ok) {
+    e->staged_why = "a product has no matrix-core plan (unquantized matrices or shapes)";
+    return EF_HIP_OK;
+  }
+  const size_t Kb = std::max(c.D, c.F);
+  const int bpad = stage_bpad(B);
+  const size_t ta = stage_table_bytes(static_cast<int>(c.D), B), tb = stage_table_bytes(static_cast<int>(Kb), B);
+  EFH_RC(dev_alloc(e, &e->ta4, ta));
+  EFH_RC(dev_alloc(e, &e->ta8, ta));
+  EFH_RC(dev_alloc(e, &e->tb4, tb));
+  EFH_RC(dev_alloc(e, &e->tb8, tb));
+  EFH_RC(dev_alloc(e, &e->ta_s, c.D / 32 * bpad));
+  EFH_RC(dev_alloc(e, &e->tb_s, Kb / 32 * bpad));
+  EFH_RC(dev_alloc(e, &e->ta_ssp, c.D / 32 * bpad));
+  EFH_RC(dev_alloc(e, &e->tb_ssp, static_cast<size_t>(bpad)));
+  for (auto [p, n] : {std::pair<void*, size_t>{e->ta4, ta}, {e->ta8, ta}, {e->tb4, tb}, {e->tb8, tb},
+                      {e->ta_s, c.D / 32 * bpad * 4}, {e->tb_s, Kb / 32 * bpad * 4},
+                      {e->ta_ssp, c.D / 32 * bpad * 8}})
+    EFH_HIP(hipMemsetAsync(p, 0, n, e->stream));
+  if (need > e->gemv_ws_bytes) {
+    void* gw = nullptr;
+    EFH_HIP(hipMalloc(&gw, need));
+    e->allocs.push_back(gw);
+    e->gemv_ws = gw;
+    e->gemv_ws_bytes = need;
+  }
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  e->bpad = bpad;
+  e->staged = true;
+  e->staged_why.clear();
+  return EF_HIP_OK;
+}
+
+// The layers of a several-sequence step over staged tables.
+int enqueue_staged_layers(ef_hip_engine e, unsigned groups) {
+  const ef_hip_model_config& c = e->c;
+  const int B = e->B;
+  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
+  hipStream_t s = e->stream;
+  const MfmaStage sa = table_set(e, true), sb = table_set(e, false);
+  if (groups & kGEmbed) {
+    const ef_hip_layer& w0 = e->layers[0];
+    const AEmit em = table_emit(e, true, {w0.wq, w0.wk, w0.wv}, w0.attn_norm_dev, D);
+    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
+                           e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now, &em));
+  }
+  AttnArgs a = attn_args(e);
+  const bool group_attn = attention_uses_group(a, B);
+  for (size_t l = 0; l < c.L; ++l) {
+    const ef_hip_layer& w = e->layers[l];
+    const LayerJobs j = layer_jobs(e, l);
+    if (groups & kGQkv)
+      EFH_RC(launch_gemv_mfma_staged(j.qkv, 3, kEpiStore, sa, B, D, e->gemv_ws, e->gemv_ws_bytes, s));
+    a.kcache = e->kc + l * B * S * kvd;
+    a.vcache = e->vc + l * B * S * kvd;
+    a.em = group_attn ? table_emit(e, false, {w.wo}, nullptr, D) : AEmit{};
+    if (groups & kGAttn) {
+      EFH_RC(launch_attention(a, B, s));
+      if (!group_attn) {
+        MfmaStage pb = sb;
+        pb.ssp = e->tb_ssp;  // written by the preparation, unused by the product
+        EFH_RC(launch_stage_tables(e->ctx, D, static_cast<int>(D), B, nullptr, pb, s));
+      }
+    }
+    if (groups & kGOproj) {
+      const AEmit em = table_emit(e, true, {w.w_gate, w.w_up}, w.ffn_norm_dev, D);
+      EFH_RC(launch_gemv_mfma_staged(&j.o, 1, kEpiResidual, sb, B, D, e->gemv_ws, e->gemv_ws_bytes, s, &em));
+    }
+    if (groups & kGGateUp) {
+      const AEmit em = table_emit(e, false, {w.w_down}, nullptr, F);
+      EFH_RC(launch_gemv_mfma_staged(&j.gu, 1, kEpiSwiglu, sa, B, F, e->gemv_ws, e->gemv_ws_bytes, s, &em));
+    }
+    if (groups & kGDown) {
+      const bool last = l + 1 == c.L;
+      const ef_hip_layer& nx = e->layers[last ? l : l + 1];
+      const AEmit em = last ? table_emit(e, true, {e->lm_head}, e->final_norm, D)
+                            : table_emit(e, true, {nx.wq, nx.wk, nx.wv}, nx.attn_norm_dev, D);
+      EFH_RC(launch_gemv_mfma_staged(&j.dn, 1, kEpiResidual, sb, B, D, e->gemv_ws, e->gemv_ws_bytes, s, &em));
+    }
+  }
+  return EF_HIP_OK;
+}
+
+int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
+  const ef_hip_model_config& c = e->c;
+  const int B = e->B;
+  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
+  hipStream_t s = e->stream;
+  if (e->step_on && groups == kAllGroups) {  // the embedding and every layer in one launch
+    EFH_RC(launch_step(step_args(e), s));
+    return enqueue_tail(e, mode, groups);
+  }
+  if (e->staged) {
+    EFH_RC(enqueue_staged_layers(e, groups));
+    return enqueue_tail(e, mode, groups, true);
+  }
+  if (groups & kGEmbed)
+    EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
+                           e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now));
+  AttnArgs a = attn_args(e);
   for (size_t l = 0; l < c.L; ++l) {
     const ef_hip_layer& w = e->layers[l];
     const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, D, D},
@@ -336,15 +525,20 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
 }
 
 // After the layers: final RMSNorm + lm_head, then the token pick and the step bookkeeping, or
-// only the position advance (a prompt position whose logits are not needed).
-int enqueue_tail(ef_hip_engine e, int mode, unsigned groups) {
+// only the position advance (a prompt position whose logits are not needed).  staged_in: the last
+// down projection staged lm_head's input tables (the staged step; not after a prefill).
+int enqueue_tail(ef_hip_engine e, int mode, unsigned groups, bool staged_in) {
   const ef_hip_model_config& c = e->c;
   const int B = e->B;
   const size_t D = c.D, V = c.V, S = e->max_seq;
   hipStream_t s = e->stream;
   if ((mode & kLogits) && (groups & kGLmHead)) {
     const GemvJob lm{e->lm_head, nullptr, e->x, e->logits, D, V};
-    EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s, e->gemv_ws, e->gemv_ws_bytes));
+    if (staged_in) {
+      EFH_RC(launch_gemv_mfma_staged(&lm, 1, kEpiStore, table_set(e, true), B, V, e->gemv_ws, e->gemv_ws_bytes, s));
+    } else {
+      EFH_RC(launch_gemv(&lm, 1, kEpiStore, e->final_norm, c.eps, B, D, V, s, e->gemv_ws, e->gemv_ws_bytes));
+    }
   }
   if (!(groups & kGPick)) return EF_HIP_OK;
   if (mode & (kGreedy | kSample)) {
@@ -728,6 +922,7 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
   if (he != hipSuccess) return cleanup_fail(fail_hip(he, "engine init"));
   if ((rc = build_step(e)) != EF_HIP_OK) return cleanup_fail(rc);
+  if ((rc = build_staged(e)) != EF_HIP_OK) return cleanup_fail(rc);
   e->magic = kEngineMagic;
   *out = e;
   return EF_HIP_OK;
@@ -967,6 +1162,14 @@ int ef_hip_engine_persistent(ef_hip_engine e, int* on, const char** why) {
   EFH_CHECK(on != nullptr, "engine_persistent: null output");
   *on = e->step_on ? 1 : 0;
   if (why != nullptr) *why = e->step_why.c_str();
+  return EF_HIP_OK;
+}
+
+int ef_hip_engine_tables(ef_hip_engine e, int* on, const char** why) {
+  EFH_RC(check_engine(e));
+  EFH_CHECK(on != nullptr, "engine_tables: null output");
+  *on = e->staged ? 1 : 0;
+  if (why != nullptr) *why = e->staged_why.c_str();
   return EF_HIP_OK;
 }
 

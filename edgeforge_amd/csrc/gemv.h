@@ -1,6 +1,7 @@
 // Launchers of the packed GEMV kernels (gemv.hip), shared by the C-ABI and the decode engine.
 #pragma once
 
+#include "afrag.h"
 #include "common.h"
 
 namespace efh {
@@ -60,15 +61,19 @@ struct MfmaStage {
   int n_ssp = 0;
   float eps = 0.0f;
 };
+constexpr int kStageMaxK = 8192;  // longest K launch_stage_tables prepares
 size_t stage_table_bytes(int K, int batch);
 int stage_bpad(int batch);
 // The tables from x [batch][ldx] (one partial sum per sequence; norm_w may be null).
 int launch_stage_tables(const float* x, size_t ldx, int K, int batch, const float* norm_w, const MfmaStage& st,
                         hipStream_t stream);
 // The batched product over staged tables (one launch of <= 1024 sequences; ws as for launch_gemv,
-// gemv_mfma_workspace_bytes of the same jobs).
+// gemv_mfma_workspace_bytes of the same jobs).  With em on (one job whose rows are the next
+// product's K), its outputs are also staged as that product's tables (afrag.h).
+// Workspace of launch_gemv_mfma_staged (0: no matrix-core plan; emit: the launch stages its outputs).
+size_t gemv_mfma_staged_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, bool emit);
 int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const MfmaStage& st, int batch, size_t ldy,
-                            void* ws, size_t ws_bytes, hipStream_t stream);
+                            void* ws, size_t ws_bytes, hipStream_t stream, const AEmit* em = nullptr);
 
 // F32 / F16 / BF16 weights (gemv_dense.hip): same jobs, epilogues and fused RMSNorm, any cols up to
 // kMaxDenseCols; all jobs of one launch share the type.  launch_gemv routes these types here.

@@ -44,6 +44,7 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "afrag.h"
 #include "gemv.h"
 
 namespace efh {
@@ -92,6 +93,7 @@ struct MArgs {
   int n_ssp;
   float eps;
   float* post_out;
+  AEmit em;  // the outputs also staged as the next product's tables (store / residual / SwiGLU)
 };
 
 struct PrepArgs {
@@ -755,6 +757,8 @@ __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb
   __syncthreads();
   const int S = a.ksplit, j = lane & 15, g = lane >> 4;
   const size_t gsz = static_cast<size_t>(a.B) * ROWS * NM;
+  // staged outputs [sequence of the workgroup][row of the workgroup], after the partial sums
+  float* stage = reinterpret_cast<float*>(lb + static_cast<size_t>(kWavesM) * F * NM * kWave * 16);
   float* mine = a.part + (static_cast<size_t>(grp) * S + ks) * gsz;
   for (int f = wave; f < F; f += kWavesM) {
     const int rt = f / NS, t = f % NS;
@@ -780,14 +784,29 @@ __device__ __forceinline__ void combine_and_store(const MArgs& a, const MJob& jb
       if (row >= jb.rows) continue;
       const float post = post_p[sq - post_base];
       float* y = jb.y + sq * jb.ldy + row;
+      float out;
       if (EPI == kEpiResidual) {
-        *y = *y + v[0][r] * post;
+        out = *y + v[0][r] * post;
       } else if (EPI == kEpiSwiglu) {
-        *y = silu_m(v[0][r] * post) * (v[NM - 1][r] * post);
+        out = silu_m(v[0][r] * post) * (v[NM - 1][r] * post);
       } else {
-        *y = v[0][r] * post;
+        out = v[0][r] * post;
       }
+      *y = out;
+      if (a.em.on()) stage[(t * kSeqTile + 4 * g + r) * ROWS + rl] = out;
     }
+  }
+  if (S > 1 || !a.em.on()) return;
+  // the outputs as the next product's tables: one (sequence, 32-row block) per half-wave
+  __syncthreads();
+  constexpr int kBlocksWg = ROWS / 32, kUnits = NS * kSeqTile * kBlocksWg;
+  for (int u0 = 0; u0 < kUnits; u0 += kT / 32) {
+    const int u = u0 + static_cast<int>(threadIdx.x) / 32, kk = threadIdx.x & 31;
+    const bool ok = u < kUnits;
+    const int sl = ok ? u / kBlocksWg : 0, blk = ok ? u % kBlocksWg : 0;
+    const int sq = s0 + sl, rowg = row0 + blk * 32;
+    const bool live = ok && sq < a.B && rowg < jb.rows;
+    emit_block(a.em, sq, rowg >> 5, kk, live ? stage[sl * ROWS + blk * 32 + kk] : 0.0f, live);
   }
 }
 
@@ -825,16 +844,33 @@ __global__ __launch_bounds__(kT) void gemv_mfma_kernel(MArgs a) {
     // the epilogue factor of each of this workgroup's sequences: 1 / rms from the producer's
     // partial sums (in index order), or 1; the first row group's first split also hands them to
     // finalize_kernel
-    if (threadIdx.x < NS * kSeqTile) {
-      const int sq = s0 + threadIdx.x;
-      float f = 1.0f;
-      if (a.ssp != nullptr && sq < a.B) {
-        double tot = 0.0;
-        for (int p = 0; p < a.n_ssp; ++p) tot += a.ssp[static_cast<size_t>(p) * a.bpad + sq];
-        f = static_cast<float>(1.0 / sqrt(tot / static_cast<double>(a.K) + static_cast<double>(a.eps)));
+    // Eight threads per sequence: thread j adds partials j, j + 8, ... in order (eight loads in
+    // flight), then the eight threads' DPP tree.  The order depends on nothing but the partials, so
+    // every workgroup, launch shape and batch size gets the same factor for the same input.
+    if (threadIdx.x < NS * kSeqTile * 8) {  // whole waves
+      constexpr int G = 8;
+      const int sl = threadIdx.x / G, j = threadIdx.x % G, sq = s0 + sl;
+      const bool has = a.ssp != nullptr && sq < a.B;
+      double tot = 0.0;
+      if (has) {
+        for (int p0 = 0; p0 < a.n_ssp; p0 += 8 * G) {
+          double v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int p = p0 + j + i * G;
+            v[i] = p < a.n_ssp ? a.ssp[static_cast<size_t>(p) * a.bpad + sq] : 0.0;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) tot += v[i];
+        }
       }
-      s_post[threadIdx.x] = f;
-      if (a.post_out != nullptr && blockIdx.x == 0 && sq < a.B) a.post_out[sq] = f;
+      tot = group_sum_dpp<G>(tot);
+      if (j == G - 1) {
+        const float f =
+            has ? static_cast<float>(1.0 / sqrt(tot / static_cast<double>(a.K) + static_cast<double>(a.eps))) : 1.0f;
+        s_post[sl] = f;
+        if (a.post_out != nullptr && blockIdx.x == 0 && sq < a.B) a.post_out[sq] = f;
+      }
     }
     const __amdgpu_buffer_rsrc_t bsr =
         make_rsrc(a.bscale, static_cast<uint32_t>(nb) * static_cast<uint32_t>(a.bpad) * 4u);
@@ -861,38 +897,46 @@ struct FinArgs {
   int n_jobs, B, rows_wg, S, total;  // total = groups * rows_wg * B outputs
   const float* part;
   const float* post;
+  AEmit em;
 };
 
 // One output (sequence, row) per thread: the splits' sums in index order, the scale, the epilogue.
+// With em on, the 32 consecutive threads of a (sequence, 32-row block) also stage their outputs as
+// the next product's tables (rows per group are a multiple of 32 then).
 template <int EPI>
 __global__ __launch_bounds__(256) void finalize_kernel(FinArgs a) {
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.total) return;
+  const bool in = idx < a.total;
   const int per_group = a.rows_wg * a.B;
-  const int tile = idx / per_group, o = idx % per_group;
+  const int tile = in ? idx / per_group : 0, o = in ? idx % per_group : 0;
   MJob jb = a.job[0];
   for (int i = 1; i < a.n_jobs; ++i)
     if (tile >= a.job[i].tile_begin) jb = a.job[i];
   const int sq = o / a.rows_wg, row = (tile - jb.tile_begin) * a.rows_wg + o % a.rows_wg;
-  if (row >= jb.rows) return;
-  const size_t gsz = static_cast<size_t>(per_group) * NM;
-  const float* p = a.part + static_cast<size_t>(tile) * a.S * gsz + static_cast<size_t>(o) * NM;
-  float v[NM];
+  const bool live = in && row < jb.rows;
+  float out = 0.0f;
+  if (live) {
+    const size_t gsz = static_cast<size_t>(per_group) * NM;
+    const float* p = a.part + static_cast<size_t>(tile) * a.S * gsz + static_cast<size_t>(o) * NM;
+    float v[NM];
 #pragma unroll
-  for (int mt = 0; mt < NM; ++mt) {
-    float sum = p[mt];
-    for (int k = 1; k < a.S; ++k) sum += p[k * gsz + mt];
-    v[mt] = sum * a.post[sq];
+    for (int mt = 0; mt < NM; ++mt) {
+      float sum = p[mt];
+      for (int k = 1; k < a.S; ++k) sum += p[k * gsz + mt];
+      v[mt] = sum * a.post[sq];
+    }
+    float* y = jb.y + sq * jb.ldy + row;
+    if (EPI == kEpiResidual) {
+      out = *y + v[0];
+    } else if (EPI == kEpiSwiglu) {
+      out = silu_m(v[0]) * v[NM - 1];
+    } else {
+      out = v[0];
+    }
+    *y = out;
   }
-  float* y = jb.y + sq * jb.ldy + row;
-  if (EPI == kEpiResidual) {
-    *y = *y + v[0];
-  } else if (EPI == kEpiSwiglu) {
-    *y = silu_m(v[0]) * v[NM - 1];
-  } else {
-    *y = v[0];
-  }
+  if (a.em.on()) emit_block(a.em, sq, row >> 5, row & 31, out, live);
 }
 
 // (RT, NS) shapes the kernels are instantiated for: the ones whose registers fit in 256 VGPRs
@@ -982,7 +1026,8 @@ double shape_cost(int rt, int nm, int ns, int sg, int groups, int S, int bps, si
   return t;
 }
 
-Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) {
+// even_rt: only shapes whose workgroup rows are a multiple of 32 (outputs staged as tables).
+Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, bool even_rt = false) {
   Plan p;
   if (mfma_gemv_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return p;
   const size_t K = jobs[0].W->cols;
@@ -1014,11 +1059,13 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx) 
   for (int si = 0; si < n_shapes; ++si) {
     const int rt = shapes[si].RT, ns = shapes[si].NS;
     if ((ov.RT > 0 && rt != ov.RT) || (ov.NS > 0 && ns != ov.NS) || (ns > 1 && p.NT < ns)) continue;
+    if (even_rt && rt % 2 != 0) continue;
     const int sg = (p.NT + ns - 1) / ns;
     const int rows_wg = rt * kTileRows;
     const int groups = groups_for(jobs, n_jobs, rows_wg);
     // the workgroup's partial sums of every wave in LDS for the reduction
-    const size_t lds = static_cast<size_t>(kWavesM) * rt * p.nm * ns * kWave * 4 * sizeof(float);
+    size_t lds = static_cast<size_t>(kWavesM) * rt * p.nm * ns * kWave * 4 * sizeof(float);
+    if (even_rt) lds += static_cast<size_t>(rt) * kTileRows * ns * kSeqTile * sizeof(float);  // staged outputs
     if (lds > lim) continue;
     for (int s_try = 1; s_try <= std::min(32, std::max(1, nb / 8)); ++s_try) {
       const int bps = (nb + s_try - 1) / s_try;
@@ -1166,7 +1213,8 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
         cj[j].y = jobs[j].y + b0 * yld;
         cj[j].ldy = yld;
       }
-      if (rc == EF_HIP_OK) rc = launch_gemv_mfma_staged(cj, n_jobs, epi, st, nb, ldy, buf + off, pl.bytes, stream);
+      if (rc == EF_HIP_OK)
+        rc = launch_gemv_mfma_staged(cj, n_jobs, epi, st, nb, ldy, buf + off, pl.bytes, stream, nullptr);
       const hipError_t e = hipFreeAsync(buf, stream);
       if (e != hipSuccess && rc == EF_HIP_OK) rc = fail_hip(e, "hipFreeAsync");
     }
@@ -1276,6 +1324,13 @@ int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm
 }
 
 
+size_t gemv_mfma_staged_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int batch, bool emit) {
+  const Plan p = plan_mfma(jobs, n_jobs, epi, batch, jobs[0].W->cols, emit);
+  return p.ok ? p.bytes : 0;
+}
+
+static_assert(kStageMaxK == kSeqPrepMaxK, "launch_stage_tables limit");
+
 size_t stage_table_bytes(int K, int batch) {
   const size_t tiles = (static_cast<size_t>(batch) + kSeqTile - 1) / kSeqTile;
   return tiles * static_cast<size_t>(K / 32) * 2 * kWave * 16;
@@ -1284,7 +1339,7 @@ int stage_bpad(int batch) { return ((batch + kSeqTile - 1) / kSeqTile) * kSeqTil
 
 int launch_stage_tables(const float* x, size_t ldx, int K, int batch, const float* norm_w, const MfmaStage& st,
                         hipStream_t stream) {
-  EFH_CHECK(K % 32 == 0 && K <= kSeqPrepMaxK && batch >= 1 && batch <= kMaxTiles * kSeqTile,
+  EFH_CHECK(K % 32 == 0 && K <= kStageMaxK && batch >= 1 && batch <= kMaxTiles * kSeqTile,
             "stage_tables: K must be a multiple of 32 up to 8192, batch in [1, 1024]");
   EFH_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0, "stage_tables: x rows must be 16-byte aligned");
   EFH_CHECK(st.bpad >= stage_bpad(batch) && st.bscale && st.ssp && (st.t4 || st.t8), "stage_tables: outputs");
@@ -1303,9 +1358,15 @@ int launch_stage_tables(const float* x, size_t ldx, int K, int batch, const floa
 }
 
 int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const MfmaStage& st, int batch, size_t ldy,
-                            void* ws, size_t ws_bytes, hipStream_t stream) {
+                            void* ws, size_t ws_bytes, hipStream_t stream, const AEmit* em) {
   const size_t K = jobs[0].W->cols;
-  const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, K);
+  const bool emit = em != nullptr && em->on();
+  const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, K, emit);
+  if (emit) {
+    EFH_CHECK(n_jobs == 1 && jobs[0].W->rows % 32 == 0 && static_cast<int>(jobs[0].W->rows / 32) == em->nb &&
+                  em->bpad >= stage_bpad(batch),
+              "gemv_mfma_staged: staging the outputs needs one job whose rows are the next product's K");
+  }
   EFH_CHECK(pl.ok, "gemv_mfma_staged: no matrix-core plan for this launch");
   EFH_CHECK(batch <= pl.chunk, "gemv_mfma_staged: more sequences than one launch covers");
   EFH_CHECK((!pl.q4 || st.t4) && (!pl.q8 || st.t8), "gemv_mfma_staged: a table of the launch's column order is missing");
@@ -1335,6 +1396,7 @@ int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const Mfma
   a.n_ssp = st.n_ssp;
   a.eps = st.eps;
   a.post_out = pl.S > 1 ? post : nullptr;
+  if (emit) a.em = *em;
   const int rows_wg = pl.RT * kTileRows;
   int tiles = 0;
   for (int j = 0; j < n_jobs; ++j) {
@@ -1366,6 +1428,7 @@ int launch_gemv_mfma_staged(const GemvJob* jobs, int n_jobs, int epi, const Mfma
     f.total = tiles * rows_wg * batch;
     f.part = a.part;
     f.post = post;
+    if (emit) f.em = *em;
     void* fin = epi == kEpiStore ? reinterpret_cast<void*>(&finalize_kernel<kEpiStore>)
                                  : (epi == kEpiResidual ? reinterpret_cast<void*>(&finalize_kernel<kEpiResidual>)
                                                         : reinterpret_cast<void*>(&finalize_kernel<kEpiSwiglu>));

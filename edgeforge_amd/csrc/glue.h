@@ -1,6 +1,7 @@
 // Launchers of the decode-step glue kernels (glue.hip).
 #pragma once
 
+#include "afrag.h"
 #include "common.h"
 
 namespace efh {
@@ -21,6 +22,7 @@ struct AttnArgs {
   float scale;          // float(1 / sqrt(hd))
   int pre_vrows;        // set by launch_attention: the first chunk's V rows have their own LDS
   int chunk;            // set by launch_attention: rows of the LDS staging buffer (>= 64)
+  AEmit em;             // KV-group kernel: ctx also staged as the o-projection's tables (afrag.h)
 };
 
 // Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of
@@ -37,9 +39,11 @@ int launch_advance_by(int32_t* pos_dev, int n, hipStream_t s);
 // With rope_now, also copies the cos / sin table rows at *pos_dev there (half floats each).
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
                     float* out, long ldo, hipStream_t s, const float* cos_t = nullptr, const float* sin_t = nullptr,
-                    int half = 0, float* rope_now = nullptr);
+                    int half = 0, float* rope_now = nullptr, const AEmit* em = nullptr);
 size_t attention_lds_bytes(int hd, int max_seq);
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s);
+// Whether launch_attention runs the KV-group kernel (the one that can stage ctx as tables).
+bool attention_uses_group(const AttnArgs& a, int batch);
 int launch_rmsnorm(const float* x, const float* w, float eps, int n, long ld, int batch, float* out, hipStream_t s);
 // With out_eos: eos_p[b] is stored beside the picked token (the chat loop's per-step P(EOS)).
 int launch_finish_step(const int32_t* next, int batch, int32_t* hist, long hist_ld, int32_t* hist_len, int32_t* out,

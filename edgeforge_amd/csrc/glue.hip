@@ -14,6 +14,7 @@
 #include <utility>
 
 #include "glue.h"
+#include "afrag.h"
 #include "qdot.h"
 
 #pragma clang fp contract(off)
@@ -26,10 +27,12 @@ constexpr int kAttnThreads = 256;
 // x[b] = row hist[b][pos] of the embedding table (kern::row_f32 / embedding_bf16).  With rope_now,
 // workgroup (0, 0) also copies RoPE's cos and sin rows at pos into rope_now[0, half) and
 // [half, 2 half), so the step's attention launches read them without first reading the position.
+// With em on, each row is also staged as the first product's tables (afrag.h): 32 consecutive
+// threads hold one block of one sequence.
 __global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long rows, long cols, long rb,
                                 const int32_t* __restrict__ hist, long hist_ld, const int32_t* __restrict__ pos_dev,
                                 float* __restrict__ out, long ldo, const float* __restrict__ cos_t,
-                                const float* __restrict__ sin_t, int half, float* __restrict__ rope_now) {
+                                const float* __restrict__ sin_t, int half, float* __restrict__ rope_now, AEmit em) {
   const int b = blockIdx.y;
   if (rope_now != nullptr && blockIdx.x == 0 && b == 0) {
     const long base = static_cast<long>(*pos_dev) * half;
@@ -41,9 +44,13 @@ __global__ void embed_at_kernel(const uint8_t* __restrict__ W, int qtype, long r
   const int32_t id = hist[b * hist_ld + *pos_dev];
   const bool ok = id >= 0 && id < rows;
   const uint8_t* row = W + (ok ? id : 0) * rb;
-  for (long c = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols;
-       c += static_cast<long>(gridDim.x) * blockDim.x) {
-    out[b * ldo + c] = ok ? decode_elem(row, qtype, c) : __int_as_float(0x7FC00000);
+  const long step = static_cast<long>(gridDim.x) * blockDim.x;
+  for (long c0 = static_cast<long>(blockIdx.x) * blockDim.x; c0 < cols; c0 += step) {  // uniform trip count
+    const long c = c0 + threadIdx.x;
+    const bool in = c < cols;
+    const float v = in ? (ok ? decode_elem(row, qtype, c) : __int_as_float(0x7FC00000)) : 0.0f;
+    if (in) out[b * ldo + c] = v;
+    if (em.on()) emit_block(em, b, static_cast<int>(c >> 5), static_cast<int>(c & 31), v, in);
   }
 }
 
@@ -618,6 +625,11 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
   for (int u = 0; u < kGroupMaxOut; ++u) {
     const int idx = t + u * kGroupThreads;
     if (idx < hpg * hd) out[idx] = o[u];
+    // staged as the o-projection's tables: 32 consecutive threads hold one block of this sequence
+    if (a.em.on()) {
+      const int e = g * hpg * hd + idx;
+      emit_block(a.em, b, e >> 5, e & 31, o[u], idx < hpg * hd);
+    }
   }
 }
 
@@ -735,11 +747,14 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* __restri
 
 int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld, const int32_t* pos_dev, int batch,
                     float* out, long ldo, hipStream_t s, const float* cos_t, const float* sin_t, int half,
-                    float* rope_now) {
+                    float* rope_now, const AEmit* em) {
+  EFH_CHECK(em == nullptr || !em->on() || (W->cols % 32 == 0 && static_cast<int>(W->cols / 32) == em->nb),
+            "embed_at: staging needs cols % 32 == 0 and the product's K");
   const unsigned gx = static_cast<unsigned>(std::min<size_t>((W->cols + 255) / 256, 16));
+  const AEmit e = em != nullptr ? *em : AEmit{};
   hipLaunchKernelGGL(embed_at_kernel, dim3(gx, batch), dim3(256), 0, s, W->dev, W->qtype, static_cast<long>(W->rows),
                      static_cast<long>(W->cols), static_cast<long>(W->row_bytes), hist, hist_ld, pos_dev, out, ldo,
-                     cos_t, sin_t, half, rope_now);
+                     cos_t, sin_t, half, rope_now, e);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }
@@ -790,20 +805,31 @@ int attention_choice() {
   return 0;
 }
 
+// Many sequences: one workgroup per (KV group, sequence) when that fills the chip (or is forced)
+// and the group's scores fit in LDS.
+bool attention_uses_group(const AttnArgs& a, int batch) {
+  const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
+  const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
+  const int hpg = a.H / a.KV, choice = attention_choice();
+  const size_t glds = attention_group_lds_bytes(hpg, a.hd, a.max_seq);
+  const bool group_ok = hpg >= 2 && a.hd % 8 == 0 && a.hd * kAttnChunk <= 4 * kGroupPreSlots * kGroupThreads &&
+                        hpg * a.hd <= kGroupMaxOut * kGroupThreads && glds <= lim;
+  return group_ok && (choice == 2 || (choice == 0 && static_cast<long>(a.KV) * batch >= cus / 2));
+}
+
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
   const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
-  // Many sequences: one workgroup per (KV group, sequence) when that fills the chip (or is forced)
-  // and the group's scores fit in LDS.
-  const int hpg = a.H / a.KV, choice = attention_choice();
-  const size_t glds = attention_group_lds_bytes(hpg, a.hd, a.max_seq);
-  const bool group_ok = hpg >= 2 && a.hd % 8 == 0 && a.hd * kAttnChunk <= 4 * kGroupPreSlots * kGroupThreads && hpg * a.hd <= kGroupMaxOut * kGroupThreads &&
-                        glds <= lim;
-  if (group_ok && (choice == 2 || (choice == 0 && static_cast<long>(a.KV) * batch >= cus / 2))) {
+  const int choice = attention_choice();
+  if (attention_uses_group(a, batch)) {
+    const int hpg = a.H / a.KV;
+    EFH_CHECK(!a.em.on() || (hpg * a.hd) % 32 == 0, "attention: staging needs H / KV * hd % 32 == 0");
+    const size_t glds = attention_group_lds_bytes(hpg, a.hd, a.max_seq);
     hipLaunchKernelGGL(attention_group_kernel, dim3(a.KV, batch), dim3(kGroupThreads), glds, s, a);
     EFH_HIP(hipGetLastError());
     return EF_HIP_OK;
   }
+  EFH_CHECK(!a.em.on(), "attention: only the KV-group kernel stages its output as tables");
   // hd = 64 with the step's RoPE row: one wave per (head, sequence), unless another kernel is forced
   if (a.hd == kWaveHd && a.rope_now != nullptr && a.H % a.KV == 0 && choice != 1 && choice != 2) {
     const size_t wlds = (2 * static_cast<size_t>(kWaveHd) + static_cast<size_t>(a.max_seq)) * sizeof(float);

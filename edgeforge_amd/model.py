@@ -202,6 +202,13 @@ class Engine:
         EL.call("ef_hip_engine_persistent", self.h, C.byref(on), C.byref(why))
         return bool(on.value), (why.value or b"").decode()
 
+    def staged_tables(self) -> tuple[bool, str]:
+        """Whether several-sequence steps run over producer-staged product inputs, and why not
+        (ef_hip_engine_tables)."""
+        on, why = C.c_int(0), C.c_char_p()
+        EL.call("ef_hip_engine_tables", self.h, C.byref(on), C.byref(why))
+        return bool(on.value), (why.value or b"").decode()
+
     def profile(self, reps: int = 20, sampler: dict | None = None, rng: H.RngStates | None = None) -> dict:
         """Milliseconds per step of each kernel group of a decode step (ef_hip_engine_profile)."""
         out = (C.c_double * len(self.PROFILE_GROUPS))()

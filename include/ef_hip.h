@@ -264,6 +264,16 @@ int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, voi
  * forward / generate / reply call with EF_HIP_ERUNTIME and turns the persistent step off. */
 int ef_hip_engine_persistent(ef_hip_engine e, int* on, const char** why);
 
+/* A several-sequence engine runs its decode step over producer-staged inputs: the embedding lookup,
+ * the KV-group attention and the o / gate-up / down products write the next product's matrix-core
+ * input tables (block-scaled fp16 hi + lo pairs, with the RMSNorm's per-block partial sums) as they
+ * store their outputs, so no product runs a preparation launch.  *on = 1 when this engine does;
+ * *why (owned by the engine) says why not otherwise: one sequence, an unquantized matrix, no
+ * matrix-core plan for a product, or EF_HIP_DECODE_TABLES=prep at engine creation (the
+ * per-product preparation, kept for comparison).  No counterpart in the reference (a CPU build has
+ * no kernel boundaries); it lets a caller see which step path runs. */
+int ef_hip_engine_tables(ef_hip_engine e, int* on, const char** why);
+
 /* ---- quality of a quantized model (eval-quant, src/eval_quant.cpp) ---------------------------------
  * compare_dist (src/eval_quant.cpp:48-96) over n positions of device logits: KL(P_ref || P_ours) in
  * double, top-1 agreement, the reference confident (its top-1 probability >= 0.5), ours finite;

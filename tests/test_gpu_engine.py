@@ -203,10 +203,15 @@ def test_config5_batched_greedy_32_steps_match_oracle(tinyllama, B):
     eng.close()
 
 
-def test_config5_batched_sampled_replays_on_cpu(tinyllama, hip):
+def test_config5_batched_sampled_replays_on_cpu(tinyllama, hip, monkeypatch):
     """Config 5 at B=64 with config 3's sampler (T 0.8, top-k 40, top-p 0.95, penalty 1.1 over the
     context), one seed per sequence: every id of every sequence equals the CPU Sampler's pick
-    (src/sampler.cpp:13-70, one Sampler per sequence) on the device's own logits of that step."""
+    (src/sampler.cpp:13-70, one Sampler per sequence) on the device's own logits of that step.
+    The prompt goes through the decode step too (EF_HIP_PREFILL=serial), so the teacher-forced
+    replay recomputes exactly the logits the generation sampled from: the batched prefill agrees
+    with the decode step to the products' rounding only, and a sampled id whose uniform draw falls
+    that close to a boundary of the cumulative distribution would move."""
+    monkeypatch.setenv("EF_HIP_PREFILL", "serial")
     dm, _ = tinyllama
     B, n = 64, 32
     cfg = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
@@ -448,4 +453,60 @@ def test_persistent_step_off_where_it_does_not_apply(hip, monkeypatch):
     eng = Engine(dm, max_seq=16, batch=2)
     on, why = eng.persistent()
     assert not on and "batch" in why
+    eng.close()
+
+
+# ---- several-sequence steps over producer-staged product inputs ----
+
+@pytest.mark.parametrize("cfg,B,q8,attn", [
+    (SMALL, 3, {(0, "wk"), (1, "wv"), (2, "w_down")}, None),  # per-head attention: o's input prepared
+    (ODD, 5, {(1, "wq")}, "group"),  # KV-group attention stages o's input; K = 96, three heads per group
+    (TWO_LAYER, 64, frozenset(), None),  # TinyLlama's layer shapes at B=64 (KV-group attention, K split)
+    (TWO_LAYER, 16, frozenset({(0, "wk"), (0, "wv"), (1, "w_down")}), None),
+])
+def test_staged_tables_match_per_product_preparation(hip, cfg, B, q8, attn, monkeypatch):
+    """A several-sequence engine stages every product's input in the producing kernel (embedding,
+    attention, o / gate-up / down epilogues); its logits at every position equal those of the
+    per-product preparation (EF_HIP_DECODE_TABLES=prep) to float rounding, and the first and last
+    sequences match the oracle's Transformer."""
+    print(f"[case] staged tables vs preparation D={cfg.D} L={cfg.L} B={B} q8={sorted(q8)} attn={attn}", flush=True)
+    if attn is not None:
+        monkeypatch.setenv("EF_HIP_ATTENTION", attn)
+    dm = DeviceModel.synthetic(cfg, seed=51, q8=q8)
+    n = 10
+    ids = D.rng(52).integers(0, cfg.V, size=(B, n)).astype(np.int32)
+    logits = {}
+    for kind in ("staged", "prep"):
+        if kind == "prep":
+            monkeypatch.setenv("EF_HIP_DECODE_TABLES", "prep")
+        else:
+            monkeypatch.delenv("EF_HIP_DECODE_TABLES", raising=False)
+        eng = Engine(dm, max_seq=n, batch=B)
+        on, why = eng.staged_tables()
+        assert on == (kind == "staged"), why
+        logits[kind] = _teacher_forced_logits(eng, [ids[:, p] for p in range(n)], 0)
+        eng.close()
+    worst = max(_logit_err(logits["staged"][p][b], logits["prep"][p][b]) for p in range(n) for b in range(B))
+    print(f"staged vs prep: worst relative logit difference {worst:.2e}", flush=True)
+    assert worst < 1e-5
+    om = OracleModel(dm)
+    for b in (0, B - 1):
+        ot = om.transformer(n)
+        for p in range(n):
+            assert _logit_err(logits["staged"][p][b], ot.forward(int(ids[b, p]), p)) < 1e-4, (b, p)
+        ot.close()
+
+
+def test_staged_tables_off_where_they_do_not_apply(hip, monkeypatch):
+    """One sequence, or EF_HIP_DECODE_TABLES=prep at creation: the engine says why it prepares each
+    product's input itself."""
+    dm = DeviceModel.synthetic(SMALL, seed=3)
+    eng = Engine(dm, max_seq=16)
+    on, why = eng.staged_tables()
+    assert not on and "one sequence" in why
+    eng.close()
+    monkeypatch.setenv("EF_HIP_DECODE_TABLES", "prep")
+    eng = Engine(dm, max_seq=16, batch=4)
+    on, why = eng.staged_tables()
+    assert not on and "EF_HIP_DECODE_TABLES" in why
     eng.close()
