@@ -714,11 +714,15 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
   WRegs<Q4> W[kMaxBlocksPerWave][RT][NM];
   h8 A[2][NS][2];
   f4v Sc[2][NS];
+  // Loads are issued in the order their blocks need them and kept there by scheduling barriers:
+  // loads complete in order, so a block's wait then never covers a later block's prefetch.
   const int kb = kb0 + wave;
   load_wb(W[0], kb);
-  load_wb(W[1], kb + kWavesM);
   load_a(A[0], kb);
   load_s(Sc[0], kb);
+  __builtin_amdgcn_sched_barrier(0);
+  load_wb(W[1], kb + kWavesM);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < kMaxBlocksPerWave; ++i) {
     const int b = kb + i * kWavesM;
@@ -727,7 +731,9 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
       load_a(A[(i + 1) & 1], b + kWavesM);
       load_s(Sc[(i + 1) & 1], b + kWavesM);
     }
+    __builtin_amdgcn_sched_barrier(0);
     if (i + 2 < kMaxBlocksPerWave) load_wb(W[i + 2], b + 2 * kWavesM);
+    __builtin_amdgcn_sched_barrier(0);
     block_products<RT, NM, NS, Q4, BS>(W[i], A[i & 1], acc, Sc[i & 1]);
   }
 }
@@ -945,7 +951,7 @@ struct Shape {
   int RT, NS;
 };
 constexpr Shape kShapesStore[] = {{2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {4, 4}, {8, 1}, {8, 2}};
-constexpr Shape kShapesSwiglu[] = {{2, 1}, {2, 2}, {2, 4}, {3, 1}, {3, 2}, {4, 1}, {4, 2}};
+constexpr Shape kShapesSwiglu[] = {{2, 1}, {2, 2}, {2, 4}, {3, 1}, {3, 2}, {4, 1}, {4, 2}, {6, 1}};
 
 template <int EPI, int RT, int NS, bool BS>
 void* kfn() {
@@ -956,6 +962,7 @@ void* kfn() {
 template <int EPI, bool BS = false>
 void* pick_mfma(int rt, int ns) {
   if constexpr (EPI == kEpiSwiglu) {
+    if (rt == 6) return kfn<EPI, 6, 1, BS>();
     if (rt == 4) return ns == 2 ? kfn<EPI, 4, 2, BS>() : kfn<EPI, 4, 1, BS>();
     if (rt == 3) return ns == 2 ? kfn<EPI, 3, 2, BS>() : kfn<EPI, 3, 1, BS>();
     return ns == 4 ? kfn<EPI, 2, 4, BS>() : (ns == 2 ? kfn<EPI, 2, 2, BS>() : kfn<EPI, 2, 1, BS>());
