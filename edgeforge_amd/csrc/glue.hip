@@ -510,8 +510,9 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
     }
   });
   const int pos = *a.pos_dev, n_pos = pos + 1;
-  const float* cr = a.cos_t + static_cast<long>(pos) * half;
-  const float* sr = a.sin_t + static_cast<long>(pos) * half;
+  // RoPE's rows at pos: the step's copy (no load waiting on the position) or the tables
+  const float* cr = a.rope_now != nullptr ? a.rope_now : a.cos_t + static_cast<long>(pos) * half;
+  const float* sr = a.rope_now != nullptr ? a.rope_now + half : a.sin_t + static_cast<long>(pos) * half;
   for (int idx = t; idx < hpg * half; idx += kGroupThreads) {
     const int hh = idx / half, j = idx - hh * half;
     const float qa = q[hh * hd + j], qb = q[hh * hd + j + half];
