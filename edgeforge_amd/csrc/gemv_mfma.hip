@@ -59,7 +59,9 @@ constexpr int kSeqTile = 16;                    // sequences per A operand (one 
 constexpr int kMaxTiles = 64;                   // sequence tiles per launch: 1024 sequences (rows)
 constexpr int kMaxJobsM = 4;
 constexpr int kPrepBlocks = kTP / kWave;        // blocks per xfrag workgroup: one per wave
-constexpr int kMaxBlocksPerWave = 8;            // K blocks per wave of one batched GEMV workgroup
+// K blocks per wave of one batched GEMV workgroup: 24 for the smallest shapes (two accumulator
+// tiles: a whole K of up to 6144 without a split), 8 otherwise (more unrolled blocks would spill)
+__host__ __device__ constexpr int max_blocks_per_wave(int rt, int nm, int ns) { return rt * nm * ns <= 2 ? 24 : 8; }
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
@@ -696,7 +698,7 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
         dst[t][h] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(tab, voff_a, so, 0));
       }
   };
-  // Fully unrolled over at most kMaxBlocksPerWave blocks.  Every prefetch is issued
+  // Fully unrolled over at most MB blocks.  Every prefetch is issued
   // unconditionally (a block past this workgroup's range is read and never used), so every path
   // has the same loads in flight and the wait before each block's products covers only that
   // block's loads.
@@ -711,7 +713,8 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
       }
     }
   };
-  WRegs<Q4> W[kMaxBlocksPerWave][RT][NM];
+  constexpr int MB = max_blocks_per_wave(RT, NM, NS);
+  WRegs<Q4> W[MB][RT][NM];
   h8 A[2][NS][2];
   f4v Sc[2][NS];
   // Loads are issued in the order their blocks need them and kept there by scheduling barriers:
@@ -724,15 +727,15 @@ __device__ __forceinline__ void k_loop(const MJob& jb, int tile_row0, int nb, in
   load_wb(W[1], kb + kWavesM);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < kMaxBlocksPerWave; ++i) {
+  for (int i = 0; i < MB; ++i) {
     const int b = kb + i * kWavesM;
     if (b >= kb1) break;
-    if (i + 1 < kMaxBlocksPerWave) {
+    if (i + 1 < MB) {
       load_a(A[(i + 1) & 1], b + kWavesM);
       load_s(Sc[(i + 1) & 1], b + kWavesM);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < kMaxBlocksPerWave) load_wb(W[i + 2], b + 2 * kWavesM);
+    if (i + 2 < MB) load_wb(W[i + 2], b + 2 * kWavesM);
     __builtin_amdgcn_sched_barrier(0);
     block_products<RT, NM, NS, Q4, BS>(W[i], A[i & 1], acc, Sc[i & 1]);
   }
@@ -1019,7 +1022,7 @@ const MfmaOverride& mfma_override() {
 // 2 KB of A operands per sequence tile and the tile-block's weights through the CU's L2 port at
 // ~40 B/cycle.
 double shape_cost(int rt, int nm, int ns, int sg, int groups, int S, int bps, size_t wbytes, size_t part_bytes,
-                  int cus) {
+                  int cus, bool emit) {
   const double units = static_cast<double>(rt) * nm * bps;
   const double mfma = units * 2.0 * ns * 16.0 / 4.0;
   const double valu = units * (12.0 + 4.0 * ns) * 4.0 / 4.0;
@@ -1029,7 +1032,9 @@ double shape_cost(int rt, int nm, int ns, int sg, int groups, int S, int bps, si
   const double rounds = std::ceil(static_cast<double>(wgs) / cus);
   const double hbm = static_cast<double>(wbytes) * 2.4e9 / 5.0e12;  // cycles at 2.4 GHz, ~5 TB/s
   double t = std::max(rounds * wg, hbm + 2500.0);
-  if (S > 1) t += 3600.0 + static_cast<double>(part_bytes) / (20.0 * cus);  // launch + partial traffic
+  // launch + partial traffic; a finalize that also stages the next product's tables measured
+  // 4.6 us per launch at B = 64 (emit)
+  if (S > 1) t += (emit ? 11000.0 : 3600.0) + static_cast<double>(part_bytes) / (20.0 * cus);
   return t;
 }
 
@@ -1077,9 +1082,9 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, 
     for (int s_try = 1; s_try <= std::min(32, std::max(1, nb / 8)); ++s_try) {
       const int bps = (nb + s_try - 1) / s_try;
       const int S = (nb + bps - 1) / bps;
-      if (S != s_try || (ov.S > 0 && S != ov.S) || bps > kWavesM * kMaxBlocksPerWave) continue;
+      if (S != s_try || (ov.S > 0 && S != ov.S) || bps > kWavesM * max_blocks_per_wave(rt, p.nm, ns)) continue;
       const size_t part = S > 1 ? static_cast<size_t>(groups) * S * p.chunk * rows_wg * p.nm * sizeof(float) : 0;
-      const double c = shape_cost(rt, p.nm, ns, sg, groups, S, bps, wbytes, 2 * part, cus);
+      const double c = shape_cost(rt, p.nm, ns, sg, groups, S, bps, wbytes, 2 * part, cus, even_rt);
       if (!found || c < p.cost) {
         found = true;
         p.cost = c;
