@@ -580,10 +580,12 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
         take(base + 2 * kWave + lane, s2);
         take(base + 3 * kWave + lane, s3);
       }
+      // partials that took no position are exact zeros (adding them changes nothing): their
+      // reductions are skipped (n_pos is uniform)
       s0 = wave_sum_d_dpp(s0);
-      s1 = wave_sum_d_dpp(s1);
-      s2 = wave_sum_d_dpp(s2);
-      s3 = wave_sum_d_dpp(s3);
+      if (n_pos > kWave) s1 = wave_sum_d_dpp(s1);
+      if (n_pos > 2 * kWave) s2 = wave_sum_d_dpp(s2);
+      if (n_pos > 3 * kWave) s3 = wave_sum_d_dpp(s3);
       double tot = 0.0;
       tot += s0;
       tot += s1;
