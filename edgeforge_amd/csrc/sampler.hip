@@ -353,14 +353,16 @@ __device__ void bitonic_global(uint64_t* g, int n, uint64_t* buf) {
 
 // ---- sequential loops of the sampler ---------------------------------------------------------------
 // The reference's double sums, nucleus cut and CDF walk are left-to-right loops; thread 0 runs them
-// in that order.  A global array is staged into LDS kStage values at a time by the whole
-// workgroup, so thread 0 reads LDS; an array already in LDS is read in place.  step(v, i) consumes
-// element i and returns true to stop; every thread returns thread 0's stop index (n if none).
+// in that order.  A global array is staged into LDS kStage values at a time, double-buffered: while
+// thread 0 consumes one block the waves after the first stage the next, so thread 0 reads LDS and
+// never waits on global memory after the first block; an array already in LDS is read in place.
+// step(v, cnt, first) consumes values in order and returns where the loop ends; every thread
+// returns thread 0's stop index (n if none).  `stage` holds 2 kStage doubles.
 constexpr int kStage = 4096;
-// Thread 0's pass over src[0..m) (element i is number base + i), eight values per group: the
-// reads of a group overlap, and step(v, cnt, first) consumes cnt <= 8 values in order, returning
-// the position in the group where the loop ends (-1: go on).  Returns the index where it ended,
-// or m.
+// Thread 0's pass over an array already in LDS (the top-k path's kept terms, at most a few hundred),
+// eight values per group: the reads of a group overlap, and step(v, cnt, first) consumes cnt <= 8
+// values in order, returning the position in the group where the loop ends (-1: go on).  Returns
+// the index where it ended, or m.
 template <typename F>
 __device__ __forceinline__ int consume(const double* src, int m, int base, F& step) {
   int i = 0;
@@ -382,6 +384,54 @@ __device__ __forceinline__ int consume(const double* src, int m, int base, F& st
   return m;
 }
 
+// The same over a staged block of a global array (element i is number base + i), the next group's
+// reads issued before the current group is consumed (the adds never wait on LDS);
+// step(v, cnt, first) consumes cnt <= 8 values in order, returning the position in the group where
+// the loop ends (-1: go on).  Returns the index where it ended, or m.
+template <typename F>
+__device__ __forceinline__ int consume_pipelined(const double* src, int m, int base, F& step) {
+  auto load8 = [&](double (&v)[8], int i) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[i + u];
+  };
+  int i = 0;
+  if (m >= 8) {
+    double v0[8], v1[8];
+    load8(v0, 0);
+    // two groups per iteration, alternating buffers: the count is a constant once step is inlined
+    for (; i + 24 <= m; i += 16) {
+      load8(v1, i + 8);
+      int e = step(v0, 8, base + i);
+      if (e >= 0) return i + e;
+      load8(v0, i + 16);
+      e = step(v1, 8, base + i + 8);
+      if (e >= 0) return i + 8 + e;
+    }
+    // one or two whole groups left, v0 holding group i
+    if (i + 16 <= m) {
+      load8(v1, i + 8);
+      int e = step(v0, 8, base + i);
+      if (e >= 0) return i + e;
+      e = step(v1, 8, base + i + 8);
+      if (e >= 0) return i + 8 + e;
+      i += 16;
+    } else {
+      const int e = step(v0, 8, base + i);
+      if (e >= 0) return i + e;
+      i += 8;
+    }
+  }
+  if (i < m) {
+    const int cnt = m - i;
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = u < cnt ? src[i + u] : 0.0;
+    const int e = step(v, cnt, base + i);
+    if (e >= 0) return i + e;
+  }
+  return m;
+}
+
 template <typename F>
 __device__ int serial_loop(const double* p, int n, bool in_lds, double* stage, int* s_stop, F&& step) {
   if (in_lds) {
@@ -391,18 +441,27 @@ __device__ int serial_loop(const double* p, int n, bool in_lds, double* stage, i
     __syncthreads();
     return r;
   }
+  const int m0 = min(kStage, n);
+  for (int i = threadIdx.x; i < m0; i += blockDim.x) stage[i] = p[i];
+  __syncthreads();
   int stop = n;
   for (int base = 0; base < n; base += kStage) {
-    const int m = min(kStage, n - base);
-    for (int i = threadIdx.x; i < m; i += blockDim.x) stage[i] = p[base + i];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int i = consume(stage, m, base, step);
-      *s_stop = i < m ? base + i : n;
+    const int m = min(kStage, n - base), c = base / kStage;
+    const double* cur = stage + (c & 1) * kStage;
+    if (threadIdx.x < kWave) {
+      if (threadIdx.x == 0) {
+        const int i = consume_pipelined(cur, m, base, step);
+        *s_stop = i < m ? base + i : n;
+      }
+    } else if (base + kStage < n) {  // the next block into the other buffer
+      double* nxt = stage + ((c + 1) & 1) * kStage;
+      const int nb = base + kStage, mn = min(kStage, n - nb);
+      for (int i = static_cast<int>(threadIdx.x) - kWave; i < mn; i += static_cast<int>(blockDim.x) - kWave)
+        nxt[i] = p[nb + i];
     }
     __syncthreads();
     stop = *s_stop;
-    __syncthreads();  // stage and s_stop are rewritten next round
+    __syncthreads();  // s_stop is rewritten next round
     if (stop < n) break;
   }
   return stop;
@@ -454,7 +513,7 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
 }
 
 // The sampler after the sort (src/sampler.cpp:42-69): softmax over the kept ids, the nucleus, the
-// draw and the CDF walk.  `sorted` holds the keys in descending order, `stage` kStage doubles of LDS.
+// draw and the CDF walk.  `sorted` holds the keys in descending order, `stage` 2 kStage doubles of LDS.
 __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, int keep, bool topk, double* prob,
                             double* s_prob, double* stage, int& s_stop, double& s_sum, int& s_keep) {
   // softmax over the kept ids in double (src/sampler.cpp:42-49); with top-k the kept probabilities
@@ -737,7 +796,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     bitonic_global(keys, a.npow2, s_keys);
     sorted = keys;
   }
-  static_assert(sizeof(s_keys) >= kStage * sizeof(double), "staging buffer");
+  static_assert(sizeof(s_keys) >= 2 * kStage * sizeof(double), "staging buffers");
   sample_tail(a, b, sorted, keep, topk, prob, s_prob, reinterpret_cast<double*>(s_keys), s_stop, s_sum, s_keep);
 }
 
@@ -787,7 +846,7 @@ __global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
 // The sampler after a split sort: the merged keys, every id kept unless top-k (above the LDS path)
 // keeps k.
 __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
-  __shared__ double s_stage[kStage];
+  __shared__ double s_stage[2 * kStage];
   __shared__ int s_stop, s_keep;
   __shared__ double s_sum;
   const int b = blockIdx.x, V = a.vocab;
