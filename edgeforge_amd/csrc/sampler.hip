@@ -384,52 +384,39 @@ __device__ __forceinline__ int consume(const double* src, int m, int base, F& st
   return m;
 }
 
-// The same over a staged block of a global array (element i is number base + i), the next group's
-// reads issued before the current group is consumed (the adds never wait on LDS);
-// step(v, cnt, first) consumes cnt <= 8 values in order, returning the position in the group where
-// the loop ends (-1: go on).  Returns the index where it ended, or m.
+// The same over a staged block of a global array (element i is number base + i): the first
+// m - m % 32 values go through a ring of four groups, three groups' reads in flight ahead of the one
+// being consumed (an LDS read takes longer than a group's eight dependent adds), the rest as above.
 template <typename F>
 __device__ __forceinline__ int consume_pipelined(const double* src, int m, int base, F& step) {
   auto load8 = [&](double (&v)[8], int i) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) v[u] = src[i + u];
   };
-  int i = 0;
-  if (m >= 8) {
-    double v0[8], v1[8];
+  const int ng = (m / 32) * 4;  // groups through the ring, a multiple of four
+  if (ng > 0) {
+    double v0[8], v1[8], v2[8], v3[8];
     load8(v0, 0);
-    // two groups per iteration, alternating buffers: the count is a constant once step is inlined
-    for (; i + 24 <= m; i += 16) {
-      load8(v1, i + 8);
-      int e = step(v0, 8, base + i);
-      if (e >= 0) return i + e;
-      load8(v0, i + 16);
-      e = step(v1, 8, base + i + 8);
-      if (e >= 0) return i + 8 + e;
-    }
-    // one or two whole groups left, v0 holding group i
-    if (i + 16 <= m) {
-      load8(v1, i + 8);
-      int e = step(v0, 8, base + i);
-      if (e >= 0) return i + e;
-      e = step(v1, 8, base + i + 8);
-      if (e >= 0) return i + 8 + e;
-      i += 16;
-    } else {
-      const int e = step(v0, 8, base + i);
-      if (e >= 0) return i + e;
-      i += 8;
+    load8(v1, 8);
+    load8(v2, 16);
+    for (int g = 0; g < ng; g += 4) {
+      load8(v3, 8 * (g + 3));
+      int e = step(v0, 8, base + 8 * g);
+      if (e >= 0) return 8 * g + e;
+      if (g + 4 < ng) load8(v0, 8 * (g + 4));
+      e = step(v1, 8, base + 8 * (g + 1));
+      if (e >= 0) return 8 * (g + 1) + e;
+      if (g + 5 < ng) load8(v1, 8 * (g + 5));
+      e = step(v2, 8, base + 8 * (g + 2));
+      if (e >= 0) return 8 * (g + 2) + e;
+      if (g + 6 < ng) load8(v2, 8 * (g + 6));
+      e = step(v3, 8, base + 8 * (g + 3));
+      if (e >= 0) return 8 * (g + 3) + e;
     }
   }
-  if (i < m) {
-    const int cnt = m - i;
-    double v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = u < cnt ? src[i + u] : 0.0;
-    const int e = step(v, cnt, base + i);
-    if (e >= 0) return i + e;
-  }
-  return m;
+  const int i0 = 8 * ng;
+  const int e = consume(src + i0, m - i0, base + i0, step);
+  return i0 + e;
 }
 
 template <typename F>
@@ -549,17 +536,27 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
     // n = the number of terms taken; once cum is final and below top_p the loop would take all
     // the running sums of a group in registers; the first that reaches top_p ends the loop, a
     // group that leaves cum unchanged ends it with all terms kept
-    int n = serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int) {
+    // the group's running sums form one chain of adds; the comparisons read them off the chain
+    // (values past cnt are zeros: the sums stay put, so the first crossing is inside the group)
+    int n = serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int, int) {
       const double before = cum;
-      int hit = -1;
+      double c[8], x = cum;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        if (u < cnt && hit < 0) {
-          cum = cum + v[u];
-          if (cum >= tp) hit = u;
-        }
+        x = x + v[u];
+        c[u] = x;
       }
-      if (hit >= 0) return hit;
+      int hit = -1;
+#pragma unroll
+      for (int u = 7; u >= 0; --u)
+        if (c[u] >= tp) hit = u;
+      if (hit >= 0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u == hit) cum = c[u];
+        return hit;
+      }
+      cum = x;
       return (cum == before && before > 0.0) ? 0 : -1;
     });
     if (threadIdx.x == 0) s_keep = n < keep && cum >= tp ? n + 1 : keep;  // cum < tp: every term
@@ -583,20 +580,23 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
   }
   double cum = 0.0;
   int pick = keep - 1;  // the first i with r < cum; the last kept id when the sum ends below r
-  serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int cnt, int first) {
+  serial_loop(prob, keep, in_lds, stage, &s_stop, [&](const double (&v)[8], int, int first) {
     const double before = cum;
-    int hit = -1;
+    double c[8], x = cum;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      if (u < cnt && hit < 0) {
-        cum = cum + v[u];
-        if (r < cum) hit = u;
-      }
+      x = x + v[u];
+      c[u] = x;
     }
+    int hit = -1;
+#pragma unroll
+    for (int u = 7; u >= 0; --u)
+      if (r < c[u]) hit = u;
     if (hit >= 0) {
       pick = first + hit;
       return hit;
     }
+    cum = x;
     return (cum == before && before > 0.0) ? 0 : -1;  // cum is final and r >= cum
   });
   if (threadIdx.x == 0) a.out[b] = static_cast<int>(key_id(sorted[pick]));
