@@ -70,6 +70,36 @@ def profile_gate_up(H, L, model, batch: int, launches: int = 400):
     return avg.value, nbytes, reps
 
 
+def profile_sampler(H, L, calls: int = 50) -> dict:
+    """Microseconds per sampler call (host clock around `calls` back-to-back calls) on seeded N(0, 3)
+    logits, V = 32000, 64-token histories: top-p 0.95 without top-k (the full-sort path) and top-k 40 +
+    top-p 0.95 (config 3), at B = 1 and B = 64."""
+    V = 32000
+    cfgs = {"top_p_only": dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.1),
+            "top_k40_top_p": dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)}
+    res = {}
+    for batch in (1, 64):
+        g = np.random.default_rng(5)
+        logits = (g.standard_normal((batch, V), dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+        hist = g.integers(0, V, size=(batch, 64)).astype(np.int32)
+        dl, dh = H.DeviceArray.from_host(logits), H.DeviceArray.from_host(hist)
+        hl = H.DeviceArray.from_host(np.full(batch, 64, np.int32))
+        ws = H.DeviceArray((L.lib().ef_hip_sample_workspace_bytes(V, batch),), np.uint8)
+        out = H.DeviceArray((batch,), np.int32)
+        for name, cfg in cfgs.items():
+            rng = H.RngStates(list(range(batch)))
+            for _ in range(5):
+                H.sample(dl, V, cfg, out, batch=batch, hist=dh, hist_len=hl, hist_ld=64, rng=rng, ws=ws)
+            H.sync()
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                H.sample(dl, V, cfg, out, batch=batch, hist=dh, hist_len=hl, hist_ld=64, rng=rng, ws=ws)
+            H.sync()
+            res[f"{name}_b{batch}_us"] = round((time.perf_counter() - t0) / calls * 1e6, 1)
+            log(f"[bench] sampler {name} B={batch}: {res[f'{name}_b{batch}_us']} us/call")
+    return res
+
+
 def profile_plain(H, L, model, key, qtype, block, batch: int, launches: int = 400):
     w0 = model.weights[key]
     src = model.packed[key]
@@ -209,6 +239,12 @@ def main() -> int:
     ap.add_argument("--only-batched", action="store_true",
                     help="profiling mode: only the B=64 Q4_0 5632x2048 matvec launches (fragment preparation + "
                          "matrix-core GEMV) over rotating replicas; prints their average time")
+    ap.add_argument("--no-step-profile", action="store_true",
+                    help="skip the per-group decode profile (ef_hip_engine_profile): for runs under rocprofv3, where "
+                         "that call has crashed the host")
+    ap.add_argument("--only-sampler", action="store_true",
+                    help="profiling mode: only sampler calls on [B, 32000] N(0,3) logits (top-p 0.95 without top-k, "
+                         "then top-k 40 / top-p 0.95; T 0.8, penalty 1.1) at B=1 and B=64; prints us per call")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -223,6 +259,9 @@ def main() -> int:
     H.init(0)
     dev = L.device_name()
     log(f"[bench] device {dev}")
+    if args.only_sampler:
+        print(json.dumps(profile_sampler(H, L)), flush=True)
+        return 0
     t0 = time.time()
     model = DeviceModel.synthetic(TINYLLAMA, seed=2024)
     log(f"[bench] synthetic TinyLlama-1.1B built and quantized on the device in {time.time() - t0:.1f}s")
@@ -247,7 +286,7 @@ def main() -> int:
     eng = Engine(model, max_seq=23 + max(K, W) + 1)
     eng.generate([prompt], W + 1)
     toks, pre_s, dec_s = eng.generate([prompt], K + 1)
-    prof_b1 = step_profile(eng, dec_s / K * 1e3, TINYLLAMA)
+    prof_b1 = None if args.no_step_profile else step_profile(eng, dec_s / K * 1e3, TINYLLAMA)
     eng.close()
     tps = K / dec_s
     log(f"[bench] B=1 decode: {K} steps in {dec_s * 1e3:.2f} ms -> {tps:.1f} tok/s "
@@ -270,7 +309,8 @@ def main() -> int:
         eng = Engine(model, max_seq=23 + max(K, W) + 1, batch=B)
         eng.generate(prompts, W + 1)
         _, pre64, dec64 = eng.generate(prompts, K + 1)
-        extra["step_profile_b64"] = step_profile(eng, dec64 / K * 1e3, TINYLLAMA)
+        if not args.no_step_profile:
+            extra["step_profile_b64"] = step_profile(eng, dec64 / K * 1e3, TINYLLAMA)
         seeds = list(range(100, 100 + B))
         eng.generate(prompts, W + 1, sampler=samp, rng=H.RngStates(seeds))
         _, _, sdec64 = eng.generate(prompts, K + 1, sampler=samp, rng=H.RngStates(seeds))
@@ -299,6 +339,7 @@ def main() -> int:
     extra["q4_0_5632x2048_b64_mfma_frac"] = round(q4b_flops / (q4b_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
     lm_ms, lm_bytes = profile_plain(H, L, model, "lm_head", L.Q8_0, 34, batch=1)
     extra["lm_head_q8_0_b1_gbs"] = round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1)
+    extra["sampler_us_per_call"] = profile_sampler(H, L, calls=20)
     mb = membench(L)
     extra["membench_gbs"] = mb["median_gbs"]
     log(f"[bench] membench (1 GiB read, checksum ok): median {mb['median_gbs']} GB/s, best {mb['best_gbs']} GB/s")
