@@ -169,6 +169,24 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Wave-wide unsigned max through DPP, returned on every lane (lanes a step does not feed keep their
+// own value).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_self_u(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = max(v, dpp_self_u<0xB1>(v));
+  v = max(v, dpp_self_u<0x4E>(v));
+  v = max(v, dpp_self_u<0x141>(v));
+  v = max(v, dpp_self_u<0x140>(v));
+  v = max(v, dpp_self_u<0x142, 0xA>(v));
+  v = max(v, dpp_self_u<0x143, 0xC>(v));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // Wave-wide double sum through DPP, returned on every lane (lane 63 holds it, then a broadcast).
 __device__ __forceinline__ double wave_sum_d_dpp(double v) {
   v = group_sum_dpp<32>(v);

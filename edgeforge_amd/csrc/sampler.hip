@@ -31,6 +31,8 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kRegSlots = 32;  // logits per thread on the register path (V <= 32768)
 constexpr int kMaxTopK = 1024;
+constexpr int kFloorMaxRank = 4;     // top-k by a key floor for k <= 4 * waves (the rest: radix select)
+constexpr int kMaxGathered = 2 * kThreads;  // keys above the floor that one LDS sort takes
 constexpr int kMtN = 312, kMtM = 156;
 
 // ---- std::mt19937_64 on the device (ISO C++ [rand.predef]) -------------------------------------------
@@ -607,6 +609,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   constexpr int kWaves = kThreads / kWave;
   __shared__ uint32_t s_hist[256], s_sfx[256];
   __shared__ uint32_t s_whist[kWaves * 256];  // per-wave histograms of the radix select
+  __shared__ uint32_t s_floor[kWaves * kFloorMaxRank];  // each wave's largest lane maxima (order bits)
+  __shared__ uint32_t s_floor_bits;
   __shared__ float s_val[kThreads / kWave];
   __shared__ int s_idx[kThreads / kWave];
   __shared__ int s_cnt, s_keep, s_stop;
@@ -633,15 +637,16 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   const bool topk = a.top_k > 0 && a.top_k < V && a.top_k <= kMaxTopK;
   const bool reg = a.temperature > 0.0f && topk && V <= kRegSlots * kThreads;
   float rv[kRegSlots];
-  auto for_each_value = [&](auto&& f) {
+  auto ov = [&](int j) { return order_bits(rv[j]); };  // the high half of slot j's key
+  auto for_each_key = [&](auto&& f) {
     if (reg) {
 #pragma unroll
       for (int j = 0; j < kRegSlots; ++j) {
         const int id = threadIdx.x + kThreads * j;
-        if (id < V) f(rv[j], id);
+        if (id < V) f((static_cast<uint64_t>(ov(j)) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - id));
       }
     } else {
-      for (int i = threadIdx.x; i < V; i += blockDim.x) f(work[i], i);
+      for (int i = threadIdx.x; i < V; i += blockDim.x) f(make_key(work[i], i));
     }
   };
   if (reg) {
@@ -716,7 +721,6 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   int keep = V;
   const uint64_t* sorted = nullptr;
   if (topk) {
-    // radix select of the k-th largest key, 8 bits per pass from the top
     if (threadIdx.x == 0) {
       s_prefix = 0;
       s_mask = 0;
@@ -725,17 +729,72 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       s_cnt = 0;
     }
     __syncthreads();
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    // Candidates by a floor (k <= 64, logits in registers), on the keys' high halves (order bits):
+    // each wave records its m largest lane maxima (m >= k / waves; one more than that, at most 4,
+    // for a closer floor), every round removing the lanes that hold the recorded maximum, and the
+    // floor is the k-th largest of the kWaves * m records.  Each record >= floor stands for a lane
+    // of its own whose largest key has order bits >= floor, so at least k keys do, and the k largest
+    // keys are all among them (a floor of 0 takes every key).  Those keys (for spread logits about
+    // k + k / 8) are gathered and sorted; the first k are the kept set, the same keys the radix
+    // select below finds.  Empty lanes have maximum 0.
+    int n_keys = -1;  // keys gathered in s_keys, or -1 when the radix select runs
+    const int m_min = (a.top_k + kWaves - 1) / kWaves, m = min(kFloorMaxRank, m_min + 1);
+    if (reg && m_min <= kFloorMaxRank) {
+      uint32_t cur = 0;
+#pragma unroll
+      for (int j = 0; j < kRegSlots; ++j)
+        if (static_cast<int>(threadIdx.x) + kThreads * j < V) cur = max(cur, ov(j));
+      for (int r = 0; r < m; ++r) {
+        const uint32_t wm = wave_max_u32_dpp(cur);
+        if (lane == 0) s_floor[wave * kFloorMaxRank + r] = wm;
+        if (cur == wm) cur = 0;
+      }
+      if (lane == 0)
+        for (int r = m; r < kFloorMaxRank; ++r) s_floor[wave * kFloorMaxRank + r] = 0u;  // rank below every record
+      __syncthreads();
+      if (wave == 0) {  // the k-th largest record: rank by (value, then position)
+        static_assert(kWaves * kFloorMaxRank == kWave, "one record per lane");
+        const uint32_t v = s_floor[lane];
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < kWave; ++j) {
+          const uint32_t u = s_floor[j];
+          rank += (u > v || (u == v && j < lane)) ? 1 : 0;
+        }
+        if (rank == a.top_k - 1) s_floor_bits = v;
+      }
+      __syncthreads();
+      const uint32_t floor_bits = s_floor_bits;
+#pragma unroll
+      for (int j = 0; j < kRegSlots; ++j) {
+        const int id = threadIdx.x + kThreads * j;
+        if (id < V && ov(j) >= floor_bits) {
+          const int pos = atomicAdd(&s_cnt, 1);
+          if (pos < kMaxGathered)
+            s_keys[pos] = (static_cast<uint64_t>(ov(j)) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - id);
+        }
+      }
+      __syncthreads();
+      n_keys = s_cnt;
+      __syncthreads();
+      if (n_keys > kMaxGathered) {  // more than one sort in LDS takes: the radix select instead
+        n_keys = -1;
+        if (threadIdx.x == 0) s_cnt = 0;
+        __syncthreads();
+      }
+    }
+    if (n_keys < 0) {
+    // radix select of the k-th largest key, 8 bits per pass from the top.
     // Each wave counts into its own histogram (keys of similar logits share their top digits,
     // and one shared histogram serialises those atomics across the waves).  The digit d kept is
     // the largest with S(d) = (keys still in play with digit >= d) >= need, found by a parallel
     // suffix sum; need then drops by S(d + 1).
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
     for (int shift = 56; shift >= 0 && !s_done; shift -= 8) {
       for (int i = threadIdx.x; i < kWaves * 256; i += blockDim.x) s_whist[i] = 0u;
       __syncthreads();
       const uint64_t prefix = s_prefix, mask = s_mask;
-      for_each_value([&](float v, int i) {
-        const uint64_t k = make_key(v, i);
+      for_each_key([&](uint64_t k) {
         if ((k & mask) == prefix) atomicAdd(&s_whist[wave * 256 + ((k >> shift) & 255u)], 1u);
       });
       __syncthreads();
@@ -768,17 +827,18 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       __syncthreads();
     }
     const uint64_t prefix = s_prefix, mask = s_mask;
-    for_each_value([&](float v, int i) {
-      const uint64_t k = make_key(v, i);
+    for_each_key([&](uint64_t k) {
       if ((k & mask) >= prefix) {
         const int pos = atomicAdd(&s_cnt, 1);
         if (pos < kChunk) s_keys[pos] = k;
       }
     });
     __syncthreads();
+    n_keys = a.top_k;
+    }
     int n2 = 1;
-    while (n2 < a.top_k) n2 <<= 1;
-    for (int i = a.top_k + threadIdx.x; i < n2; i += blockDim.x) s_keys[i] = 0ull;
+    while (n2 < n_keys) n2 <<= 1;
+    for (int i = n_keys + threadIdx.x; i < n2; i += blockDim.x) s_keys[i] = 0ull;
     __syncthreads();
     if (n2 <= kWave) {
       bitonic_wave(s_keys, n2);

@@ -114,3 +114,40 @@ def test_sampler_seeded_distribution(hip):
         assert t == cpu.sample(l)
         counts[t] += 1
     assert np.all(np.abs(counts / n - [0.7, 0.2, 0.1]) < 0.03)
+
+
+@pytest.mark.parametrize("layout", ["one_thread", "two_waves", "all_equal", "few_finite"])
+@pytest.mark.parametrize("top_k", [1, 16, 40, 128, 129])
+def test_sampler_topk_floor_layouts(hip, layout, top_k):
+    """The radix select's key floor (each wave's m-th largest lane maximum, the smallest over the
+    waves) on layouts that put the k largest logits in few lanes: the kept set, and so the ids,
+    must still equal the reference's (src/sampler.cpp:26-43).  Thread t of the 1024-thread
+    workgroup holds ids t + 1024 j."""
+    V, batch = 32000, 4
+    print(f"[case] sampler floor layout={layout} k={top_k}", flush=True)
+    g = D.rng(7 + top_k)
+    logits = (g.standard_normal((batch, V), dtype=np.float32)).astype(np.float32)
+    if layout == "one_thread":  # the 31 largest in thread 5, the next in thread 900
+        logits[:, 5::1024] += np.float32(20.0)
+        logits[:, 900::1024] += np.float32(10.0)
+    elif layout == "two_waves":  # every large logit in waves 3 and 11
+        for w in (3, 11):
+            for t in range(64 * w, 64 * w + 64):
+                logits[:, t::1024] += np.float32(8.0)
+    elif layout == "all_equal":  # ties everywhere: keys differ only by id
+        logits[:] = np.float32(0.25)
+    else:  # only 50 finite logits above -inf
+        logits[:] = -np.inf
+        idx = g.choice(V, size=50, replace=False)
+        logits[:, idx] = g.standard_normal(50).astype(np.float32)
+    cfg = dict(temperature=0.9, top_k=top_k, top_p=0.97, repetition_penalty=1.0)
+    seeds = [11 + b for b in range(batch)]
+    rng = hip.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    hist = np.zeros((batch, 1), np.int32)
+    out = hip.DeviceArray((batch,), np.int32)
+    for step in range(3):
+        hip.sample(hip.DeviceArray.from_host(logits), V, cfg, out, batch=batch, hist=hip.DeviceArray.from_host(hist),
+                   hist_len=hip.DeviceArray.from_host(np.zeros(batch, np.int32)), hist_ld=1, rng=rng)
+        want = [cpu[b].sample(logits[b], []) for b in range(batch)]
+        assert [int(v) for v in out.numpy()] == want, (layout, top_k, step)
