@@ -10,9 +10,11 @@
 //    select over the keys plus a bitonic sort of the k winners in LDS; top-k off (or > 1024) is a
 //    full bitonic sort of all keys in the workspace;
 //  * the softmax over the kept ids, the top-p cut, its renormalisation and the CDF walk are the
-//    reference's sequential double loops, run by one thread in the same order.  They stop early
-//    at the first term that leaves the running sum unchanged: the terms are sorted, non-negative
-//    and non-increasing, so no later one can change it either;
+//    reference's left-to-right double sums: on one thread in the same order (the top-k path and
+//    more than 32768 kept ids), stopping at the first term that leaves the running sum unchanged
+//    (the terms are sorted, non-negative and non-increasing, so no later one can change it), or
+//    reproduced exactly in parallel rounds that count each term's rounding within the running
+//    sum's binade (exact_scan, below);
 //  * the draw is std::uniform_real_distribution<double>(0, 1) over a std::mt19937_64 kept on the
 //    device (one state per sequence), advanced once per call exactly when temperature > 0.
 // The one libm call is exp(double); the device's exp and glibc's agree to the last bit except in
@@ -903,8 +905,245 @@ __global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
   out[pos] = x;
 }
 
+// ---- the reference's left-to-right double sums, in parallel and bit for bit -----------------------------
+// s_j = RN(s_{j-1} + t_j) from s_{-1} = 0.  While s stays in one binade [2^e, 2^(e+1)) it is a
+// multiple of u = 2^(e-52), and a step adds t_j rounded to a multiple of u: s_j = s_{j-1} + k_j u,
+// k_j = t_j / u rounded to the nearest integer, provided s_{j-1} + t_j < 2^(e+1) and t_j / u is
+// not halfway between integers (a tie rounds to the even multiple, which depends on s_{j-1}).  The
+// k_j do not depend on each other, so a round takes every remaining step at the current binade:
+// the k_j, their prefix sums (integers below 2^53, exact in doubles), and the first step that
+// leaves the binade or is a tie.  Every step before that one is exact; that one is a plain double
+// add by the thread that holds its term, and the next round starts after it in its binade.  A sum
+// that passes through b binades takes about b + 1 rounds (the one-term start from 0 included).
+constexpr int kScanPer = 32;  // terms per thread, contiguous: element kScanPer * thread + i
+
+struct ScanShared {
+  double s, hit_sum;  // running sum before element j0; the running sum at the hit
+  int j0, hit, done;
+  double wsum[kThreads / kWave];
+  int wbad[kThreads / kWave], whit[kThreads / kWave];
+};
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ double uniform_d(double v) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// MODE 0: the sum of t_0 .. t_{n-1}; 1: the first j with s_j >= x; 2: the first j with x < s_j.
+// Returns that j (n when no step satisfies the predicate) on every thread and sets *sum to s_j
+// (to the whole sum when none does).  Every term must be finite and >= 0.
+// Control flow: every decision of a round is taken on values read from LDS and made wave-uniform
+// (readfirstlane), with no early continue, so the loop stays one uniform loop and the step's owner
+// runs its step inside the round.  (With the decisions left per lane, the compiler built the round
+// as an inner loop that only the owner lane left, so the owner's wave never reached the step and
+// the other lanes repeated the round.)  A round either ends the scan or takes one step, so n + 1
+// rounds suffice; the bound makes every wave's exit certain.
+template <int MODE>
+__device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShared& sh, double* sum) {
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * kScanPer;
+  constexpr int kW = kThreads / kWave;
+  auto pred = [&](double s) { return MODE == 1 ? s >= x : (MODE == 2 ? x < s : false); };
+  if (tid == 0) {
+    sh.s = 0.0;
+    sh.j0 = 0;
+    sh.hit = n;
+    sh.done = n == 0;
+  }
+  for (int round = 0; round <= n + 1; ++round) {
+    __syncthreads();
+    const double s = uniform_d(sh.s);
+    const int j0 = uniform_i(sh.j0), done = uniform_i(sh.done);
+    __syncthreads();  // read before any thread rewrites the state
+    if (done) break;
+    int jb = j0, jh = n;  // the step taken as a plain add this round; the first hit
+    double sp = s;        // the running sum before step jb (on its owner)
+    const bool usable = s >= 0x1p-1000;  // s = m 2^ex, m in [0.5, 1): u = 2^(ex - 53), s / u = s 2^sc
+    if (usable) {
+      int ex;
+      (void)frexp(s, &ex);
+      const int sc = 53 - ex;
+      const double M0 = ldexp(s, sc);
+      const bool mine = base + kScanPer > j0 && base < n;
+      double T = 0.0;
+      if (mine) {
+#pragma unroll
+        for (int i = 0; i < kScanPer; ++i) {
+          const int j = base + i;
+          if (j >= j0 && j < n) T += rint(ldexp(t[i], sc));
+        }
+      }
+      // exclusive prefix of the thread totals: lanes below this one, then the waves below
+      // (a thread after the first inexact step may hold huge totals; they never enter the
+      // prefix of a thread before it)
+      double incl = T;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const double y = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += y;
+      }
+      double K = __shfl_up(incl, 1, kWave);
+      if (lane == 0) K = 0.0;
+      if (lane == kWave - 1) sh.wsum[wave] = incl;
+      __syncthreads();
+      for (int w = 0; w < wave; ++w) K += sh.wsum[w];
+      int my_bad = n, my_hit = n;
+      double my_hs = 0.0, Kb = 0.0;
+      if (mine) {
+        bool stop = false;
+#pragma unroll
+        for (int i = 0; i < kScanPer; ++i) {
+          const int j = base + i;
+          if (!stop && j >= j0 && j < n) {
+            const double y = ldexp(t[i], sc), k = rint(y), Mp = M0 + K;  // s_{j-1} / u, exact
+            if (fabs(y - k) == 0.5 || !(y < 0x1p53 - Mp)) {
+              my_bad = j;
+              Kb = Mp;
+              stop = true;
+            } else {
+              K += k;
+              if (MODE != 0) {
+                const double sj = ldexp(M0 + K, -sc);
+                if (pred(sj)) {
+                  my_hit = j;
+                  my_hs = sj;
+                  stop = true;
+                }
+              }
+            }
+          }
+        }
+      }
+      const int wb = wave_min_i(my_bad), wh = wave_min_i(my_hit);
+      if (lane == 0) {
+        sh.wbad[wave] = wb;
+        sh.whit[wave] = wh;
+      }
+      __syncthreads();
+      int b2 = n, h2 = n;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) {
+        b2 = min(b2, sh.wbad[w]);
+        h2 = min(h2, sh.whit[w]);
+      }
+      jb = uniform_i(b2);
+      jh = uniform_i(h2);
+      if (jh < jb) {  // a hit before any inexact step
+        if (my_hit == jh) {
+          sh.hit = jh;
+          sh.hit_sum = my_hs;
+          sh.done = 1;
+        }
+      } else if (jb >= n) {  // every remaining step exact: the total
+        if (tid == 0) {
+          double tot = 0.0;
+          for (int w = 0; w < kW; ++w) tot += sh.wsum[w];
+          sh.s = ldexp(M0 + tot, -sc);
+          sh.done = 1;
+        }
+      } else {
+        sp = ldexp(Kb, -sc);  // meaningful on the owner of jb only
+      }
+    }
+    const bool take = !usable || (jh >= jb && jb < n);  // wave-uniform
+    if (take && jb / kScanPer == tid) {  // the step at jb as the reference takes it
+      double tj = 0.0;
+#pragma unroll
+      for (int i = 0; i < kScanPer; ++i)
+        if (base + i == jb) tj = t[i];
+      const double sn = sp + tj;
+      if (MODE != 0 && pred(sn)) {
+        sh.hit = jb;
+        sh.hit_sum = sn;
+        sh.done = 1;
+      } else {
+        sh.s = sn;
+        sh.j0 = jb + 1;
+        sh.done = jb + 1 >= n;
+      }
+    }
+  }
+  __syncthreads();
+  const int hit = sh.hit;
+  *sum = hit < n ? sh.hit_sum : sh.s;
+  __syncthreads();  // sh is reused by the next scan
+  return hit;
+}
+
+// sample_tail with the kept terms in registers (keep <= kThreads * kScanPer) and every sequential
+// loop an exact_scan: the same sums, cut and pick as the reference's loops (src/sampler.cpp:42-69).
+// A term that is not finite is a NaN (a NaN logit, or +inf minus the +inf maximum): the reference's
+// sum is then NaN, so are all its probabilities, no comparison holds, and the pick is the last
+// kept id after one draw, which is what this returns.
+__device__ void sample_tail_scan(const SampleArgs& a, int b, const uint64_t* sorted, int keep, ScanShared& sh,
+                                 int& s_flag) {
+  const int tid = threadIdx.x, base = tid * kScanPer;
+  const float mx = key_value(sorted[0]);
+  double t[kScanPer];
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) {
+    const int j = base + i;
+    t[i] = j < keep ? exp(static_cast<double>(key_value(sorted[j]) - mx)) : 0.0;
+    finite = finite && isfinite(t[i]);
+  }
+  if (tid == 0) s_flag = 0;
+  __syncthreads();
+  if (!finite) s_flag = 1;
+  __syncthreads();
+  if (s_flag) {
+    if (tid == 0) {
+      (void)mt_uniform(reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes));
+      a.out[b] = static_cast<int>(key_id(sorted[keep - 1]));
+    }
+    return;
+  }
+  double sum;
+  exact_scan<0>(t, keep, 0.0, sh, &sum);
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) t[i] = t[i] / sum;
+  int kp = keep;
+  if (a.top_p < 1.0f) {  // nucleus: the first n with cum >= top_p; s2 is cum there (or the whole sum)
+    double cum;
+    const int n = exact_scan<1>(t, keep, static_cast<double>(a.top_p), sh, &cum);
+    kp = max(n < keep ? n + 1 : keep, 1);
+#pragma unroll
+    for (int i = 0; i < kScanPer; ++i) t[i] = t[i] / cum;
+  }
+  if (tid == 0) {
+    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
+    sh.hit_sum = mt_uniform(st);
+  }
+  __syncthreads();
+  const double r = sh.hit_sum;
+  __syncthreads();
+  double cum;
+  const int i = exact_scan<2>(t, kp, r, sh, &cum);
+  if (tid == 0) a.out[b] = static_cast<int>(key_id(sorted[i < kp ? i : kp - 1]));
+}
+
+__device__ __forceinline__ int tail_keep(const SampleArgs& a) {
+  return a.top_k > 0 && a.top_k < a.vocab ? a.top_k : a.vocab;
+}
+
 // The sampler after a split sort: the merged keys, every id kept unless top-k (above the LDS path)
-// keeps k.
+// keeps k.  Up to kThreads * kScanPer kept ids (a kernel of its own: with the loops below in the
+// same kernel, the registers spilled).
+__global__ __launch_bounds__(kThreads) void sample_scan_kernel(SampleArgs a) {
+  __shared__ ScanShared sh;
+  __shared__ int s_flag;
+  sample_tail_scan(a, blockIdx.x, merged_of(a, blockIdx.x), tail_keep(a), sh, s_flag);
+}
+
+// More kept ids: the loops one term at a time.
 __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
   __shared__ double s_stage[2 * kStage];
   __shared__ int s_stop, s_keep;
@@ -912,8 +1151,7 @@ __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
   const int b = blockIdx.x, V = a.vocab;
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
   double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));
-  const int keep = a.top_k > 0 && a.top_k < V ? a.top_k : V;
-  sample_tail(a, b, merged_of(a, b), keep, false, prob, nullptr, s_stage, s_stop, s_sum, s_keep);
+  sample_tail(a, b, merged_of(a, b), tail_keep(a), false, prob, nullptr, s_stage, s_stop, s_sum, s_keep);
 }
 
 }  // namespace
@@ -984,7 +1222,12 @@ int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_h
     hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
     hipLaunchKernelGGL(chunk_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
     hipLaunchKernelGGL(rank_merge_kernel, dim3(n2 / 256, batch), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(sample_tail_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    const int keep = cfg.top_k > 0 && cfg.top_k < vocab ? cfg.top_k : vocab;
+    if (keep <= kThreads * kScanPer) {
+      hipLaunchKernelGGL(sample_scan_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL(sample_tail_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+    }
   } else {
     hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
   }

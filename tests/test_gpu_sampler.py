@@ -151,3 +151,40 @@ def test_sampler_topk_floor_layouts(hip, layout, top_k):
                    hist_len=hip.DeviceArray.from_host(np.zeros(batch, np.int32)), hist_ld=1, rng=rng)
         want = [cpu[b].sample(logits[b], []) for b in range(batch)]
         assert [int(v) for v in out.numpy()] == want, (layout, top_k, step)
+
+
+@pytest.mark.parametrize("layout", ["peaked", "all_equal", "two_levels", "plus_inf", "minus_inf_tail", "tiny_tail"])
+@pytest.mark.parametrize("top_p", [1.0, 0.9, 0.5, 1e-6])
+def test_sampler_full_sort_sums(hip, layout, top_p):
+    """Sampling without top-k (the sorted softmax, nucleus and CDF sums over every id): ids equal
+    the reference's for distributions whose running sums cross many binades, stop at the first
+    term, tie everywhere, or are NaN (+inf logits: the reference then takes the last sorted id)
+    (src/sampler.cpp:42-69)."""
+    V, batch = 32000, 4
+    print(f"[case] sampler full-sort layout={layout} top_p={top_p}", flush=True)
+    g = D.rng(900 + len(layout))
+    logits = g.standard_normal((batch, V), dtype=np.float32)
+    if layout == "peaked":  # one id carries almost all the mass: the cut and the draw stop at term 0
+        logits[:, 77] = np.float32(40.0)
+    elif layout == "all_equal":
+        logits[:] = np.float32(-1.5)
+    elif layout == "two_levels":
+        logits[:] = np.float32(0.0)
+        logits[:, ::3] = np.float32(2.0)
+    elif layout == "plus_inf":
+        logits[:, 5] = np.float32(np.inf)
+    elif layout == "minus_inf_tail":
+        logits[:, 1000:] = np.float32(-np.inf)
+    else:  # terms down to the smallest doubles
+        logits = (logits * np.float32(80.0)).astype(np.float32)
+    cfg = dict(temperature=1.0, top_k=0, top_p=top_p, repetition_penalty=1.0)
+    seeds = [31 + b for b in range(batch)]
+    rng = hip.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    hist = np.zeros((batch, 1), np.int32)
+    out = hip.DeviceArray((batch,), np.int32)
+    for step in range(4):
+        hip.sample(hip.DeviceArray.from_host(logits), V, cfg, out, batch=batch, hist=hip.DeviceArray.from_host(hist),
+                   hist_len=hip.DeviceArray.from_host(np.zeros(batch, np.int32)), hist_ld=1, rng=rng)
+        want = [cpu[b].sample(logits[b], []) for b in range(batch)]
+        assert [int(v) for v in out.numpy()] == want, (layout, top_p, step)
