@@ -35,6 +35,12 @@ constexpr int kRegSlots = 32;  // logits per thread on the register path (V <= 3
 constexpr int kMaxTopK = 1024;
 constexpr int kFloorMaxRank = 4;     // top-k by a key floor for k <= 4 * waves (the rest: radix select)
 constexpr int kMaxGathered = 2 * kThreads;  // keys above the floor that one LDS sort takes
+constexpr int kScanPer = 32;  // sums over sorted terms: terms per thread, contiguous (kScanPer * thread + i)
+// The softmax-term region of a sequence's workspace: V rounded up to whole kScanPer-term columns
+// (rank_merge_kernel stores term j at (j % kScanPer) * columns + j / kScanPer).
+__host__ __device__ constexpr size_t prob_region_bytes(size_t v) {
+  return (((v + kScanPer - 1) / kScanPer) * kScanPer * 8 + 255) & ~size_t{255};
+}
 constexpr int kMtN = 312, kMtM = 156;
 
 // ---- std::mt19937_64 on the device (ISO C++ [rand.predef]) -------------------------------------------
@@ -626,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
   float* work = reinterpret_cast<float*>(ws);                                   // [V]
   double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));        // [V] (no top-k)
-  uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + ((V * 8 + 255) & ~255));  // [npow2]
+  uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + prob_region_bytes(V));  // [npow2]
   const float* lg = a.logits + b * a.ld;
 
   if (a.eos_p != nullptr) {
@@ -866,7 +872,10 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
 // Workspace of one sequence: work [V] floats, prob [V] doubles, keys [npow2], merged [npow2].
 __device__ __forceinline__ uint64_t* keys_of(const SampleArgs& a, int b) {
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
-  return reinterpret_cast<uint64_t*>(ws + ((a.vocab * 4 + 255) & ~255) + ((a.vocab * 8 + 255) & ~255));
+  return reinterpret_cast<uint64_t*>(ws + ((a.vocab * 4 + 255) & ~255) + prob_region_bytes(a.vocab));
+}
+__device__ __forceinline__ double* prob_of(const SampleArgs& a, int b) {
+  return reinterpret_cast<double*>(a.ws + static_cast<size_t>(b) * a.ws_stride + ((a.vocab * 4 + 255) & ~255));
 }
 __device__ __forceinline__ uint64_t* merged_of(const SampleArgs& a, int b) {
   return keys_of(a, b) + ((static_cast<size_t>(a.npow2) * 8 + 255) & ~size_t{255}) / 8;
@@ -903,6 +912,21 @@ __global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
     pos += lo;
   }
   out[pos] = x;
+  // the softmax term of the key at its sorted position, exp(double(v - max)) as the reference
+  // forms it (src/sampler.cpp:44-47; the maximum is the largest run head), laid out for
+  // sample_scan_kernel: with C = ceil(V / kScanPer) columns, the term of position j goes to
+  // (j % kScanPer) * C + j / kScanPer, so that thread t's contiguous terms j = kScanPer t + i are
+  // read with term i of every thread adjacent (coalesced)
+  if (pos < a.vocab) {
+    uint64_t top = keys[0];
+    for (int q = 1; q < runs; ++q) {
+      const uint64_t h = keys[static_cast<size_t>(q) * kChunk];
+      top = h > top ? h : top;
+    }
+    const int cols = (a.vocab + kScanPer - 1) / kScanPer;
+    prob_of(a, blockIdx.y)[(pos % kScanPer) * cols + pos / kScanPer] =
+        exp(static_cast<double>(key_value(x) - key_value(top)));
+  }
 }
 
 // ---- the reference's left-to-right double sums, in parallel and bit for bit -----------------------------
@@ -915,7 +939,6 @@ __global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
 // leaves the binade or is a tie.  Every step before that one is exact; that one is a plain double
 // add by the thread that holds its term, and the next round starts after it in its binade.  A sum
 // that passes through b binades takes about b + 1 rounds (the one-term start from 0 included).
-constexpr int kScanPer = 32;  // terms per thread, contiguous: element kScanPer * thread + i
 
 struct ScanShared {
   double s, hit_sum;  // running sum before element j0; the running sum at the hit
@@ -924,10 +947,45 @@ struct ScanShared {
   int wbad[kThreads / kWave], whit[kThreads / kWave];
 };
 
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
-  return v;
+// Wave-wide unsigned minimum through DPP, on every lane.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_self_min(uint32_t v) {
+  return min(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL,
+                                                                   ROW_MASK, 0xF, false)));
+}
+__device__ __forceinline__ int wave_min_dpp(int v) {  // v >= 0
+  uint32_t u = static_cast<uint32_t>(v);
+  u = dpp_self_min<0xB1>(u);
+  u = dpp_self_min<0x4E>(u);
+  u = dpp_self_min<0x141>(u);
+  u = dpp_self_min<0x140>(u);
+  u = dpp_self_min<0x142, 0xA>(u);
+  u = dpp_self_min<0x143, 0xC>(u);
+  return __builtin_amdgcn_readlane(static_cast<int>(u), 63);
+}
+
+// A double moved by a DPP control; lanes without a source (or outside row_mask) read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_zero_d(double v) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b)), CTRL, ROW_MASK, 0xF, true));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b >> 32)), CTRL, ROW_MASK, 0xF, true));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Exclusive prefix sum over the wave's lanes (lane 0 gets 0): the lanes shifted by one, then an
+// inclusive scan by DPP row shifts and row broadcasts.  A lane's prefix adds only lanes below it.
+__device__ __forceinline__ double wave_excl_scan_dpp(double v) {
+  double x = dpp_zero_d<0x138>(v);  // wave_shr:1
+  x += dpp_zero_d<0x111>(x);        // row_shr:1
+  x += dpp_zero_d<0x112>(x);        // row_shr:2
+  x += dpp_zero_d<0x114>(x);        // row_shr:4
+  x += dpp_zero_d<0x118>(x);        // row_shr:8
+  x += dpp_zero_d<0x142, 0xA>(x);   // row_bcast:15 into rows 1 and 3
+  x += dpp_zero_d<0x143, 0xC>(x);   // row_bcast:31 into rows 2 and 3
+  return x;
 }
 
 __device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -974,30 +1032,35 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
       const double M0 = ldexp(s, sc);
       const bool mine = base + kScanPer > j0 && base < n;
       double T = 0.0;
+      bool tie = false;
       if (mine) {
 #pragma unroll
         for (int i = 0; i < kScanPer; ++i) {
           const int j = base + i;
-          if (j >= j0 && j < n) T += rint(ldexp(t[i], sc));
+          if (j >= j0 && j < n) {
+            const double y = ldexp(t[i], sc), k = rint(y);
+            T += k;
+            tie = tie || fabs(y - k) == 0.5;
+          }
         }
       }
-      // exclusive prefix of the thread totals: lanes below this one, then the waves below
-      // (a thread after the first inexact step may hold huge totals; they never enter the
-      // prefix of a thread before it)
-      double incl = T;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const double y = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += y;
-      }
-      double K = __shfl_up(incl, 1, kWave);
-      if (lane == 0) K = 0.0;
-      if (lane == kWave - 1) sh.wsum[wave] = incl;
+      // exclusive prefix of the thread totals: lanes below this one, then the waves below (a
+      // thread after the first inexact step may hold huge totals; they never enter the prefix of
+      // a thread before it)
+      double K = wave_excl_scan_dpp(T);
+      if (lane == kWave - 1) sh.wsum[wave] = K + T;
       __syncthreads();
       for (int w = 0; w < wave; ++w) K += sh.wsum[w];
+      // Only a thread that may hold the first inexact step or the first hit walks its terms.  A
+      // step that leaves the binade without a tie has s_{j-1} / u + k_j >= 2^53 (its k_j rounds
+      // t_j / u up past the boundary or t_j already reaches it), so a tie-free thread whose last
+      // running sum is below 2^(e+1) has only exact steps; the running sums rise, so the last one
+      // decides whether any step of the thread meets the predicate.
       int my_bad = n, my_hit = n;
       double my_hs = 0.0, Kb = 0.0;
-      if (mine) {
+      const double M_end = M0 + K + T;
+      const bool walk = mine && (tie || !(M_end < 0x1p53) || (MODE != 0 && pred(ldexp(M_end, -sc))));
+      if (walk) {
         bool stop = false;
 #pragma unroll
         for (int i = 0; i < kScanPer; ++i) {
@@ -1022,7 +1085,7 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
           }
         }
       }
-      const int wb = wave_min_i(my_bad), wh = wave_min_i(my_hit);
+      const int wb = wave_min_dpp(my_bad), wh = wave_min_dpp(my_hit);
       if (lane == 0) {
         sh.wbad[wave] = wb;
         sh.whit[wave] = wh;
@@ -1086,13 +1149,14 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
 __device__ void sample_tail_scan(const SampleArgs& a, int b, const uint64_t* sorted, int keep, ScanShared& sh,
                                  int& s_flag) {
   const int tid = threadIdx.x, base = tid * kScanPer;
-  const float mx = key_value(sorted[0]);
+  const double* p = prob_of(a, b);  // the sorted softmax terms, written by rank_merge_kernel
+  const int cols = (a.vocab + kScanPer - 1) / kScanPer;
   double t[kScanPer];
   bool finite = true;
 #pragma unroll
   for (int i = 0; i < kScanPer; ++i) {
     const int j = base + i;
-    t[i] = j < keep ? exp(static_cast<double>(key_value(sorted[j]) - mx)) : 0.0;
+    t[i] = j < keep ? p[i * cols + tid] : 0.0;
     finite = finite && isfinite(t[i]);
   }
   if (tid == 0) s_flag = 0;
@@ -1160,7 +1224,7 @@ size_t sample_workspace_stride(int vocab) {
   size_t n2 = 1;
   while (n2 < static_cast<size_t>(vocab)) n2 <<= 1;
   const size_t v = static_cast<size_t>(vocab);
-  return ((v * 4 + 255) & ~size_t{255}) + ((v * 8 + 255) & ~size_t{255}) + 2 * ((n2 * 8 + 255) & ~size_t{255});
+  return ((v * 4 + 255) & ~size_t{255}) + prob_region_bytes(v) + 2 * ((n2 * 8 + 255) & ~size_t{255});
 }
 
 int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t s) {
