@@ -188,3 +188,27 @@ def test_sampler_full_sort_sums(hip, layout, top_p):
                    hist_len=hip.DeviceArray.from_host(np.zeros(batch, np.int32)), hist_ld=1, rng=rng)
         want = [cpu[b].sample(logits[b], []) for b in range(batch)]
         assert [int(v) for v in out.numpy()] == want, (layout, top_p, step)
+
+
+@pytest.mark.parametrize("V,top_k,top_p", [(40000, 0, 0.9), (40000, 2000, 0.95), (50000, 30000, 1.0), (5000, 0, 0.9),
+                                           (32768, 0, 0.8), (33, 0, 0.5)])
+def test_sampler_other_vocab_sizes(hip, V, top_k, top_p):
+    """Vocabularies other than TinyLlama's: above the 32768 ids the parallel sums take (the
+    sequential fallback), top-k above the LDS path with a large vocabulary (the parallel sums over
+    k ids), and small ones (src/sampler.cpp:13-70)."""
+    batch = 3
+    print(f"[case] sampler V={V} top_k={top_k} top_p={top_p}", flush=True)
+    g = D.rng(V + top_k)
+    cfg = dict(temperature=0.9, top_k=top_k, top_p=top_p, repetition_penalty=1.2)
+    seeds = [5 + b for b in range(batch)]
+    rng = hip.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    ws = hip.DeviceArray((EL.lib().ef_hip_sample_workspace_bytes(V, batch),), np.uint8)
+    out = hip.DeviceArray((batch,), np.int32)
+    for step in range(3):
+        logits = (g.standard_normal((batch, V), dtype=np.float32) * np.float32(2.0 + step)).astype(np.float32)
+        hist = g.integers(0, V, size=(batch, 16)).astype(np.int32)
+        hip.sample(hip.DeviceArray.from_host(logits), V, cfg, out, batch=batch, hist=hip.DeviceArray.from_host(hist),
+                   hist_len=hip.DeviceArray.from_host(np.full(batch, 16, np.int32)), hist_ld=16, rng=rng, ws=ws)
+        want = [cpu[b].sample(logits[b], hist[b]) for b in range(batch)]
+        assert [int(v) for v in out.numpy()] == want, (V, top_k, top_p, step)
