@@ -887,6 +887,52 @@ __global__ __launch_bounds__(kThreads) void chunk_sort_kernel(SampleArgs a) {
   bitonic_global(keys_of(a, blockIdx.y) + static_cast<size_t>(blockIdx.x) * kChunk, kChunk, s_keys);
 }
 
+// The same runs with their keys formed here (no key-writing launch before): workgroup r takes ids
+// kChunk r .. kChunk r + kChunk - 1, applies the repetition penalty to those of them in the history
+// (each once) and the temperature, exactly as sample_kernel does (src/sampler.cpp:16-27), forms
+// the keys in registers (ids past the vocabulary get key 0, below every key), sorts them and
+// stores the run.
+__global__ __launch_bounds__(kThreads) void key_sort_kernel(SampleArgs a) {
+  __shared__ uint64_t s_keys[2 * kChunk];
+  __shared__ uint32_t s_seen[kChunk / 32];
+  const int b = blockIdx.y, t = threadIdx.x, base = blockIdx.x * kChunk, V = a.vocab;
+  const float* lg = a.logits + b * a.ld;
+  float v[kKeysPerThread];
+#pragma unroll
+  for (int u = 0; u < kKeysPerThread; ++u) {
+    const int id = base + t + kThreads * u;
+    v[u] = id < V ? lg[id] : 0.0f;
+  }
+  if (a.penalty != 1.0f) {
+    for (int i = t; i < kChunk / 32; i += kThreads) s_seen[i] = 0u;
+    __syncthreads();
+    const int n = a.hist_len[b];
+    const int32_t* h = a.hist + b * a.hist_ld;
+    for (int i = t; i < n; i += kThreads) {
+      const int id = h[i] - base;
+      if (h[i] >= 0 && h[i] < V && id >= 0 && id < kChunk) atomicOr(&s_seen[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kKeysPerThread; ++u) {
+      const int id = t + kThreads * u;
+      if (base + id < V && (s_seen[id >> 5] >> (id & 31) & 1u))
+        v[u] = v[u] > 0.0f ? __fdiv_rn(v[u], a.penalty) : v[u] * a.penalty;
+    }
+  }
+  uint64_t x[kKeysPerThread];
+#pragma unroll
+  for (int u = 0; u < kKeysPerThread; ++u) {
+    const int id = base + t + kThreads * u;
+    x[u] = id < V ? make_key(__fdiv_rn(v[u], a.temperature), static_cast<uint32_t>(id)) : 0ull;
+  }
+  int parity = 0;
+  for (int k = 2; k <= kChunk; k <<= 1) chunk_steps(x, 0, k, k >> 1, s_keys, parity);
+  uint64_t* g = keys_of(a, b) + base;
+#pragma unroll
+  for (int u = 0; u < kKeysPerThread; ++u) g[t + kThreads * u] = x[u];
+}
+
 // The sorted runs merged in one pass: key i of run r goes to i + (keys of every run r' < r that are
 // >= it) + (keys of every run r' > r that are > it), counted by binary search in each descending run:
 // the runs' ties resolve by run index, so the positions are a permutation and the result is the
@@ -1283,8 +1329,12 @@ int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_h
   const bool topk_lds = cfg.top_k > 0 && cfg.top_k < vocab && cfg.top_k <= kMaxTopK;
   if (cfg.temperature > 0.0f && !topk_lds && n2 >= 2 * kChunk) {
     a.phase = 1;
-    hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
-    hipLaunchKernelGGL(chunk_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
+    if (eos_p != nullptr) {  // P(eos) needs the whole vocabulary: the one-workgroup key launch
+      hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL(chunk_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL(key_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
+    }
     hipLaunchKernelGGL(rank_merge_kernel, dim3(n2 / 256, batch), dim3(256), 0, s, a);
     const int keep = cfg.top_k > 0 && cfg.top_k < vocab ? cfg.top_k : vocab;
     if (keep <= kThreads * kScanPer) {
