@@ -986,7 +986,12 @@ __global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
 // add by the thread that holds its term, and the next round starts after it in its binade.  A sum
 // that passes through b binades takes about b + 1 rounds (the one-term start from 0 included).
 
+// The first kScanHead terms are added one by one (thread 0, from LDS) before the rounds: a sum
+// crosses most of its binades within its largest terms, where each crossing would cost a round.
+constexpr int kScanHead = 256;
+
 struct ScanShared {
+  double head[kScanHead];
   double s, hit_sum;  // running sum before element j0; the running sum at the hit
   int j0, hit, done;
   double wsum[kThreads / kWave];
@@ -1056,11 +1061,54 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * kScanPer;
   constexpr int kW = kThreads / kWave;
   auto pred = [&](double s) { return MODE == 1 ? s >= x : (MODE == 2 ? x < s : false); };
-  if (tid == 0) {
-    sh.s = 0.0;
-    sh.j0 = 0;
-    sh.hit = n;
-    sh.done = n == 0;
+  const int nh = min(n, kScanHead);
+  if (base < nh) {
+#pragma unroll
+    for (int i = 0; i < kScanPer; ++i)
+      if (base + i < nh) sh.head[base + i] = t[i];
+  }
+  __syncthreads();
+  if (tid == 0) {  // the head, term by term as the reference adds them
+    // groups of eight: the next group's LDS reads issued before this group's chain of adds, the
+    // running sums read off the chain for the predicate (terms past the head are exact zeros,
+    // which leave a nonnegative sum unchanged)
+    double s = 0.0, hs = 0.0;
+    int hit = n;
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = u < nh ? sh.head[u] : 0.0;
+    for (int j = 0; j < nh; j += 8) {
+      double w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = j + 8 + u < nh ? sh.head[j + 8 + u] : 0.0;
+      double c[8], x = s;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        x = x + v[u];
+        c[u] = x;
+      }
+      if (MODE != 0) {
+        int h = -1;
+#pragma unroll
+        for (int u = 7; u >= 0; --u)
+          if (j + u < nh && pred(c[u])) h = u;
+        if (h >= 0) {
+          hit = j + h;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (u == h) hs = c[u];
+          break;
+        }
+      }
+      s = x;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = w[u];
+    }
+    sh.s = s;
+    sh.hit_sum = hs;
+    sh.hit = hit;
+    sh.j0 = nh;
+    sh.done = hit < n || nh >= n;
   }
   for (int round = 0; round <= n + 1; ++round) {
     __syncthreads();
