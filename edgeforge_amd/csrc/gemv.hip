@@ -614,18 +614,29 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   int nw = ov.waves > 0 ? ov.waves : 4;
   bool use_dma = fast && ov.path != 2 && dma_layout(G, 1, nw, nullptr) <= kDmaLdsTarget;
   if (!use_dma) nw = kWaves;
-  // rows per tile: nw waves x (64/G) groups x R rows; R as large as keeps >= 2 tiles per CU
+  // rows per tile: nw waves x (64/G) groups x R rows.  Register path: R as large as keeps >= 2
+  // tiles per CU.  DMA path: the R that gives the busiest CU the fewest rows (rounds of tiles over
+  // the CUs x rows per tile), the larger R on a tie (fewer workgroups re-stage x).  q/k/v (2560
+  // rows) takes R = 2, 160 tiles of 16 rows, instead of 320 tiles of 8 (64 CUs with two): 90.1 ->
+  // 86 us per B = 1 step; lm_head keeps R = 2 (R = 1: 17.8 -> 20.5 us).
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
   int R = 1;
   if (fast) {
-    for (int cand : {4, 2}) {
+    size_t best = 0;
+    for (int cand : {1, 2, 4}) {
       const size_t per_tile = static_cast<size_t>(nw * (kWave / G) * cand);
       size_t tiles = 0;
       for (int j = 0; j < n_jobs; ++j) tiles += (jobs[j].W->rows + per_tile - 1) / per_tile;
-      if (tiles * static_cast<size_t>(batch) >= static_cast<size_t>(2 * cus) &&
-          (!use_dma || dma_layout(G, cand, nw, nullptr) <= kDmaLdsTarget)) {
+      tiles *= static_cast<size_t>(batch);
+      if (!use_dma) {
+        if (cand == 1 || tiles >= static_cast<size_t>(2 * cus)) R = cand;
+        continue;
+      }
+      if (cand > 1 && dma_layout(G, cand, nw, nullptr) > kDmaLdsTarget) continue;
+      const size_t busiest = (tiles + cus - 1) / cus * per_tile;
+      if (best == 0 || busiest <= best) {
+        best = busiest;
         R = cand;
-        break;
       }
     }
   }
