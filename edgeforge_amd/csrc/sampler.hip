@@ -934,28 +934,80 @@ __global__ __launch_bounds__(kThreads) void key_sort_kernel(SampleArgs a) {
 }
 
 // The sorted runs merged in one pass: key i of run r goes to i + (keys of every run r' < r that are
-// >= it) + (keys of every run r' > r that are > it), counted by binary search in each descending run:
-// the runs' ties resolve by run index, so the positions are a permutation and the result is the
-// descending order.
-__global__ __launch_bounds__(256) void rank_merge_kernel(SampleArgs a) {
+// >= it) + (keys of every run r' > r that are > it): the runs' ties resolve by run index, so the
+// positions are a permutation and the result is the descending order.  A workgroup's 256 keys are
+// consecutive in one run, so in every other run the keys that fall between its first and its last
+// key form one window: two binary searches in global memory per run bound it, the windows are
+// copied to LDS with coalesced loads, and each key counts its place inside them in LDS.  A window
+// that does not fit is searched in global memory as a whole.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeWindow = 3072;  // keys of all windows held in LDS (24 KB; typically 7 x ~256 are used)
+constexpr int kMaxRuns = 64;        // runs of kChunk keys: vocabularies up to 262144
+
+__global__ __launch_bounds__(kMergeThreads) void rank_merge_kernel(SampleArgs a) {
+  __shared__ uint64_t s_win[kMergeWindow];
+  __shared__ int s_lo[kMaxRuns], s_hi[kMaxRuns], s_off[kMaxRuns];
   const uint64_t* keys = keys_of(a, blockIdx.y);
   uint64_t* out = merged_of(a, blockIdx.y);
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= a.npow2) return;
-  const int runs = a.npow2 / kChunk, r = e / kChunk;
+  const int t = threadIdx.x, e0 = blockIdx.x * kMergeThreads, e = e0 + t;
+  const int runs = a.npow2 / kChunk, r = e0 / kChunk;
+  // keys before a key y in run q: q < r counts keys >= y, q > r keys > y (descending runs)
+  auto count_before = [&](const uint64_t* run, int q, uint64_t y) {
+    int lo = 0, hi = kChunk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const bool before = q < r ? run[mid] >= y : run[mid] > y;
+      if (before) lo = mid + 1;
+      else hi = mid;
+    }
+    return lo;
+  };
+  const bool windows = runs <= kMaxRuns;  // more runs: every search in global memory
+  if (windows && t < runs && t != r) {  // run t's window: the counts of the slice's largest and smallest key
+    const uint64_t* run = keys + static_cast<size_t>(t) * kChunk;
+    s_lo[t] = count_before(run, t, keys[e0]);
+    s_hi[t] = count_before(run, t, keys[e0 + kMergeThreads - 1]);
+  }
+  __syncthreads();
+  if (windows && t == 0) {  // LDS offsets of the windows that fit, in run order; -1: global search
+    int off = 0;
+    for (int q = 0; q < runs; ++q) {
+      s_off[q] = -1;
+      if (q == r) continue;
+      const int w = s_hi[q] - s_lo[q];
+      if (off + w <= kMergeWindow) {
+        s_off[q] = off;
+        off += w;
+      }
+    }
+  }
+  __syncthreads();
+  if (windows) {
+    for (int q = 0; q < runs; ++q) {
+      if (q == r || s_off[q] < 0) continue;
+      const uint64_t* run = keys + static_cast<size_t>(q) * kChunk + s_lo[q];
+      uint64_t* w = s_win + s_off[q];
+      for (int i = t; i < s_hi[q] - s_lo[q]; i += kMergeThreads) w[i] = run[i];
+    }
+  }
+  __syncthreads();
   const uint64_t x = keys[e];
   int pos = e - r * kChunk;
   for (int q = 0; q < runs; ++q) {
     if (q == r) continue;
-    const uint64_t* run = keys + static_cast<size_t>(q) * kChunk;
-    int lo = 0, hi = kChunk;  // first index whose key is below x (q < r) or not above x (q > r)
+    if (!windows || s_off[q] < 0) {
+      pos += count_before(keys + static_cast<size_t>(q) * kChunk, q, x);
+      continue;
+    }
+    const uint64_t* w = s_win + s_off[q];
+    int lo = 0, hi = s_hi[q] - s_lo[q];
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      const bool before = q < r ? run[mid] >= x : run[mid] > x;
+      const bool before = q < r ? w[mid] >= x : w[mid] > x;
       if (before) lo = mid + 1;
       else hi = mid;
     }
-    pos += lo;
+    pos += s_lo[q] + lo;
   }
   out[pos] = x;
   // the softmax term of the key at its sorted position, exp(double(v - max)) as the reference
@@ -1383,7 +1435,7 @@ int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_h
     } else {
       hipLaunchKernelGGL(key_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
     }
-    hipLaunchKernelGGL(rank_merge_kernel, dim3(n2 / 256, batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(rank_merge_kernel, dim3(n2 / kMergeThreads, batch), dim3(kMergeThreads), 0, s, a);
     const int keep = cfg.top_k > 0 && cfg.top_k < vocab ? cfg.top_k : vocab;
     if (keep <= kThreads * kScanPer) {
       hipLaunchKernelGGL(sample_scan_kernel, dim3(batch), dim3(kThreads), 0, s, a);
