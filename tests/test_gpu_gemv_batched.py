@@ -57,9 +57,11 @@ def test_batched_gemv_each_sequence_meets_the_gates(hip, qtype, rows, cols, batc
     assert np.array_equal(dy.numpy().view(np.uint32), got.view(np.uint32))  # reproducible bits
 
 
-def test_batched_swiglu_and_residual_chain(hip):
-    """Transformer::forward's FFN chain (src/model.cpp:249-262) for 64 sequences at once."""
-    B, D_, F = 64, 2048, 5632
+@pytest.mark.parametrize("B", [64, 300])  # 300: the many-sequence kernel (a batched prefill's shape)
+def test_batched_swiglu_and_residual_chain(hip, B):
+    """Transformer::forward's FFN chain (src/model.cpp:249-262) for 64 and 300 sequences at once."""
+    print(f"[case] ffn chain B={B}", flush=True)
+    D_, F = 2048, 5632
     X = np.stack([D.normal(40 + b, D_) for b in range(B)]).astype(np.float32)
     nw = (1.0 + 0.1 * D.normal(41, D_)).astype(np.float32)
     g = O.quantize(O.Q4_0, D.normal(42, (F, D_), 0.02))
@@ -74,7 +76,7 @@ def test_batched_swiglu_and_residual_chain(hip):
     hip.matvec_residual(Dn, dact, dx, batch=B)  # K = 5632 at B = 64: split-K with a finalize pass
     got_act, got = dact.numpy(), dx.numpy()
     L = O.lib()
-    for b in range(0, B, 9):
+    for b in list(range(0, B, 9)) + [B - 1]:
         h = np.empty(D_, np.float32)
         L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), D_, 1e-5)
         gate, up = O.matvec_jobs([(O.Q4_0, g, h), (O.Q4_0, u, h)])
@@ -85,9 +87,11 @@ def test_batched_swiglu_and_residual_chain(hip):
         assert np.abs(got[b] - ref).max() <= ABS_TOL, b
 
 
-def test_batched_mixed_type_jobs_with_norm(hip):
-    """q/k/v with k, v stored Q8_0 in one launch for 8 sequences, input RMSNorm fused."""
-    B, cols = 8, 2048
+@pytest.mark.parametrize("B", [8, 270])
+def test_batched_mixed_type_jobs_with_norm(hip, B):
+    """q/k/v with k, v stored Q8_0 in one launch for 8 and 270 sequences, input RMSNorm fused."""
+    print(f"[case] mixed q/k/v B={B}", flush=True)
+    cols = 2048
     X = np.stack([D.normal(60 + b, cols) for b in range(B)]).astype(np.float32)
     nw = (1.0 + 0.05 * D.normal(61, cols)).astype(np.float32)
     shapes = [(O.Q4_0, 2048), (O.Q8_0, 256), (O.Q8_0, 256)]
@@ -101,7 +105,7 @@ def test_batched_mixed_type_jobs_with_norm(hip):
     hip.matvec_jobs_rmsnorm([(ws[i], dx, outs[i]) for i in range(3)], hip.DeviceArray.from_host(nw), 1e-5, batch=B,
                             ldx=cols, ldy=2048)
     L = O.lib()
-    for b in range(B):
+    for b in range(0, B, 1 if B <= 16 else 7):
         h = np.empty(cols, np.float32)
         L.efo_rmsnorm(O.ptr(h, O._f32p), O.ptr(X[b], O._f32p), O.ptr(nw, O._f32p), cols, 1e-5)
         for i, (qt, rows) in enumerate(shapes):
