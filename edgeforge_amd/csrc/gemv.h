@@ -46,6 +46,12 @@ int refresh_tiled(const ef_hip_weight_s* w, hipStream_t s);
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken);
 
+// Batched products over K = 2048 that read the packed rows in place, in one launch with no
+// workspace (gemv_batch.hip).  Sets *taken when it enqueued the launch; otherwise the caller takes
+// another path.
+int launch_gemv_batch(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch,
+                      size_t ldx, size_t ldy, hipStream_t stream, bool* taken);
+
 // Block-scaled A tables of the matrix-core GEMV, staged by the kernel that produces its input
 // (or by launch_stage_tables): t4 / t8 in the Q4_0 / Q8_0 column orders
 // ([sequence tile][block][hi, lo][64 lanes][16 B], stage_table_bytes each), a power-of-two scale

@@ -574,6 +574,8 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     }
   }
   bool taken = false;
+  EFH_RC(launch_gemv_batch(jobs, n_jobs, epi, norm_w, eps, batch, ldx, ldy, stream, &taken));
+  if (taken) return EF_HIP_OK;
   EFH_RC(launch_gemv_mfma(jobs, n_jobs, epi, norm_w, eps, batch, ldx, ldy, ws, ws_bytes, stream, &taken));
   if (taken) return EF_HIP_OK;
   Args a{};

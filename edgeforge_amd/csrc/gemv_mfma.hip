@@ -46,6 +46,7 @@
 
 #include "afrag.h"
 #include "gemv.h"
+#include "qfrag.h"
 
 namespace efh {
 namespace {
@@ -63,8 +64,6 @@ constexpr int kPrepBlocks = kTP / kWave;        // blocks per xfrag workgroup: o
 // tiles: a whole K of up to 6144 without a split), 8 otherwise (more unrolled blocks would spill)
 __host__ __device__ constexpr int max_blocks_per_wave(int rt, int nm, int ns) { return rt * nm * ns <= 2 ? 24 : 8; }
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 struct MJob {
@@ -129,45 +128,6 @@ __device__ __forceinline__ void dma_copy(__amdgpu_buffer_rsrc_t r, uint32_t src_
 
 __device__ __forceinline__ float f16lo(uint32_t v) { return half_bits_to_float(v & 0xFFFFu); }
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-// (v & mask) | fp16(1024) pattern in both halves, minus (1024 + bias) in both halves: exact.  The
-// mask comes in a scalar register and the pattern in a vector register, so that the AND-OR is one
-// v_and_or_b32 (its three-operand encoding takes no literal constants).
-__device__ __forceinline__ uint32_t codes2(uint32_t v, uint32_t mask, _Float16 minus) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(mask);
-  uint32_t pat = 0x64006400u, r;
-  asm("" : "+v"(pat));  // keep the pattern in a register
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(pat));
-  h2 h;
-  __builtin_memcpy(&h, &r, 4);
-  const h2 c = {minus, minus};
-  h = h + c;
-  __builtin_memcpy(&r, &h, 4);
-  return r;
-}
-
-__device__ __forceinline__ h8 q4_operand(uint32_t q) {
-  const uint32_t s = q >> 8;
-  const _Float16 lo = static_cast<_Float16>(-1032.0f), hi = static_cast<_Float16>(-1152.0f);
-  const uint32_t w[4] = {codes2(q, 0x000F000Fu, lo), codes2(q, 0x00F000F0u, hi), codes2(s, 0x000F000Fu, lo),
-                         codes2(s, 0x00F000F0u, hi)};
-  h8 r;
-  __builtin_memcpy(&r, w, 16);
-  return r;
-}
-
-__device__ __forceinline__ h8 q8_operand(uint32_t q0, uint32_t q1) {
-  const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
-  const _Float16 m = static_cast<_Float16>(-1152.0f);
-  const uint32_t w[4] = {codes2(u0, 0x00FF00FFu, m), codes2(u0 >> 8, 0x00FF00FFu, m), codes2(u1, 0x00FF00FFu, m),
-                         codes2(u1 >> 8, 0x00FF00FFu, m)};
-  h8 r;
-  __builtin_memcpy(&r, w, 16);
-  return r;
-}
-
-__device__ __forceinline__ float silu_m(float g) { return g / (1.0f + expf(-g)); }  // src/kernels.cpp:94
 
 // grid (ceil(nb / 16), tiles): workgroup (x, t) prepares sequences 16 t .. 16 t + 15 for blocks
 // 16 x .. 16 x + 15.  Every workgroup of a tile recomputes the tile's per-sequence factors (a read of
