@@ -6,38 +6,38 @@
 // of one matrix, and is the only workgroup computing those outputs.  The workgroups of one row run
 // get ids of one residue mod 8, which the dispatcher places on one XCD, so each weight byte comes
 // from HBM once and the run's sequence groups share it through that XCD's L2.  B = 64 over 5632 rows
-// is 64 runs of 5 or 6 tiles x 4 sequence groups: 256 workgroups, one per CU.
+// is 64 runs of 5 or 6 tiles x 4 sequence groups: 256 workgroups, one per CU.  Wave w owns the K
+// blocks [8w, 8w + 8) of every tile and works alone until the final combine: it has a private LDS
+// region, its own per-sequence scale, and no workgroup barrier before the combine.
 //
-// Activations (A operand of v_mfma_f32_16x16x32_f16, 16 sequences x 32 weights).  Wave w owns the
-// K blocks [8w, 8w + 8).  At entry it loads those blocks of its sequences' FP32 rows (and of the
-// RMSNorm weights) straight into registers; the workgroup reduces each sequence's statistics
-// through LDS (double sum of squares for kern::rmsnorm, max |x|); then the wave forms its fragments
-// once: v = norm_w * (x * inv) (HF order, src/kernels.cpp:69-75) or x, times a per-sequence power of
-// two keeping |v'| < 2^15, split exactly into fp16 hi + lo (v' - hi - lo is below 2^-22 |v'|).  They
-// stay in 64 VGPRs for the whole launch, shared by every row tile.  Lane l holds sequence l % 16
-// and 8 values of lane group g = l / 16, in the slot order of its codes (below).
+// Activations (A operand of v_mfma_f32_16x16x32_f16, 16 sequences x 32 weights).  The wave fetches
+// its K range of its 16 sequences' FP32 rows (and of the RMSNorm weights) with LDS-DMA, one 1 KB
+// row piece per instruction, reads its fragment values back (lane l: sequence l % 16, lane group
+// g = l / 16), takes v = norm_w * x (or x), scales by a power of two keeping |v'| < 2^15 (from the
+// maximum over its own range) and splits v' exactly into fp16 hi + lo (v' - hi - lo below
+// 2^-22 |v'|), two fused mixed-precision instructions per value.  The fragments stay in 64 VGPRs
+// for the whole launch, shared by every row tile.  1 / rms (kern::rmsnorm's statistic, a double sum
+// of x^2 combined over the waves) scales the results in the epilogue.
 //
-// Weights (B operand, 32 weights x 16 rows).  A tile's 16 rows are 16 x row_bytes contiguous bytes
-// of the packed matrix (Q4_0 1152, Q8_0 2176 per row).  The 8 waves fetch them two rows each with
-// coalesced 16-byte lane loads into registers, two tiles ahead of the tile being computed, and
-// write them into one of two LDS slots with rows an odd number of 16-byte units apart (the 16 rows
-// one B fragment reads fall in distinct banks).  Per block pair of its range (36 / 68 bytes, 4-byte
-// aligned), lane (row n = l % 16, group g) then reads aligned dwords of row n:
+// Weights (B operand, 32 weights x 16 rows).  The wave fetches its K range of each tile's 16 rows
+// (9 / 17 coalesced 16-byte pieces per row for Q4_0 / Q8_0) into registers, the first tiles at
+// entry, and writes each tile into one of two LDS slots before computing it, rows an odd number of
+// 16-byte units apart (the 16 rows one B fragment reads fall in distinct banks).  Lane (row
+// n = l % 16, group g) then reads aligned dwords of row n per block pair (36 / 68 bytes):
 //   Q4_0 pair (dwords 0..8): dw0 = d | c0 c1, dw1..dw3 = c2..c13, dw4 = c14 c15 | d', dw5..dw8 = c'0..c'15.
-//     Odd block: lane group g takes dw(5 + g), bytes c'4g .. c'4g+3.
-//     Even block: g >= 1 takes dw(g), bytes c(4g-2) .. c(4g+1); g = 0 takes c0 c1 c14 c15, one
-//     v_perm of dw0 and dw4.  The scales are the low half of dw0 and the high half of dw4.
-//   Q8_0 pair (dwords 0..16): dw0 = d | q0 q1, dw1..dw7 = q2..q29, dw8 = q30 q31 | d', dw9..dw16 = q'0..q'31.
-//     Odd block: g takes dw(9 + 2g), dw(10 + 2g).  Even block: g >= 1 takes dw(2g), dw(2g + 1);
-//     g = 0 takes q0 q1 q30 q31 (v_perm of dw0 and dw8) and dw1.
-// The A operands follow the same code order per block parity (a_offsets), so no bytes are shuffled
-// beyond that one v_perm per pair.  Codes become exact fp16 B operands (qfrag.h); D = A_hi B, then
-// D += A_lo B through the accumulator input, and d D enters an FP32 accumulator per output.
+//     Even block: bytes c4g .. c4g+3 = alignbyte(dw(g+1), dw(g), 2).  Odd block: dw(5 + g).
+//   Q8_0 pair (dwords 0..16): dw0 = d | q0 q1, dw1..dw8 = q2..q31 | d', dw9..dw16 = q'0..q'31.
+//     Even block: q8g .. q8g+7 from dw(2g) .. dw(2g+2) by two alignbytes.  Odd block: dw(9+2g), dw(10+2g).
+//   The scales are the low half of dw0 and the high half of dw4 (dw8).
+// Lane group g takes the codes of weights 4g..4g+3 and 16+4g..19+4g (Q4_0) or 8g..8g+7 (Q8_0), the
+// slot orders of qfrag.h, and the A fragments follow the same order.  Per block pair the products
+// run software-pipelined: D = A_hi B, D += A_lo B through the accumulator input, and d D enters an
+// FP32 accumulator per output, while the next pair's codes become B operands.
 //
-// Combine.  Each wave's sums cover its K range; after the last tile the 8 partials of every output
-// are added through LDS in wave order (a fixed order: same bits every call, for any batch), the
-// per-sequence power of two undone and the epilogue applied (store, residual add, SwiGLU of a
-// gate and an up matrix).
+// Combine.  Each wave's sums cover its K range; after the last tile every wave multiplies them by
+// its power of two and the 8 partials of every output are added through LDS in wave order (a fixed
+// order: same bits every call, for any batch); then 1 / rms (norm) and the epilogue (store, residual
+// add, SwiGLU of a gate and an up matrix).
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -49,13 +49,9 @@
 namespace efh {
 namespace {
 
-constexpr int kGT = 512;            // threads per workgroup
-constexpr int kGW = kGT / kWave;    // waves
 constexpr int kGMaxTiles = 6;       // row tiles (16 rows) per workgroup
-constexpr int kGNBW = 8;            // K blocks per wave
-constexpr int kGK = kGW * kGNBW * 32;  // the K this kernel serves: 2048
+constexpr int kGK = 2048;           // the K this kernel serves
 constexpr int kGMaxJobs = 4;
-constexpr int kGRedBytes = kGW * kGMaxTiles * kWave * 16;  // the waves' partial sums, per matrix
 
 template <bool Q4>
 struct QShape {
@@ -100,45 +96,56 @@ __device__ __forceinline__ void split2(float v0, float v1, float s, uint32_t& hi
       : "v"(v0), "v"(v1), "v"(s));
 }
 
-// Each wave owns a private LDS region: first its 16 activation rows of its K range (1 KB each,
-// 1040 bytes apart so that the 16 rows of one fragment read fall in distinct banks), then, once its
-// fragments are formed, two slots of its K range of a row tile's 16 rows (16 x 144 bytes for
-// Q4_0, 16 x 272 for Q8_0, per matrix: rows an odd number of 16-byte units apart, so the 16 rows
-// one B fragment reads fall in distinct banks again).  No wave reads another wave's region, so
-// nothing before the final combine waits for the workgroup.
-constexpr int kGARow = 1040;
-constexpr int kGAWave = 17408;  // >= 16 * kGARow and >= 2 slots of a Q8_0 SwiGLU tile (2 x 2 x 4352)
-constexpr int kGNormOff = kGW * kGAWave;
-constexpr int kGLds = kGNormOff + kGW * 1024;
-
-template <bool Q4>
-struct WShape {  // one wave's K range of a 16-row tile
-  static constexpr int kRow = kGNBW * (Q4 ? 18 : 34);         // 144 / 272 bytes
-  static constexpr int kPiecesRow = kRow / 16;                 // 9 / 17
-  static constexpr int kTile = 16 * kRow;                      // 2304 / 4352
-  static constexpr int kLoads = (16 * kPiecesRow + kWave - 1) / kWave;  // 3 / 5 lane loads
+// Workgroup shapes: NW waves split the K blocks, NBW = 64 / NW each.  Each wave owns a private LDS
+// region: first its 16 activation rows of its K range (NBW x 128 bytes each, rows an odd number of
+// 16-byte units apart so that the 16 rows of one fragment read fall in distinct banks), then, once
+// its fragments are formed, two slots of its K range of a row tile's 16 rows (per matrix; rows an
+// odd number of 16-byte units apart again).  No wave reads another wave's region, so nothing before
+// the final combine waits for the workgroup.
+template <int NW>
+struct Wg {
+  static constexpr int kT = NW * kWave;
+  static constexpr int kNBW = kGK / 32 / NW;                  // 8 (8 waves) or 4 (16 waves)
+  static constexpr int kARow = kNBW * 128 + 16;
+  static constexpr int kWRowQ8 = ((kNBW * 34 + 15) / 16) * 16;
+  static constexpr int kAWave = 16 * kARow > 2 * 2 * 16 * kWRowQ8 ? 16 * kARow : 2 * 2 * 16 * kWRowQ8;
+  static constexpr int kNormOff = NW * kAWave;
+  static constexpr int kLds = kNormOff + NW * kNBW * 128;
+  static constexpr int kRed = NW * kGMaxTiles * kWave * 16;  // the waves' partial sums, per matrix
 };
 
-// Weight tiles whose rows are requested at entry (registers): as many as 72 VGPRs hold.
-template <bool Q4, int NM>
+template <bool Q4, int NW>
+struct WShape {  // one wave's K range of a 16-row tile, whole 16-byte pieces per row
+  static constexpr int kPiecesRow = (Wg<NW>::kNBW * (Q4 ? 18 : 34) + 15) / 16;  // 9/5 (Q4_0), 17/9 (Q8_0)
+  static constexpr int kRow = kPiecesRow * 16;
+  static constexpr int kTile = 16 * kRow;
+  static constexpr int kLoads = (16 * kPiecesRow + kWave - 1) / kWave;
+};
+
+// Weight tiles whose rows are requested at entry (registers): as many as 72 VGPRs hold (two waves
+// per SIMD), 24 with four.
+template <bool Q4, int NM, int NW>
 constexpr int pre_tiles() {
-  const int per = NM * WShape<Q4>::kLoads * 4;
-  const int p = 72 / per;
+  const int per = NM * WShape<Q4, NW>::kLoads * 4;
+  const int p = (NW == 16 ? 24 : 72) / per;
   return p < 1 ? 1 : (p > kGMaxTiles ? kGMaxTiles : p);
 }
 
-template <int EPI, bool NORM, bool Q4>
+template <int EPI, bool NORM, bool Q4, int NW>
 __device__ __forceinline__ void gemv_body(const GArgs& a, const GJob& jb, int t_begin, int ntw, int sg,
                                           uint8_t* lds, float* s_postw, double* s_ss) {
   using QS = QShape<Q4>;
-  using WS = WShape<Q4>;
+  using WS = WShape<Q4, NW>;
+  using G = Wg<NW>;
   constexpr int NM = EPI == kEpiSwiglu ? 2 : 1;
-  constexpr int kPre = pre_tiles<Q4, NM>();
+  constexpr int kPre = pre_tiles<Q4, NM, NW>();
   constexpr int kSlot = NM * WS::kTile;
+  constexpr int kGNBW = G::kNBW;
+  constexpr int kGW = NW;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x & (kWave - 1);
   const int m = lane & 15, g = lane >> 4;
   const int kb0 = wave * kGNBW;
-  uint8_t* region = lds + wave * kGAWave;
+  uint8_t* region = lds + wave * G::kAWave;
 
   // ---- 1. activations: this wave's K range of its 16 sequences, one 1 KB row piece per LDS-DMA
   //      instruction (rows past the batch read zeros), and its 1 KB of norm weights
@@ -146,13 +153,18 @@ __device__ __forceinline__ void gemv_body(const GArgs& a, const GJob& jb, int t_
   const int n_valid = min(16, a.B - s_base);
   const uint32_t ldxb = static_cast<uint32_t>(a.ldx) * 4u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + static_cast<size_t>(s_base) * a.ldx, n_valid * ldxb);
+  // one instruction per row: NBW x 128 bytes = 64 (8 waves) or 32 (16 waves) lanes of 16 bytes
   const uint32_t kofs = static_cast<uint32_t>(kb0) * 128u + 16u * lane;  // byte offset in a row
+  const bool alane = lane < kGNBW * 8;
 #pragma unroll
   for (int r = 0; r < 16; ++r)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(region + r * kGARow), 16, r * ldxb + kofs, 0, 0, 0);
-  uint8_t* nbuf = lds + kGNormOff + wave * 1024;
-  if constexpr (NORM)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.norm_w, kGK * 4u), (lds_void*)nbuf, 16, kofs, 0, 0, 0);
+    if (alane)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(region + r * G::kARow), 16, r * ldxb + kofs, 0, 0, 0);
+  uint8_t* nbuf = lds + G::kNormOff + wave * (kGNBW * 128);
+  if constexpr (NORM) {
+    if (alane)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.norm_w, kGK * 4u), (lds_void*)nbuf, 16, kofs, 0, 0, 0);
+  }
 
   // ---- 2. the first kPre tiles: this wave's K range of their 16 rows (16-byte pieces, 9 / 17 per
   //      row), both matrices, into registers
@@ -188,7 +200,7 @@ __device__ __forceinline__ void gemv_body(const GArgs& a, const GJob& jb, int t_
   //      reads after LDS-DMA loads: wait here until only the weight loads issued after the DMAs
   //      are outstanding (vector-memory operations retire in order).
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPre * NM * WS::kLoads) : "memory");
-  const uint8_t* arow = region + m * kGARow;
+  const uint8_t* arow = region + m * G::kARow;
   const uint32_t p0 = Q4 ? 16u * g : 32u * g, p1 = Q4 ? 64u + 16u * g : 32u * g + 16u;
   f4v F[kGNBW][2];
 #pragma unroll
@@ -220,7 +232,7 @@ __device__ __forceinline__ void gemv_body(const GArgs& a, const GJob& jb, int t_
     ax = fmaxf(ax, __shfl_xor(ax, 32, kWave));
     if constexpr (NORM) {
       double ss = 0.0;
-      const uint8_t* xr = region + m * kGARow;
+      const uint8_t* xr = region + m * G::kARow;
 #pragma unroll
       for (int bi = 0; bi < kGNBW; ++bi)
 #pragma unroll
@@ -408,11 +420,11 @@ __device__ __forceinline__ void gemv_body(const GArgs& a, const GJob& jb, int t_
   }
 }
 
-template <int EPI, bool NORM>
-__global__ __launch_bounds__(kGT) void gemv_batch_kernel(GArgs a) {
+template <int EPI, bool NORM, int NW>
+__global__ __launch_bounds__(Wg<NW>::kT) void gemv_batch_kernel(GArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  __shared__ float s_postw[kGW * 16];
-  __shared__ double s_ss[kGW * 16];
+  __shared__ float s_postw[NW * 16];
+  __shared__ double s_ss[NW * 16];
   // workgroup -> (row run, sequence group): the runs' groups on one XCD when the launch allows it
   const int id = blockIdx.x;
   int rg, sg;
@@ -431,19 +443,25 @@ __global__ __launch_bounds__(kGT) void gemv_batch_kernel(GArgs a) {
   const int gi = rg - jb.g0;
   const int t_begin = gi * jb.tiles / jb.groups, ntw = (gi + 1) * jb.tiles / jb.groups - t_begin;
   if (jb.qtype == EF_QTYPE_Q4_0) {
-    gemv_body<EPI, NORM, true>(a, jb, t_begin, ntw, sg, lds, s_postw, s_ss);
+    gemv_body<EPI, NORM, true, NW>(a, jb, t_begin, ntw, sg, lds, s_postw, s_ss);
   } else {
-    gemv_body<EPI, NORM, false>(a, jb, t_begin, ntw, sg, lds, s_postw, s_ss);
+    gemv_body<EPI, NORM, false, NW>(a, jb, t_begin, ntw, sg, lds, s_postw, s_ss);
   }
 }
 
-template <int EPI>
+template <int EPI, int NW>
 void* batch_kernel(bool norm) {
-  return norm ? reinterpret_cast<void*>(&gemv_batch_kernel<EPI, true>)
-              : reinterpret_cast<void*>(&gemv_batch_kernel<EPI, false>);
+  return norm ? reinterpret_cast<void*>(&gemv_batch_kernel<EPI, true, NW>)
+              : reinterpret_cast<void*>(&gemv_batch_kernel<EPI, false, NW>);
 }
 
-size_t batch_lds(int nm) { return std::max<size_t>(static_cast<size_t>(nm) * kGRedBytes, kGLds); }
+template <int NW>
+size_t batch_lds(int nm) { return std::max<size_t>(static_cast<size_t>(nm) * Wg<NW>::kRed, Wg<NW>::kLds); }
+
+// Waves per workgroup.  Sixteen waves of 4 K blocks measured slower than eight of 8 on the B = 64
+// 5632 x 2048 product (12.4 against 12.0 us): the activations still arrive wave rank by wave rank,
+// and a wave's tile loop takes about as long with half the blocks.
+constexpr int kNW = 8;
 
 // EF_HIP_BGEMV=0 leaves batched products to the tile-order kernel (gemv_mfma.hip).
 bool batch_disabled() {
@@ -472,7 +490,7 @@ int launch_gemv_batch(const GemvJob* jobs, int n_jobs, int epi, const float* nor
   if (norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 != 0) return EF_HIP_OK;
   if (static_cast<size_t>(std::min(batch, 16)) * xld * 4 >= (size_t(1) << 31)) return EF_HIP_OK;
   const int nm = epi == kEpiSwiglu ? 2 : 1;
-  const size_t lds = batch_lds(nm);
+  const size_t lds = batch_lds<kNW>(nm);
   const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
   if (lds > lim) return EF_HIP_OK;
   // Row runs: as many as give every CU one workgroup (CUs / sequence groups), at most 6 tiles
@@ -487,6 +505,10 @@ int launch_gemv_batch(const GemvJob* jobs, int n_jobs, int epi, const float* nor
     groups[j] = (tiles[j] + kGMaxTiles - 1) / kGMaxTiles;
     need += groups[j];
   }
+  // Every workgroup streams its 16 sequences' activations once; launches of more workgroups than
+  // about one round over the CUs (large batches: prefill) re-stream them per row run and are left
+  // to the split-K kernel, which shares each activation fragment over more rows.
+  if (static_cast<long>(need) * n_sg > cus + cus / 4) return EF_HIP_OK;
   int target = std::max(need, std::min(nt, std::max(1, cus / n_sg)));
   if (target % 8 != 0 && (target / 8 + 1) * 8 <= nt) target = (target / 8 + 1) * 8;
   int have = need;
@@ -531,11 +553,11 @@ int launch_gemv_batch(const GemvJob* jobs, int n_jobs, int epi, const float* nor
   a.xcd = g0 % 8 == 0 ? 1 : 0;
   const long wgs = static_cast<long>(g0) * n_sg;
   if (wgs > 0x7FFFFFFFL) return EF_HIP_OK;
-  void* fn = epi == kEpiStore ? batch_kernel<kEpiStore>(norm_w != nullptr)
-                              : (epi == kEpiResidual ? batch_kernel<kEpiResidual>(norm_w != nullptr)
-                                                     : batch_kernel<kEpiSwiglu>(norm_w != nullptr));
+  const bool nrm = norm_w != nullptr;
+  void* fn = epi == kEpiSwiglu ? batch_kernel<kEpiSwiglu, kNW>(nrm)
+                                : (epi == kEpiStore ? batch_kernel<kEpiStore, kNW>(nrm) : batch_kernel<kEpiResidual, kNW>(nrm));
   void* params[] = {&a};
-  EFH_HIP(hipLaunchKernel(fn, dim3(static_cast<unsigned>(wgs)), dim3(kGT), params, lds, stream));
+  EFH_HIP(hipLaunchKernel(fn, dim3(static_cast<unsigned>(wgs)), dim3(kNW * kWave), params, lds, stream));
   *taken = true;
   return EF_HIP_OK;
 }
