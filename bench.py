@@ -216,6 +216,16 @@ def membench(L) -> dict:
     return {"median_gbs": round(r.median_gbps, 1), "best_gbs": round(r.best_gbps, 1), "bytes": r.buffer_bytes}
 
 
+def under_profiler() -> bool:
+    """Whether a GPU profiler's library is loaded into this process (rocprofv3 preloads its tool and
+    exports its settings).  The per-group profile and the B=64 engine crashed the host process when
+    traced (the per-group profile's graphs are made and destroyed within one call; the batched
+    prefill's graphs are replaced when buffers grow), so a traced run leaves both out."""
+    if any(k.startswith(("ROCPROF", "ROCP_")) for k in os.environ):
+        return True
+    return "rocprof" in os.environ.get("LD_PRELOAD", "")
+
+
 def cpu_model_name() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -240,7 +250,7 @@ def main() -> int:
                     help="profiling mode: only the B=64 Q4_0 5632x2048 matvec launches (fragment preparation + "
                          "matrix-core GEMV) over rotating replicas; prints their average time")
     ap.add_argument("--no-step-profile", action="store_true",
-                    help="skip the per-group decode profile (ef_hip_engine_profile): for runs under rocprofv3, where "
+                    help="skip the per-group decode profile (ef_hip_engine_profile); implied under a profiler, where "
                          "that call has crashed the host")
     ap.add_argument("--only-sampler", action="store_true",
                     help="profiling mode: only sampler calls on [B, 32000] N(0,3) logits (top-p 0.95 without top-k, "
@@ -251,6 +261,10 @@ def main() -> int:
               "run with --gpus 1", file=sys.stderr)
         return 2
     K, W = max(1, args.steps), max(0, args.warmup)
+    if under_profiler() and not args.no_step_profile:
+        log("[bench] a profiler is loaded: the per-group profile and the B=64 engine are left out")
+        args.no_step_profile = True
+        args.batch64 = 0
 
     from edgeforge_amd import _lib as L
     from edgeforge_amd import hip as H

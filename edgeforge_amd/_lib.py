@@ -132,7 +132,6 @@ SIGNATURES = {
     "ef_hip_engine_destroy": (C.c_int, [_P]),
     "ef_hip_engine_profile": (C.c_int, [_P, C.POINTER(ef_hip_sampler_config), _P, C.c_int,
                                         C.POINTER(C.c_double)]),
-    "ef_hip_engine_persistent": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
     "ef_hip_engine_tables": (C.c_int, [_P, C.POINTER(C.c_int), C.POINTER(C.c_char_p)]),
     "ef_hip_engine_forward": (C.c_int, [_P, _i32p, _sz, C.c_int]),
     "ef_hip_engine_prefill": (C.c_int, [_P, _i32p, _sz, _sz, C.c_int]),

@@ -26,7 +26,6 @@
 #include "common.h"
 #include "gemv.h"
 #include "glue.h"
-#include "step.h"
 #include "sampler.h"
 
 namespace {
@@ -72,6 +71,10 @@ struct ef_hip_engine_s {
   int32_t* tok_dev = nullptr;  // device staging of token ids ([batch][n] rows before they move into hist)
   std::vector<void*> allocs;
   std::map<int, hipGraphExec_t> graphs;
+  // Graph executables taken out of use (stale arguments, a finished profile) are kept until the
+  // engine is destroyed instead of being destroyed mid-process: a profiler that traces the graphs'
+  // kernels may still be reading a just-finished launch's records when its executable would go.
+  std::vector<hipGraphExec_t> retired;
   ef_hip_sampler_config scfg{};
   void* rng = nullptr;
   std::atomic<int>* owner_refs = nullptr;  // live-engine count of the device model it was made from
@@ -90,12 +93,6 @@ struct ef_hip_engine_s {
   double* eos_cur = nullptr;  // [B]
   double* eos_out = nullptr;  // [B][max_seq]
   void* rng_snap = nullptr;
-  // persistent one-sequence step (step.hip): phase table and barrier words on the device
-  efh::StepPhase* step_phases = nullptr;
-  int step_n = 0;
-  unsigned* step_sync = nullptr;
-  bool step_on = false;
-  std::string step_why;  // why the persistent step is off (empty when on)
   // several-sequence step over producer-staged tables (afrag.h): table set a holds the inputs of
   // q/k/v, gate/up and lm_head (K = D, with the RMSNorm's per-block partial sums), set b those of
   // o_proj and down; each set has both column orders
@@ -153,146 +150,6 @@ int put_tokens(ef_hip_engine e, size_t pos, size_t n) {
   EFH_HIP(hipMemcpyAsync(e->tok_dev, e->stage, (words + 8) * 4, hipMemcpyHostToDevice, e->stream));
   return launch_copy_rows(e->tok_dev, static_cast<long>(n), e->hist + pos, static_cast<long>(e->max_seq),
                           static_cast<int>(n), e->B, e->stream);
-}
-
-PersistentArgs step_args(ef_hip_engine e) {
-  const ef_hip_model_config& c = e->c;
-  PersistentArgs a{};
-  a.phases = e->step_phases;
-  a.n_phases = e->step_n;
-  a.pos_dev = e->pos;
-  a.hist = e->hist;
-  a.embed = e->embed->dev;
-  a.embed_qtype = e->embed->qtype;
-  a.embed_rows = static_cast<long>(e->embed->rows);
-  a.embed_rb = static_cast<long>(e->embed->row_bytes);
-  a.x = e->x;
-  a.D = static_cast<int>(c.D);
-  a.q = e->q;
-  a.knew = e->knew;
-  a.vnew = e->vnew;
-  a.ctx = e->ctx;
-  a.cos_t = e->cos_t;
-  a.sin_t = e->sin_t;
-  a.H = static_cast<int>(c.H);
-  a.KV = static_cast<int>(c.KV);
-  a.hd = static_cast<int>(c.hd);
-  a.max_seq = static_cast<int>(e->max_seq);
-  a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.hd)));  // src/kernels.cpp:158
-  a.sync = e->step_sync;
-  return a;
-}
-
-// The persistent step's phases for a one-sequence engine (EF_HIP_STEP=persistent): per layer q/k/v (fused attention RMSNorm;
-// the first layer's also stages the embedding row), attention, o_proj + residual, gate/up (fused
-// FFN RMSNorm) + SwiGLU, down + residual.  Weights sit in region 0 (q/k/v, gate/up) or 1 (o, down);
-// each phase's are fetched by an earlier phase: o by q/k/v, gate/up by attention, down by o, the
-// next layer's q/k/v by gate/up.  Leaves e->step_on false with the reason when the model does not
-// fit the kernel.
-int build_step(ef_hip_engine e) {
-  const ef_hip_model_config& c = e->c;
-  e->step_on = false;
-  if (e->B != 1) {
-    e->step_why = "batch > 1";
-    return EF_HIP_OK;
-  }
-  // Opt-in: measured slower than one launch per kernel (a grid barrier, the coherent activation
-  // fetch after it and the wait for the stores before it cost what a kernel boundary does).
-  const char* mode_env = std::getenv("EF_HIP_STEP");
-  if (mode_env == nullptr || std::strcmp(mode_env, "persistent") != 0) {
-    e->step_why = "off unless EF_HIP_STEP=persistent";
-    return EF_HIP_OK;
-  }
-  const int groups = step_groups();
-  auto rpw = [&](size_t rows) { return static_cast<int>((rows + groups - 1) / groups); };
-  auto job = [](ef_hip_weight w, ef_hip_weight w2, float* y, int row0) {
-    StepJob j{};
-    j.W = w->dev;
-    j.W2 = w2 ? w2->dev : nullptr;
-    j.y = y;
-    j.rows = static_cast<int>(w->rows);
-    j.row_bytes = static_cast<int>(w->row_bytes);
-    j.qtype = w->qtype;
-    j.row0 = row0;
-    return j;
-  };
-  const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
-  std::vector<StepPhase> ph;
-  for (size_t l = 0; l < c.L; ++l) {
-    const ef_hip_layer& w = e->layers[l];
-    const int base = static_cast<int>(ph.size());
-    StepPhase qkv{};
-    qkv.kind = kPhaseGemv;
-    qkv.epi = kEpiStore;
-    qkv.K = static_cast<int>(D);
-    qkv.n_jobs = 3;
-    qkv.job[0] = job(w.wq, nullptr, e->q, 0);
-    qkv.job[1] = job(w.wk, nullptr, e->knew, static_cast<int>(D));
-    qkv.job[2] = job(w.wv, nullptr, e->vnew, static_cast<int>(D + kvd));
-    qkv.rows = static_cast<int>(D + 2 * kvd);
-    qkv.rpw = rpw(qkv.rows);
-    qkv.region = 0;
-    qkv.own = l == 0 ? 1 : 0;
-    qkv.embed = l == 0 ? 1 : 0;
-    qkv.x = e->x;
-    qkv.norm_w = w.attn_norm_dev;
-    qkv.eps = c.eps;
-    qkv.pf = base + 2;  // o_proj
-    StepPhase at{};
-    at.kind = kPhaseAttention;
-    at.kc = e->kc + l * S * kvd;
-    at.vc = e->vc + l * S * kvd;
-    at.pf = base + 3;  // gate / up
-    StepPhase o{};
-    o.kind = kPhaseGemv;
-    o.epi = kEpiResidual;
-    o.K = static_cast<int>(D);
-    o.n_jobs = 1;
-    o.job[0] = job(w.wo, nullptr, e->x, 0);
-    o.rows = static_cast<int>(D);
-    o.rpw = rpw(D);
-    o.region = 1;
-    o.x = e->ctx;
-    o.pf = base + 4;  // down
-    StepPhase gu{};
-    gu.kind = kPhaseGemv;
-    gu.epi = kEpiSwiglu;
-    gu.K = static_cast<int>(D);
-    gu.n_jobs = 1;
-    gu.job[0] = job(w.w_gate, w.w_up, e->act, 0);
-    gu.rows = static_cast<int>(F);
-    gu.rpw = rpw(F);
-    gu.region = 0;
-    gu.x = e->x;
-    gu.norm_w = w.ffn_norm_dev;
-    gu.eps = c.eps;
-    gu.pf = l + 1 < c.L ? base + 5 : -1;  // the next layer's q/k/v
-    StepPhase dn{};
-    dn.kind = kPhaseGemv;
-    dn.epi = kEpiResidual;
-    dn.K = static_cast<int>(F);
-    dn.n_jobs = 1;
-    dn.job[0] = job(w.w_down, nullptr, e->x, 0);
-    dn.rows = static_cast<int>(D);
-    dn.rpw = rpw(D);
-    dn.region = 1;
-    dn.x = e->act;
-    dn.pf = -1;
-    for (const StepPhase& p : {qkv, at, o, gu, dn}) ph.push_back(p);
-  }
-  e->step_why = step_unsupported(ph.data(), static_cast<int>(ph.size()), groups, static_cast<int>(c.hd),
-                                 static_cast<int>(c.H), static_cast<int>(c.KV), static_cast<int>(S),
-                                 static_cast<int>(D));
-  if (e->step_why.empty()) e->step_why = step_launch_unsupported();
-  if (!e->step_why.empty()) return EF_HIP_OK;
-  EFH_RC(dev_alloc(e, reinterpret_cast<uint8_t**>(&e->step_phases), ph.size() * sizeof(StepPhase)));
-  EFH_RC(dev_alloc(e, &e->step_sync, kStepSyncWords));
-  EFH_HIP(hipMemcpyAsync(e->step_phases, ph.data(), ph.size() * sizeof(StepPhase), hipMemcpyHostToDevice, e->stream));
-  EFH_HIP(hipMemsetAsync(e->step_sync, 0, kStepSyncWords * sizeof(unsigned), e->stream));
-  EFH_HIP(hipStreamSynchronize(e->stream));
-  e->step_n = static_cast<int>(ph.size());
-  e->step_on = true;
-  return EF_HIP_OK;
 }
 
 AttnArgs attn_args(ef_hip_engine e) {
@@ -489,10 +346,6 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   const int B = e->B;
   const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
   hipStream_t s = e->stream;
-  if (e->step_on && groups == kAllGroups) {  // the embedding and every layer in one launch
-    EFH_RC(launch_step(step_args(e), s));
-    return enqueue_tail(e, mode, groups);
-  }
   if (e->staged) {
     EFH_RC(enqueue_staged_layers(e, groups));
     return enqueue_tail(e, mode, groups, true);
@@ -665,7 +518,7 @@ int ensure_prefill(ef_hip_engine e, size_t rows) {
   EFH_HIP(hipStreamSynchronize(e->stream));
   for (auto it = e->graphs.begin(); it != e->graphs.end();) {
     if (it->first & kPrefill) {
-      (void)hipGraphExecDestroy(it->second);
+      e->retired.push_back(it->second);
       it = e->graphs.erase(it);
     } else {
       ++it;
@@ -710,32 +563,29 @@ int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
   return EF_HIP_OK;
 }
 
+// Bounds the retired executables (a long chat that keeps changing sampler settings): past 256, the
+// older half is destroyed after the stream has drained.
+int trim_retired(ef_hip_engine e) {
+  if (e->retired.size() <= 256) return EF_HIP_OK;
+  EFH_HIP(hipStreamSynchronize(e->stream));
+  const size_t half = e->retired.size() / 2;
+  for (size_t i = 0; i < half; ++i) EFH_HIP(hipGraphExecDestroy(e->retired[i]));
+  e->retired.erase(e->retired.begin(), e->retired.begin() + static_cast<long>(half));
+  return EF_HIP_OK;
+}
+
 // Drops every cached graph whose mode has any of `bits` (their captured arguments are stale).
 int drop_graphs_with(ef_hip_engine e, int bits) {
   EFH_HIP(hipStreamSynchronize(e->stream));
   for (auto it = e->graphs.begin(); it != e->graphs.end();) {
     if (it->first & bits) {
-      EFH_HIP(hipGraphExecDestroy(it->second));
+      e->retired.push_back(it->second);
       it = e->graphs.erase(it);
     } else {
       ++it;
     }
   }
-  return EF_HIP_OK;
-}
-
-// After the stream has drained: a persistent step whose barrier gave up (an error word set by the
-// kernel) fails the call and turns the persistent step off for this engine.
-int check_step(ef_hip_engine e) {
-  if (!e->step_on) return EF_HIP_OK;
-  unsigned err = 0;
-  EFH_HIP(hipMemcpy(&err, e->step_sync + 1, sizeof(err), hipMemcpyDeviceToHost));
-  if (err == 0) return EF_HIP_OK;
-  e->step_on = false;
-  e->step_why = "a grid barrier of the persistent step timed out";
-  EFH_RC(drop_graphs_with(e, ~0));
-  return fail(EF_HIP_ERUNTIME, "persistent decode step: a grid barrier timed out; the step's results are invalid "
-                               "(this engine now uses one launch per kernel)");
+  return trim_retired(e);
 }
 
 // Sampler settings and RNG states are captured into the graphs that sample.
@@ -921,7 +771,6 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
   if (he == hipSuccess) he = hipMemsetAsync(e->step_counter, 0, 4, e->stream);
   if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
   if (he != hipSuccess) return cleanup_fail(fail_hip(he, "engine init"));
-  if ((rc = build_step(e)) != EF_HIP_OK) return cleanup_fail(rc);
   if ((rc = build_staged(e)) != EF_HIP_OK) return cleanup_fail(rc);
   e->magic = kEngineMagic;
   *out = e;
@@ -933,6 +782,7 @@ int ef_hip_engine_destroy(ef_hip_engine e) {
   e->magic = 0;
   (void)hipStreamSynchronize(e->stream);
   for (auto& kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+  for (hipGraphExec_t g : e->retired) (void)hipGraphExecDestroy(g);
   for (void* p : e->allocs) (void)hipFree(p);
   for (float* p : {e->pf_x, e->pf_q, e->pf_k, e->pf_v, e->pf_ctx, e->pf_act})
     if (p) (void)hipFree(p);
@@ -966,7 +816,6 @@ int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens, size_t pos, in
   EFH_HIP(hipMemcpyAsync(e->pos, e->tok_dev + e->B, 4, hipMemcpyDeviceToDevice, e->stream));
   EFH_RC(run_step(e, compute_logits ? kLogits : 0));
   EFH_HIP(hipStreamSynchronize(e->stream));
-  EFH_RC(check_step(e));
   e->cached = pos + 1;
   return EF_HIP_OK;
 }
@@ -1080,7 +929,6 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
                           B, e->stream));
   EFH_HIP(hipMemcpyAsync(tokens_out, e->tok_dev, n * B * 4, hipMemcpyDeviceToHost, e->stream));
   EFH_HIP(hipStreamSynchronize(e->stream));
-  EFH_RC(check_step(e));
   e->cached = n_prompt + n - 1;
   e->chat_ids.clear();
   if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
@@ -1147,7 +995,7 @@ int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, voi
       if (he == hipSuccess) he = hipEventElapsedTime(&ms, ev0, ev1);
       if (he != hipSuccess) rc = fail_hip(he, "engine_profile: timed launches");
     }
-    if (ex) (void)hipGraphExecDestroy(ex);
+    if (ex) e->retired.push_back(ex);
     ms_out[g] = static_cast<double>(ms) / (static_cast<double>(reps) * kInGraph);
   }
   (void)hipEventDestroy(ev0);
@@ -1155,14 +1003,6 @@ int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, voi
   if (rc == EF_HIP_OK) rc = set_pos();
   e->chat_ids.clear();
   return rc;
-}
-
-int ef_hip_engine_persistent(ef_hip_engine e, int* on, const char** why) {
-  EFH_RC(check_engine(e));
-  EFH_CHECK(on != nullptr, "engine_persistent: null output");
-  *on = e->step_on ? 1 : 0;
-  if (why != nullptr) *why = e->step_why.c_str();
-  return EF_HIP_OK;
 }
 
 int ef_hip_engine_tables(ef_hip_engine e, int* on, const char** why) {
@@ -1353,7 +1193,6 @@ int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids, size_t n_ids, const
     if (reason == 0) EFH_RC(snapshot());
   }
   EFH_HIP(hipStreamSynchronize(e->stream));
-  EFH_RC(check_step(e));
   const auto t2 = Clock::now();
   if (eos_p_out != nullptr) std::copy(peos.begin(), peos.begin() + steps, eos_p_out);
   e->chat_ids.assign(ids, ids + n_ids);

@@ -21,13 +21,6 @@ struct GemvJob {
 // All jobs of one launch share cols, the epilogue and the optional input RMSNorm (norm_w != null:
 // x' = norm_w * (x * rsqrt(mean(x^2) + eps)), kern::rmsnorm order).  batch sequences with row
 // strides ldx / ldy.  Enqueues on `stream`; returns an EF_HIP_* status.
-struct ShapeOverride {
-  int G = 0, R = 0;  // 0: the launcher's own choice
-  int path = 0;      // 0 auto, 1 LDS-DMA kernel, 2 register-fetch kernel
-  int waves = 0;     // waves per workgroup of the LDS-DMA kernel (0: the launcher's choice)
-};
-const ShapeOverride& shape_override();
-bool mfma_gemv_disabled();  // EF_HIP_GEMV_PATH=dma|regs selects the vector-ALU kernels
 
 // Matrix-core path for batches of 2 or more sequences (gemv_mfma.hip).  Sets *taken when it enqueued
 // the launches; otherwise the caller uses the vector-ALU kernels.  ws (>= gemv_mfma_workspace_bytes

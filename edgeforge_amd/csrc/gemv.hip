@@ -488,36 +488,12 @@ void* pick_dma_kernel_g(int G, int R) {
 }
 
 template <int EPI>
-void* pick_dma_kernel(int G, int R, int nw) {
-  return nw == 8 ? pick_dma_kernel_g<EPI, 8>(G, R) : pick_dma_kernel_g<EPI, 4>(G, R);
+void* pick_dma_kernel(int G, int R) {
+  return pick_dma_kernel_g<EPI, 4>(G, R);
 }
 
 }  // namespace
 
-// Tuning knobs, read once per process: EF_HIP_GEMV_SHAPE="G,R" (G in {8,16,32}, R in {1,2,4}) forces
-// the lane-group size and rows per group of the cols % 64 == 0 kernels; EF_HIP_GEMV_PATH=dma|regs
-// forces the LDS-DMA or the register-fetch kernel; EF_HIP_GEMV_WAVES=4|8 sets the DMA kernel's waves
-// per workgroup.
-const ShapeOverride& shape_override() {
-  static const ShapeOverride ov = [] {
-    ShapeOverride o;
-    const char* e = std::getenv("EF_HIP_GEMV_SHAPE");
-    int g = 0, r = 0;
-    if (e != nullptr && std::sscanf(e, "%d,%d", &g, &r) == 2 && (g == 8 || g == 16 || g == 32) &&
-        (r == 1 || r == 2 || r == 4)) {
-      o.G = g;
-      o.R = r;
-    }
-    const char* wv = std::getenv("EF_HIP_GEMV_WAVES");
-    if (wv != nullptr && (std::atoi(wv) == 4 || std::atoi(wv) == 8)) o.waves = std::atoi(wv);
-    const char* pth = std::getenv("EF_HIP_GEMV_PATH");
-    if (pth != nullptr) o.path = std::strcmp(pth, "dma") == 0 ? 1 : (std::strcmp(pth, "regs") == 0 ? 2 : 0);
-    return o;
-  }();
-  return ov;
-}
-
-bool mfma_gemv_disabled() { return shape_override().path != 0; }
 
 int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                 size_t ldy, hipStream_t stream, void* ws, size_t ws_bytes) {
@@ -609,12 +585,10 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
     return off;
   };
   constexpr size_t kDmaLdsTarget = 80 * 1024;  // two workgroups per CU
-  const ShapeOverride& ov = shape_override();
-  // Waves per workgroup of the DMA kernel.  Eight waves spread the per-workgroup staging over
-  // twice the rows but measured slower on MI355X (gate/up 5632x2048: 8.99 us against 8.30 us at
-  // four), so four is the default and eight stays selectable.
-  int nw = ov.waves > 0 ? ov.waves : 4;
-  bool use_dma = fast && ov.path != 2 && dma_layout(G, 1, nw, nullptr) <= kDmaLdsTarget;
+  // Waves per workgroup of the DMA kernel: four.  Eight waves spread the per-workgroup staging over
+  // twice the rows but measured slower on MI355X (gate/up 5632x2048: 8.99 us against 8.30 us).
+  int nw = 4;
+  bool use_dma = fast && dma_layout(G, 1, nw, nullptr) <= kDmaLdsTarget;
   if (!use_dma) nw = kWaves;
   // rows per tile: nw waves x (64/G) groups x R rows.  Register path: R as large as keeps >= 2
   // tiles per CU.  DMA path: the R that gives the busiest CU the fewest rows (rounds of tiles over
@@ -641,11 +615,6 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
         R = cand;
       }
     }
-  }
-  if (fast && ov.G > 0) {
-    G = ov.G;
-    R = ov.R;
-    if (ov.path == 1) use_dma = true;
   }
   size_t dma_lds = 0;
   if (use_dma) {
@@ -678,9 +647,9 @@ int launch_gemv(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, f
   size_t lds_bytes = (static_cast<size_t>(nslot) * kSlot + K / 32) * sizeof(float);
   void* fn = nullptr;
   if (fast && use_dma) {
-    fn = epi == kEpiStore ? pick_dma_kernel<kEpiStore>(G, R, nw)
-                          : (epi == kEpiResidual ? pick_dma_kernel<kEpiResidual>(G, R, nw)
-                                                 : pick_dma_kernel<kEpiSwiglu>(G, R, nw));
+    fn = epi == kEpiStore ? pick_dma_kernel<kEpiStore>(G, R)
+                          : (epi == kEpiResidual ? pick_dma_kernel<kEpiResidual>(G, R)
+                                                 : pick_dma_kernel<kEpiSwiglu>(G, R));
     lds_bytes = dma_lds;
   } else if (fast) {
     fn = epi == kEpiStore ? pick_pairs_kernel<kEpiStore>(G, R, npl)

@@ -463,21 +463,12 @@ size_t batch_lds(int nm) { return std::max<size_t>(static_cast<size_t>(nm) * Wg<
 // and a wave's tile loop takes about as long with half the blocks.
 constexpr int kNW = 8;
 
-// EF_HIP_BGEMV=0 leaves batched products to the tile-order kernel (gemv_mfma.hip).
-bool batch_disabled() {
-  static const bool off = [] {
-    const char* v = std::getenv("EF_HIP_BGEMV");
-    return v != nullptr && std::strcmp(v, "0") == 0;
-  }();
-  return off;
-}
-
 }  // namespace
 
 int launch_gemv_batch(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch,
                       size_t ldx, size_t ldy, hipStream_t stream, bool* taken) {
   *taken = false;
-  if (batch_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kGMaxJobs) return EF_HIP_OK;
+  if (batch < 2 || n_jobs < 1 || n_jobs > kGMaxJobs) return EF_HIP_OK;
   const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
   for (int j = 0; j < n_jobs; ++j) {
     const ef_hip_weight_s* W = jobs[j].W;

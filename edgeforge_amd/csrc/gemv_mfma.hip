@@ -955,25 +955,6 @@ int groups_for(const GemvJob* jobs, int n_jobs, int rows_wg) {
   return g;
 }
 
-// EF_HIP_MFMA_SHAPE=RT,NS,S pins the batched kernel's shape (tuning); 0 fields stay automatic.
-struct MfmaOverride {
-  int RT = 0, NS = 0, S = 0;
-};
-const MfmaOverride& mfma_override() {
-  static const MfmaOverride ov = [] {
-    MfmaOverride o;
-    const char* e = std::getenv("EF_HIP_MFMA_SHAPE");
-    int rt = 0, ns = 0, sp = 0;
-    if (e != nullptr && std::sscanf(e, "%d,%d,%d", &rt, &ns, &sp) == 3) {
-      o.RT = rt;
-      o.NS = ns;
-      o.S = sp;
-    }
-    return o;
-  }();
-  return ov;
-}
-
 // Estimated time (CU cycles) of one shape: per workgroup its matrix-core time plus most of its
 // vector-ALU time (measured on MI355X, the two overlap only partly), or its operand stream if that
 // is longer; times the rounds of workgroups (one resident per CU), against the weights' HBM time;
@@ -1001,7 +982,7 @@ double shape_cost(int rt, int nm, int ns, int sg, int groups, int S, int bps, si
 // even_rt: only shapes whose workgroup rows are a multiple of 32 (outputs staged as tables).
 Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, bool even_rt = false) {
   Plan p;
-  if (mfma_gemv_disabled() || batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return p;
+  if (batch < 2 || n_jobs < 1 || n_jobs > kMaxJobsM) return p;
   const size_t K = jobs[0].W->cols;
   if (K % 32 != 0 || K > 65536) return p;
   size_t wbytes = 0;
@@ -1021,7 +1002,6 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, 
   const int nb = static_cast<int>(K / 32);
   const int cus = ctx().cu_count > 0 ? ctx().cu_count : 256;
   const size_t lim = ctx().lds_per_block > 0 ? ctx().lds_per_block : 65536;
-  const MfmaOverride& ov = mfma_override();
   // every instantiated (RT, NS) and split S whose LDS fits, the cheapest by shape_cost (ties: the
   // first found)
   bool found = false;
@@ -1030,7 +1010,7 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, 
                                  : static_cast<int>(sizeof(kShapesStore) / sizeof(Shape));
   for (int si = 0; si < n_shapes; ++si) {
     const int rt = shapes[si].RT, ns = shapes[si].NS;
-    if ((ov.RT > 0 && rt != ov.RT) || (ov.NS > 0 && ns != ov.NS) || (ns > 1 && p.NT < ns)) continue;
+    if (ns > 1 && p.NT < ns) continue;
     if (even_rt && rt % 2 != 0) continue;
     const int sg = (p.NT + ns - 1) / ns;
     const int rows_wg = rt * kTileRows;
@@ -1042,7 +1022,7 @@ Plan plan_mfma(const GemvJob* jobs, int n_jobs, int epi, int batch, size_t ldx, 
     for (int s_try = 1; s_try <= std::min(32, std::max(1, nb / 8)); ++s_try) {
       const int bps = (nb + s_try - 1) / s_try;
       const int S = (nb + bps - 1) / bps;
-      if (S != s_try || (ov.S > 0 && S != ov.S) || bps > kWavesM * max_blocks_per_wave(rt, p.nm, ns)) continue;
+      if (S != s_try || bps > kWavesM * max_blocks_per_wave(rt, p.nm, ns)) continue;
       const size_t part = S > 1 ? static_cast<size_t>(groups) * S * p.chunk * rows_wg * p.nm * sizeof(float) : 0;
       const double c = shape_cost(rt, p.nm, ns, sg, groups, S, bps, wbytes, 2 * part, cus, even_rt);
       if (!found || c < p.cost) {
@@ -1127,72 +1107,12 @@ size_t gemv_mfma_workspace_bytes(const GemvJob* jobs, int n_jobs, int epi, int b
   return p.ok ? p.bytes : 0;
 }
 
-namespace {
-// EF_HIP_MFMA_TABLES=block: batched products go through block-scaled tables made by
-// launch_stage_tables (the path producer-staged inputs take), for testing that path on any input.
-bool block_tables_forced() {
-  const char* v = std::getenv("EF_HIP_MFMA_TABLES");
-  return v != nullptr && std::strcmp(v, "block") == 0;
-}
-}  // namespace
 
 int launch_gemv_mfma(const GemvJob* jobs, int n_jobs, int epi, const float* norm_w, float eps, int batch, size_t ldx,
                      size_t ldy, void* ws, size_t ws_bytes, hipStream_t stream, bool* taken) {
   *taken = false;
   const Plan pl = plan_mfma(jobs, n_jobs, epi, batch, ldx);
   if (!pl.ok) return EF_HIP_OK;
-  if (block_tables_forced() && jobs[0].W->cols <= static_cast<size_t>(kSeqPrepMaxK)) {
-    const int K = static_cast<int>(jobs[0].W->cols);
-    const size_t xld = jobs[0].ldx ? jobs[0].ldx : ldx;
-    int rc = EF_HIP_OK;
-    for (int b0 = 0; b0 < batch && rc == EF_HIP_OK; b0 += pl.chunk) {
-      const int nb = std::min(pl.chunk, batch - b0);
-      const int bpad = stage_bpad(nb);
-      const size_t tb = stage_table_bytes(K, nb);
-      const size_t need = (pl.q4 ? tb : 0) + (pl.q8 ? tb : 0) + static_cast<size_t>(K / 32) * bpad * 4 + bpad * 8 + 256 +
-                          pl.bytes;
-      uint8_t* buf = nullptr;
-      EFH_HIP(hipMallocAsync(reinterpret_cast<void**>(&buf), need, stream));
-      MfmaStage st{};
-      size_t off = 0;
-      if (pl.q4) {
-        st.t4 = buf + off;
-        off += tb;
-      }
-      if (pl.q8) {
-        st.t8 = buf + off;
-        off += tb;
-      }
-      st.bscale = reinterpret_cast<float*>(buf + off);
-      off += static_cast<size_t>(K / 32) * bpad * 4;
-      off = (off + 15) & ~size_t(15);
-      st.ssp = reinterpret_cast<double*>(buf + off);  // written by the preparation either way
-      off += static_cast<size_t>(bpad) * 8;
-      off = (off + 255) & ~size_t(255);
-      st.bpad = bpad;
-      st.n_ssp = 1;
-      st.eps = eps;
-      MfmaStage mk = st;
-      if (norm_w == nullptr) {  // the product has no RMSNorm: its epilogue factor is 1
-        st.ssp = nullptr;
-        st.n_ssp = 0;
-      }
-      rc = launch_stage_tables(jobs[0].x + b0 * xld, xld, K, nb, norm_w, mk, stream);
-      GemvJob cj[kMaxJobsM];
-      for (int j = 0; j < n_jobs; ++j) {
-        cj[j] = jobs[j];
-        const size_t yld = jobs[j].ldy ? jobs[j].ldy : ldy;
-        cj[j].y = jobs[j].y + b0 * yld;
-        cj[j].ldy = yld;
-      }
-      if (rc == EF_HIP_OK)
-        rc = launch_gemv_mfma_staged(cj, n_jobs, epi, st, nb, ldy, buf + off, pl.bytes, stream, nullptr);
-      const hipError_t e = hipFreeAsync(buf, stream);
-      if (e != hipSuccess && rc == EF_HIP_OK) rc = fail_hip(e, "hipFreeAsync");
-    }
-    if (rc == EF_HIP_OK) *taken = true;
-    return rc;
-  }
   if (norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 != 0) return EF_HIP_OK;
   for (int j = 0; j < n_jobs; ++j) {
     EFH_RC(ensure_tiled(jobs[j].W, stream));

@@ -196,12 +196,6 @@ class Engine:
 
     PROFILE_GROUPS = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "pick")
 
-    def persistent(self) -> tuple[bool, str]:
-        """Whether decode steps run as one persistent launch, and why not (ef_hip_engine_persistent)."""
-        on, why = C.c_int(0), C.c_char_p()
-        EL.call("ef_hip_engine_persistent", self.h, C.byref(on), C.byref(why))
-        return bool(on.value), (why.value or b"").decode()
-
     def staged_tables(self) -> tuple[bool, str]:
         """Whether several-sequence steps run over producer-staged product inputs, and why not
         (ef_hip_engine_tables)."""

@@ -253,17 +253,6 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt_host, size_t n
 #define EF_HIP_PROF_GROUPS 8
 int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, void* rng_dev, int reps, double* ms_out);
 
-/* With the environment variable EF_HIP_STEP=persistent at engine creation, a one-sequence engine
- * runs the embedding and every layer of a decode step as ONE persistent cooperative launch (one
- * workgroup per CU, phases separated by grid barriers; the final norm, lm_head and the pick follow
- * as ordinary launches), with logits bit-identical to the default one-launch-per-kernel step.  It
- * is opt-in because it measured slower on MI355X.  *on = 1 when this engine uses it; *why (owned
- * by the engine) says why not otherwise: not requested, batch > 1, or a model outside the kernel's
- * LDS budget.  No counterpart in the reference (a CPU build has no kernel boundaries); it lets a
- * caller see which step path runs.  A grid barrier that gives up (its spin is bounded) fails the
- * forward / generate / reply call with EF_HIP_ERUNTIME and turns the persistent step off. */
-int ef_hip_engine_persistent(ef_hip_engine e, int* on, const char** why);
-
 /* A several-sequence engine runs its decode step over producer-staged inputs: the embedding lookup,
  * the KV-group attention and the o / gate-up / down products write the next product's matrix-core
  * input tables (block-scaled fp16 hi + lo pairs, with the RMSNorm's per-block partial sums) as they

@@ -252,7 +252,6 @@ def test_group_attention_forward_matches_oracle(hip, cfg, monkeypatch):
     ODD has three query heads per group) against the oracle's Transformer at every position."""
     print(f"[case] group attention forward {cfg}", flush=True)
     monkeypatch.setenv("EF_HIP_ATTENTION", "group")
-    monkeypatch.setenv("EF_HIP_STEP", "kernels")
     dm = DeviceModel.synthetic(cfg, seed=13)
     om = OracleModel(dm)
     ids = [int(v) for v in D.rng(8).integers(0, cfg.V, 12)]
@@ -308,7 +307,6 @@ def test_decode_attention_across_the_first_chunk_matches_oracle(hip, kind, monke
     forced per kernel, tokens and every step's logits match the oracle."""
     print(f"[case] decode across position 64, attention={kind}", flush=True)
     monkeypatch.setenv("EF_HIP_ATTENTION", kind)
-    monkeypatch.setenv("EF_HIP_STEP", "kernels")
     dm = DeviceModel.synthetic(LONG, seed=31)
     om = OracleModel(dm)
     prompt = [int(v) for v in D.rng(12).integers(0, LONG.V, 58)]
@@ -325,7 +323,6 @@ def test_wave_attention_short_cache_matches_oracle(hip, monkeypatch):
     through the buffer range and are never used; every position's logits match the oracle."""
     print("[case] wave attention, max_seq 12", flush=True)
     monkeypatch.setenv("EF_HIP_ATTENTION", "wave")
-    monkeypatch.setenv("EF_HIP_STEP", "kernels")
     dm = DeviceModel.synthetic(SMALL, seed=37)
     om = OracleModel(dm)
     ids = [int(v) for v in D.rng(10).integers(0, SMALL.V, 12)]
@@ -376,87 +373,10 @@ def test_engine_profile_groups_and_state(hip, B):
     eng.close()
 
 
-# ---- persistent one-sequence step (one cooperative launch for the embedding and every layer) ----
+# ---- several-sequence steps over producer-staged product inputs ----
 
 TWO_LAYER = Config(D=2048, F=5632, H=32, KV=4, hd=64, V=1024, L=2, max_pos=128)  # TinyLlama's layer shapes
 
-
-def test_config5_greedy_persistent_step_matches_oracle(tinyllama, monkeypatch):
-    """Config 5 through the opt-in persistent step: the TinyLlama engine takes it, and the 32
-    greedy tokens are the oracle's."""
-    dm, om = tinyllama
-    monkeypatch.setenv("EF_HIP_STEP", "persistent")
-    prompt = [int(v) for v in D.rng(23).integers(0, 32000, 23)]
-    want, want_logits, _, _ = om.run_once(prompt, 32)
-    eng = Engine(dm, max_seq=23 + 32)
-    on, why = eng.persistent()
-    assert on, why
-    got, _, _ = eng.generate([prompt], 32)
-    _, flip = assert_greedy_identical(got[0], want, want_logits, "config 5 persistent:")
-    assert flip is None or flip > 0
-    eng.close()
-
-
-@pytest.mark.parametrize("q8", [frozenset(), frozenset({(0, "wk"), (0, "wv"), (1, "wv")})])
-def test_persistent_step_bit_identical_to_kernel_launches(hip, q8, monkeypatch):
-    """TinyLlama's layer shapes, Q4_0 with and without Q8_0 matrices in the mix: the persistent step
-    computes every row, RMSNorm and attention exactly as the one-launch-per-kernel step, so greedy
-    tokens and the final logits are identical bit for bit, across the 64-position boundary."""
-    print(f"[case] persistent vs kernel launches, q8={sorted(q8)}", flush=True)
-    dm = DeviceModel.synthetic(TWO_LAYER, seed=41, q8=q8)
-    prompt = [int(v) for v in D.rng(14).integers(0, TWO_LAYER.V, 58)]
-    out = {}
-    for kind in ("persistent", "kernels"):
-        monkeypatch.setenv("EF_HIP_STEP", kind)
-        eng = Engine(dm, max_seq=80)
-        assert eng.persistent()[0] == (kind == "persistent"), eng.persistent()
-        toks, _, _ = eng.generate([prompt], 12)
-        out[kind] = (toks, eng.logits().copy())
-        eng.close()
-    assert np.array_equal(out["persistent"][0], out["kernels"][0])
-    assert np.array_equal(out["persistent"][1].view(np.uint32), out["kernels"][1].view(np.uint32))
-
-
-def test_persistent_step_matches_oracle_each_position(hip, monkeypatch):
-    """Small shapes (rows per workgroup of 1-2, idle workgroups, a mixed Q4_0 / Q8_0 q/k/v phase):
-    the persistent step's logits match the oracle's Transformer at every position."""
-    print("[case] persistent step, SMALL, forward per position", flush=True)
-    monkeypatch.setenv("EF_HIP_STEP", "persistent")
-    dm = DeviceModel.synthetic(SMALL, seed=43, q8={(0, "wk"), (1, "wv"), (2, "w_down")})
-    om = OracleModel(dm)
-    ids = [int(v) for v in D.rng(15).integers(0, SMALL.V, 20)]
-    eng = Engine(dm, max_seq=len(ids))
-    assert eng.persistent()[0], eng.persistent()
-    ot = om.transformer(len(ids))
-    for p, t in enumerate(ids):
-        eng.forward([t], p)
-        assert _logit_err(eng.logits()[0], ot.forward(t, p)) < 1e-4, p
-    ot.close()
-    eng.close()
-
-
-def test_persistent_step_off_where_it_does_not_apply(hip, monkeypatch):
-    """Without EF_HIP_STEP=persistent, for batches and for head_dim other than 64 the engine takes
-    the one-launch-per-kernel step and says why."""
-    dm = DeviceModel.synthetic(SMALL, seed=3)
-    eng = Engine(dm, max_seq=16)
-    on, why = eng.persistent()
-    assert not on and "EF_HIP_STEP" in why
-    eng.close()
-    monkeypatch.setenv("EF_HIP_STEP", "persistent")
-    dm = DeviceModel.synthetic(WIDE, seed=3)
-    eng = Engine(dm, max_seq=16)
-    on, why = eng.persistent()
-    assert not on and "head_dim" in why
-    eng.close()
-    dm = DeviceModel.synthetic(SMALL, seed=3)
-    eng = Engine(dm, max_seq=16, batch=2)
-    on, why = eng.persistent()
-    assert not on and "batch" in why
-    eng.close()
-
-
-# ---- several-sequence steps over producer-staged product inputs ----
 
 @pytest.mark.parametrize("cfg,B,q8,attn", [
     (SMALL, 3, {(0, "wk"), (1, "wv"), (2, "w_down")}, None),  # per-head attention: o's input prepared
