@@ -125,6 +125,7 @@ SIGNATURES = {
     "ef_hip_sample_noalloc": (C.c_int, [_P, _sz, C.c_int, _sz, C.POINTER(ef_hip_sampler_config), _P, _P, _sz, _P,
                                         _P, _P]),
     "ef_hip_argmax": (C.c_int, [_P, _sz, C.c_int, _sz, _P, _P]),
+    "ef_hip_sampler_exp": (C.c_int, [_P, _P, _sz, _P]),
     "ef_hip_profile_matvec": (C.c_int, [C.c_int, C.POINTER(_P), C.POINTER(_P), _sz, _P, _P, C.c_float, _P, C.c_int,
                                         C.c_int, _P, _f32p]),
     "ef_hip_engine_create": (C.c_int, [C.POINTER(ef_hip_model_config), C.POINTER(ef_hip_layer), _P, _P, _P, _sz,

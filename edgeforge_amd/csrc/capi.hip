@@ -476,6 +476,12 @@ int ef_hip_argmax(const float* x, size_t n, int batch, size_t ld, int32_t* out, 
   return launch_argmax(x, static_cast<int>(n), static_cast<long>(ld), batch, out, pick(stream));
 }
 
+int ef_hip_sampler_exp(const double* x, double* y, size_t n, void* stream) {
+  EFH_READY();
+  EFH_CHECK(n == 0 || (x && y), "sampler_exp: null pointer");
+  return launch_exp(x, y, n, pick(stream));
+}
+
 size_t ef_hip_rng_state_bytes(void) { return kRngStateBytes; }
 
 int ef_hip_rng_seed(void* rng, const uint64_t* seeds_host, int batch, void* stream) {

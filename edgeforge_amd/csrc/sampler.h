@@ -31,6 +31,8 @@ int launch_argmax_finish(const float* x, int n, long ld, int batch, const StepAr
 int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_hip_sampler_config& cfg,
                   const int32_t* hist, const int32_t* hist_len, long hist_ld, void* rng, int32_t* out, void* ws,
                   hipStream_t s, int eos_id = -1, double* eos_p = nullptr);
+// y[i] = exp(x[i]), the sampler's softmax-term call.
+int launch_exp(const double* x, double* y, size_t n, hipStream_t s);
 // std::mt19937_64::discard(k) on every sequence's state.
 int launch_rng_discard(void* rng, int batch, int k, hipStream_t s);
 

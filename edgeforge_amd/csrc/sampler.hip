@@ -17,12 +17,11 @@
 //    sum's binade (exact_scan, below);
 //  * the draw is std::uniform_real_distribution<double>(0, 1) over a std::mt19937_64 kept on the
 //    device (one state per sequence), advanced once per call exactly when temperature > 0.
-// The one libm call is exp(double); the device's exp and glibc's agree to the last bit except in
-// rare cases, where a flip of the chosen id would also need r to lie within an ulp of a
-// cumulative sum.
+// The one libm call, exp(double), is exp_libm (exp_f64.h): glibc's exp to the last bit.
 #include <cmath>
 
 #include "common.h"
+#include "exp_f64.h"
 #include "sampler.h"
 
 #pragma clang fp contract(off)
@@ -498,7 +497,7 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
   for (int w = 1; w < nw; ++w) m = fmax(m, red[w]);
   __syncthreads();
   double s = 0.0;
-  for (int i = t; i < V; i += blockDim.x) s += exp(static_cast<double>(lg[i]) - m);
+  for (int i = t; i < V; i += blockDim.x) s += exp_libm(static_cast<double>(lg[i]) - m);
   s = wave_sum_d(s);
   if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
   __syncthreads();
@@ -506,7 +505,7 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
   for (int w = 0; w < nw; ++w) tot += red[w];
   __syncthreads();
   if (id < 0 || id >= V) return 0.0;
-  return exp(static_cast<double>(lg[id]) - m) / tot;
+  return exp_libm(static_cast<double>(lg[id]) - m) / tot;
 }
 
 // The sampler after the sort (src/sampler.cpp:42-69): softmax over the kept ids, the nucleus, the
@@ -519,7 +518,7 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
   const bool in_lds = topk;
   if (topk) prob = s_prob;
   const float mx = key_value(sorted[0]);
-  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp(static_cast<double>(key_value(sorted[i]) - mx));
+  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp_libm(static_cast<double>(key_value(sorted[i]) - mx));
   __threadfence_block();
   __syncthreads();
   {
@@ -1023,7 +1022,7 @@ __global__ __launch_bounds__(kMergeThreads) void rank_merge_kernel(SampleArgs a)
     }
     const int cols = (a.vocab + kScanPer - 1) / kScanPer;
     prob_of(a, blockIdx.y)[(pos % kScanPer) * cols + pos / kScanPer] =
-        exp(static_cast<double>(key_value(x) - key_value(top)));
+        exp_libm(static_cast<double>(key_value(x) - key_value(top)));
   }
 }
 
@@ -1364,6 +1363,13 @@ __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
   sample_tail(a, b, merged_of(a, b), tail_keep(a), false, prob, nullptr, s_stage, s_stop, s_sum, s_keep);
 }
 
+// exp_libm over an array: the softmax-term call of the kernels above, for comparison with a host
+// libm.
+__global__ __launch_bounds__(256) void exp_kernel(const double* __restrict__ x, double* __restrict__ y, size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = exp_libm(x[i]);
+}
+
 }  // namespace
 
 size_t sample_workspace_stride(int vocab) {
@@ -1383,6 +1389,14 @@ int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t
 int launch_argmax(const float* x, int n, long ld, int batch, int32_t* out, hipStream_t s) {
   EFH_CHECK(n >= 1 && static_cast<size_t>(n) * 4 < (1ull << 32), "argmax: n must be in [1, 2^30)");
   hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(kArgmaxThreads), 0, s, x, n, ld, out);
+  EFH_HIP(hipGetLastError());
+  return EF_HIP_OK;
+}
+
+int launch_exp(const double* x, double* y, size_t n, hipStream_t s) {
+  if (n == 0) return EF_HIP_OK;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, x, y, n);
   EFH_HIP(hipGetLastError());
   return EF_HIP_OK;
 }

@@ -13,7 +13,7 @@ from . import _lib as L
 from ._lib import BF16, F16, F32, Q4_0, Q8_0, call, lib
 
 __all__ = ["DeviceArray", "Weight", "Stream", "Event", "init", "row_bytes", "matvec", "matvec_jobs",
-           "matvec_residual", "matvec_swiglu", "matvec_jobs_rmsnorm", "quantize", "rows_f32", "argmax",
+           "matvec_residual", "matvec_swiglu", "matvec_jobs_rmsnorm", "quantize", "rows_f32", "argmax", "sampler_exp",
            "RngStates", "sample", "F32", "F16", "BF16", "Q8_0", "Q4_0"]
 
 
@@ -203,6 +203,11 @@ def quantize(qtype: int, w: DeviceArray, rows: int, cols: int, search: bool = Tr
 
 def rows_f32(W: Weight, ids: DeviceArray, out: DeviceArray, batch: int = 1, stream=None) -> None:
     call("ef_hip_rows_f32", W.handle, ids.ptr, batch, out.ptr, W.cols, _s(stream))
+
+
+def sampler_exp(x: DeviceArray, y: DeviceArray, n: int, stream=None) -> None:
+    """y[:n] = exp(x[:n]) on the device, as the sampler's softmax terms are computed (float64 arrays)."""
+    call("ef_hip_sampler_exp", x.ptr, y.ptr, n, _s(stream))
 
 
 def argmax(x: DeviceArray, n: int, out: DeviceArray, batch: int = 1, ld: int | None = None, stream=None) -> None:

@@ -160,6 +160,10 @@ int ef_hip_sample_noalloc(const float* logits_dev, size_t vocab, int batch, size
                           int32_t* out_dev, void* stream);
 /* kern::argmax (src/kernels.cpp:105-111): first maximum wins. */
 int ef_hip_argmax(const float* x_dev, size_t n, int batch, size_t ld, int32_t* out_dev, void* stream);
+/* The sampler's softmax-term function (std::exp in src/sampler.cpp:46) over n device doubles:
+ * y[i] = exp(x[i]) computed as the sampling kernels compute it, so that a caller can compare the
+ * device's exp with the host libm the reference links. */
+int ef_hip_sampler_exp(const double* x_dev, double* y_dev, size_t n, void* stream);
 
 /* ---- profiling (the reference's per-op timing, src/bench_decode.cpp:164-231) -------------------
  * Runs `launches` GEMVs back to back on `stream` as one captured HIP graph (launch overhead

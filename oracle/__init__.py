@@ -129,6 +129,7 @@ def lib():
         _sig(L, "efo_sampler_sample", C.c_int32, _P, _f32p, _sz, _i32p, _sz)
         _sig(L, "efo_sampler_last_keep", _sz, _P, _i32p, _f64p, _sz)
         _sig(L, "efo_sampler_last_r", C.c_double, _P)
+        _sig(L, "efo_exp_array", None, _f64p, _f64p, _sz)
         _sig(L, "efo_transformer_create", _P, C.POINTER(efo_model), _sz, _P, C.c_int)
         _sig(L, "efo_transformer_destroy", None, _P)
         _sig(L, "efo_transformer_forward", _f32p, _P, C.c_int32, _sz, C.c_int, C.POINTER(C.c_int))
@@ -259,6 +260,14 @@ def matvec_jobs(jobs, backend: int = AVX2, pool: Pool | None = None):
         arr[i] = efo_job(ptr(ys[i], _f32p), C.pointer(ws[i]), ptr(keep[i], _f32p))
     lib().efo_matvec_jobs(backend, arr, len(jobs), pool.h if pool else None)
     return ys
+
+
+def exp_array(x: np.ndarray) -> np.ndarray:
+    """exp of every element through the host libm (the softmax-term call, src/sampler.cpp:46)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty_like(x)
+    lib().efo_exp_array(ptr(x, _f64p), ptr(y, _f64p), x.size)
+    return y
 
 
 class Sampler:

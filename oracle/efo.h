@@ -129,6 +129,9 @@ int32_t efo_sampler_sample(efo_sampler* s, const float* logits, size_t vocab, co
 /* Debug view of the last call: the kept candidate ids (sorted) and their final probabilities. */
 size_t efo_sampler_last_keep(const efo_sampler* s, int32_t* ids, double* probs, size_t cap);
 double efo_sampler_last_r(const efo_sampler* s);
+/* y[i] = exp(x[i]) through the host libm's exp, the call the softmax terms use (std::exp,
+ * src/sampler.cpp:46): the host side of the device exp(double) sweep. */
+void efo_exp_array(const double* x, double* y, size_t n);
 
 /* ---- transformer (include/ef/model.h, src/model.cpp:153-304) --------------------------------- */
 typedef struct {

@@ -200,3 +200,7 @@ size_t efo_sampler_last_keep(const efo_sampler* s, int32_t* ids, double* probs, 
 }
 
 double efo_sampler_last_r(const efo_sampler* s) { return s->last_r; }
+
+void efo_exp_array(const double* x, double* y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = exp(x[i]);
+}

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from tests import _data as D
 
 L = O.lib()
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
@@ -130,3 +131,17 @@ def test_sampler_ids_match_golden_reference_sequences(ci):
     a = O.Sampler(T, k, p, rep, seed=77)
     got = [a.sample(*sampler_inputs(ci, step)) for step in range(10)]
     assert got == GOLDEN["sampler"][str(ci)]
+
+
+def test_exp_array_is_the_host_libm():
+    """The host side of the device exp sweep: the oracle's exp equals CPython's math.exp (the same
+    libm) on sampled points, and the closed forms exp(0) = 1, exp(-inf-side underflow) = 0, exp of a
+    tiny argument = 1 rounded, and the subnormal range are kept."""
+    import math
+    x = -D.rng(17).uniform(0.0, 746.0, 4096)
+    x = np.concatenate([x, [0.0, -0.0, -1e-300, -745.2, -740.0, -709.0, -1.0]])
+    y = O.exp_array(x)
+    assert all(y[i] == math.exp(x[i]) for i in range(x.size))
+    assert y[-7] == 1.0 and y[-6] == 1.0 and y[-5] == 1.0 and y[-4] == 0.0
+    assert 0.0 < y[-3] < np.finfo(np.float64).tiny  # exp(-740) is subnormal
+    assert abs(y[-1] - 0.36787944117144233) <= np.spacing(0.36787944117144233)
