@@ -159,28 +159,62 @@ def step_profile(eng, ms_per_step: float, cfg, sampler=None, rng=None, reps: int
     return out
 
 
-CPU_RUNS = {"threads": 7, "one": 3}  # timed runs per thread count; the medians are reported
+CPU_RUNS = 5  # timed runs at the default thread count; their median is the reported value
+CPU_STEPS = 32  # greedy steps per run (the decode-protocol n)
 
 
-def cpu_baseline(model, prompt, n: int = 32):
+def cpu_baseline(model, prompt, n: int = CPU_STEPS):
     """The reference CPU path (oracle: AVX2 + persistent thread pool, src/qkernels.cpp:131-297,
-    src/threadpool.cpp) on this host, same weights, the reference protocol: (n-1)/decode_s, at the
-    default thread count and at one thread (the ladder's first row, src/bench_decode.cpp:73-81),
-    each the median of CPU_RUNS timed runs (about 10-15 s of CPU work in all)."""
+    src/threadpool.cpp) on this host, same weights, the reference protocol ((n-1)/decode_s,
+    src/bench_decode.cpp:30-49): the median of CPU_RUNS runs at the default thread count, then the
+    reference's ladder (src/bench_decode.cpp:62-81,104-137), one run per row: scalar/1, avx2/1, avx2
+    at {2, 4, physical cores, logical CPUs} and scalar at the largest of those.  Each multi-thread row
+    is checked bit-identical (tokens and every logit) to its kernel's 1-thread run, and each avx2 row's
+    tokens and logits are compared with scalar/1 (logits up to and including the first differing
+    token).  About 15 s of CPU work on a 16-CPU host.  Returns (tok/s, threads, ladder rows)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import oracle as O  # noqa: F401  (checker / baseline only)
+    import oracle as O  # checker / baseline only
     from oracle.model import OracleModel, cpu_threads
     om = OracleModel(model)
     threads = cpu_threads()
-    out = {}
-    for t, runs in ((threads, CPU_RUNS["threads"]), (1, CPU_RUNS["one"])):
-        om.run_once(prompt[:4], 2, threads=t)  # warm-up (src/bench_decode.cpp:90-95)
-        rates = []
-        for _ in range(runs):
-            _, _, pre, dec = om.run_once(prompt, n, threads=t)
-            rates.append((n - 1) / dec)
-        out[t] = float(np.median(rates))
-    return out[threads], threads, out[1]
+    om.run_once(prompt[:4], 2, threads=threads)  # warm-up: fault in every weight page (src/bench_decode.cpp:90-95)
+    rates = []
+    for _ in range(CPU_RUNS):
+        _, _, _, dec = om.run_once(prompt, n, threads=threads)
+        rates.append((n - 1) / dec)
+    value = float(np.median(rates))
+
+    phys, logical = cpu_topology()
+    counts = sorted({t for t in (2, 4, phys, logical) if t >= 2})
+    ladder = [(O.SCALAR, 1), (O.AVX2, 1)] + [(O.AVX2, t) for t in counts] + ([(O.SCALAR, counts[-1])] if counts else [])
+    names = {O.SCALAR: "scalar", O.AVX2: "avx2"}
+    ones, rows = {}, []
+    for be, t in ladder:
+        toks, logits, pre, dec = om.run_once(prompt, n, threads=t, backend=be)
+        row = {"kernels": names[be], "threads": t, "prefill_tps": round(len(prompt) / pre, 3),
+               "decode_tps": round((n - 1) / dec, 3)}
+        if t == 1:
+            ones[be] = (toks, logits)
+        else:
+            t1, l1 = ones[be]
+            row["bit_identical_to_1_thread"] = bool(np.array_equal(toks, t1) and
+                                                   np.array_equal(logits.view(np.uint32), l1.view(np.uint32)))
+        if be != O.SCALAR:
+            st, sl = ones[O.SCALAR]
+            same = int(np.argmin(np.append(toks == st, False)))  # leading tokens equal to scalar/1's
+            comparable = min(n, same + 1)
+            rel = max(float(np.abs(logits[k].astype(np.float64) - sl[k]).max() / max(np.abs(sl[k]).max(), 1e-30))
+                      for k in range(comparable))
+            row["tokens_same_as_scalar"] = same
+            row["max_rel_vs_scalar"] = float(f"{rel:.3e}")
+        rows.append(row)
+        log(f"[bench] CPU ladder {row['kernels']:>6}/{t:<3} prefill {row['prefill_tps']:8.2f} tok/s, decode "
+            f"{row['decode_tps']:8.2f} tok/s"
+            + (f", {'bit-identical to' if row['bit_identical_to_1_thread'] else 'DIFFERS from'} 1 thread"
+               if t > 1 else "")
+            + (f", vs scalar: logits rel {row['max_rel_vs_scalar']:.1e}, tokens {row['tokens_same_as_scalar']}/{n}"
+               if be != O.SCALAR else ""))
+    return value, threads, rows
 
 
 def cpu_topology() -> tuple[int, int]:
@@ -365,16 +399,22 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         t1 = time.time()
-        cpu_tps, threads, cpu1 = cpu_baseline(model, prompt)
+        cpu_tps, threads, ladder = cpu_baseline(model, prompt)
         phys, logical = cpu_topology()
-        log(f"[bench] CPU baseline: {cpu_tps:.2f} tok/s on {threads} threads, {cpu1:.2f} tok/s on 1 thread "
-            f"({time.time() - t1:.1f}s); {cpu_model_name()}, {phys} physical / {logical} logical CPUs")
+        one = next(r["decode_tps"] for r in ladder if r["kernels"] == "avx2" and r["threads"] == 1)
+        identical = all(r.get("bit_identical_to_1_thread", True) for r in ladder)
+        tokens_ok = all(r.get("tokens_same_as_scalar", CPU_STEPS) == CPU_STEPS for r in ladder)
+        log(f"[bench] CPU baseline: {cpu_tps:.2f} tok/s on {threads} threads, {one:.2f} tok/s on 1 thread "
+            f"({time.time() - t1:.1f}s); thread-count invariance {'PASS' if identical else 'FAIL'}, avx2 tokens "
+            f"{'equal' if tokens_ok else 'DIFFER from'} scalar/1; {cpu_model_name()}, {phys} physical / "
+            f"{logical} logical CPUs")
         cpu = {"value": round(cpu_tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-               "value_1_thread": round(cpu1, 3), "physical_cores": phys, "logical_cpus": logical,
-               "cpu_model": cpu_model_name(),
+               "value_1_thread": one, "physical_cores": phys, "logical_cpus": logical,
+               "cpu_model": cpu_model_name(), "ladder": ladder, "ladder_bit_identical": identical,
+               "ladder_tokens_match_scalar": tokens_ok,
                "sample": f"one sequence, 23-token prompt + 32 greedy steps (tok/s = 31/decode_s), full config-5 "
-                         f"weights, oracle AVX2 + thread pool; median of {CPU_RUNS['threads']} runs, and of "
-                         f"{CPU_RUNS['one']} runs on 1 thread as value_1_thread"}
+                         f"weights, oracle AVX2 + thread pool, median of {CPU_RUNS} runs; then the reference's "
+                         f"ladder (src/bench_decode.cpp:62-137), one run per row"}
 
     out = {
         "metric": "decode tok/s at TinyLlama-1.1B shapes B=1/64; Q4_0 matvec GB/s % of HBM peak",

@@ -27,27 +27,27 @@ def _top2_margin(l):
     return float(s[-1] - s[-2])
 
 
-# The reference's near-tie rule for greedy parity (README.md:603-607, src/verify_chat.cpp:193-216):
-# token sequences must be identical, and a difference is tolerated only where the checker's own
-# top-1 / top-2 logit margin at the first differing step is below 1e-3.
+# The reference's checker tolerates a greedy difference where its own top-1 / top-2 logit margin
+# at the first differing step is below 1e-3 (README.md:603-607, src/verify_chat.cpp:193-216).  The
+# committed seeds are held to the stricter bar: identical ids at every step, no tolerated flip.
+# The smallest oracle margin over the compared steps is printed (pytest -s) and returned, so a
+# run shows how close the closest call came.
 NEAR_TIE = 1e-3
 
 
 def assert_greedy_identical(got, want, want_logits, label=""):
-    """Identical greedy ids, or a first difference at a near-tie of the oracle's logits (then the
-    rest of the sequence is not comparable).  Returns (minimum top-2 margin over the compared steps,
-    first differing step or None)."""
+    """Identical greedy ids over every step.  Returns the minimum top-2 margin of the oracle's
+    logits over the steps.  A difference fails, and the message says whether the reference's
+    near-tie rule would have tolerated it."""
     got = [int(v) for v in got]
     want = [int(v) for v in want]
     margins = [_top2_margin(l) for l in want_logits[:len(want)]]
     k = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
-    if k is None:
-        print(f"{label} greedy ids identical over {len(want)} steps; min top-2 margin {min(margins):.3e}", flush=True)
-        return min(margins), None
-    assert margins[k] < NEAR_TIE, (f"{label} greedy ids differ at step {k} ({got[k]} vs {want[k]}) where the "
-                                   f"oracle's top-2 margin {margins[k]:.3e} is not a near-tie (< {NEAR_TIE})")
-    print(f"{label} near-tie flip at step {k}: margin {margins[k]:.3e} (tolerated, README.md:603-607)", flush=True)
-    return min(margins[:k + 1]), k
+    assert k is None, (f"{label} greedy ids differ at step {k} ({got[k]} vs {want[k]}); the oracle's "
+                       f"top-2 margin there is {margins[k]:.3e}"
+                       + (" (a near-tie the reference's checker would tolerate)" if margins[k] < NEAR_TIE else ""))
+    print(f"{label} greedy ids identical over {len(want)} steps; min top-2 margin {min(margins):.3e}", flush=True)
+    return min(margins)
 
 
 @pytest.mark.parametrize("cfg,q8", [(SMALL, {(0, "wk"), (1, "wv"), (2, "w_down")}), (ODD, {(1, "wq")}),
@@ -101,8 +101,7 @@ def test_config5_greedy_32_steps_identical(tinyllama):
     eng = Engine(dm, max_seq=23 + 32)
     got, pre, dec = eng.generate([prompt], 32)
     print(f"greedy tokens {got[0].tolist()}", flush=True)
-    _, flip = assert_greedy_identical(got[0], want, want_logits, "config 5 B=1:")
-    assert flip is None or flip > 0
+    assert_greedy_identical(got[0], want, want_logits, "config 5 B=1:")
     # logits of every decode step (teacher-forced on the same tokens)
     seq = prompt + want.tolist()
     for p in range(len(prompt) + 31):
@@ -185,16 +184,13 @@ def test_config5_batched_greedy_32_steps_match_oracle(tinyllama, B):
     for b in check:
         toks, logits, _, _ = om.run_once(prompts[b], n)
         want[b] = (toks, logits)
-        _, flip = assert_greedy_identical(got[b], toks, logits, f"config 5 B={B} seq {b}:")
-        assert flip is None or flip > 0, b
+        assert_greedy_identical(got[b], toks, logits, f"config 5 B={B} seq {b}:")
     # every decode step's logits on the generated tokens (teacher forced, all sequences at once)
     seqs = np.concatenate([prompts, got], axis=1)
     tf = _teacher_forced_logits(eng, [seqs[:, p] for p in range(23 + n - 1)], 22)
     worst = 0.0
     for b in check:
         toks, logits = want[b]
-        if got[b].tolist() != toks.tolist():
-            continue  # a tolerated near-tie: the oracle followed another sequence
         for k in range(n):
             e = _logit_err(tf[22 + k][b], logits[k])
             worst = max(worst, e)
@@ -300,11 +296,12 @@ def test_long_context_decode_matches_oracle(hip):
     eng.close()
 
 
-@pytest.mark.parametrize("kind", ["wave", "head"])
+@pytest.mark.parametrize("kind", ["wave", "head", "split"])
 def test_decode_attention_across_the_first_chunk_matches_oracle(hip, kind, monkeypatch):
     """Greedy decode from a 58-token prompt through positions 58..69, across the 64-position
-    boundary where the one-wave kernel moves from the rows it loads at entry to loaded chunks;
-    forced per kernel, tokens and every step's logits match the oracle."""
+    boundary where the one-wave kernel moves from the rows it loads at entry to loaded chunks (and
+    the position-split kernel from one split to two, combined by the last to arrive); forced per
+    kernel, tokens and every step's logits match the oracle."""
     print(f"[case] decode across position 64, attention={kind}", flush=True)
     monkeypatch.setenv("EF_HIP_ATTENTION", kind)
     dm = DeviceModel.synthetic(LONG, seed=31)

@@ -59,6 +59,35 @@ def test_gemv_config1_quantized_weights(hip, qtype):
     assert err.max() < REL_TOL
 
 
+@pytest.fixture(scope="module")
+def lm_head_q8():
+    """Config 3's lm_head: 32000x2048 from N(0,0.02), quantized Q8_0 by the oracle's quantizer
+    (src/quant.cpp:95-125), with its float64 decode."""
+    packed = O.quantize(O.Q8_0, D.normal(31, (32000, 2048), 0.02))
+    return packed, D.dequant_exact(O.Q8_0, packed, 2048)
+
+
+@pytest.mark.parametrize("batch", [1, 16, 64])
+def test_gemv_config3_lm_head_q8_0(hip, lm_head_q8, batch):
+    """The Q8_0 lm_head product on its own (src/model.cpp:272-275 -> kern::matvec): hidden vectors
+    from N(0,1), one sequence (config 3) and the batched decode's 16 and 64 (config 4).  Every
+    sequence meets both gates against the oracle's AVX2 kernel and the exact dot."""
+    packed, w64 = lm_head_q8
+    print(f"[case] Q8_0 lm_head 32000x2048 B={batch}", flush=True)
+    X = np.stack([D.normal(32 + b, 2048) for b in range(batch)])
+    got = _gemv(hip, O.Q8_0, packed, X, batch=batch)
+    x64 = X.T.astype(np.float64)
+    exact = w64 @ x64
+    mag = np.abs(w64) @ np.abs(x64)
+    rel = np.abs(got.T.astype(np.float64) - exact) / np.maximum(mag, 1e-30)
+    assert rel.max() < REL_TOL, rel.max()
+    pool = O.Pool(8)
+    for b in range(batch):
+        cpu = O.matvec(O.Q8_0, packed.reshape(-1), X[b], backend=O.AVX2, pool=pool)
+        assert np.abs(got[b] - cpu).max() <= ABS_TOL, b
+    pool.close()
+
+
 def test_gemv_edge_codes(hip):
     """tests/test_qinfer.cpp:100-122 on the device: nibble layout, zero scale, Q8 extremes."""
     blk = np.zeros(18, np.uint8)
