@@ -30,7 +30,10 @@
 
 namespace {
 constexpr uint32_t kEngineMagic = 0x45464845u;  // "EFHE"
-enum StepMode : int { kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32, kAllLogits = 64 };
+enum StepMode : int {
+  kLogits = 1, kGreedy = 2, kSample = 4, kAdvance = 8, kPrefill = 16, kEos = 32, kAllLogits = 64,
+  kSplit = 128  // decode attention by the position-split kernels (a step at a position >= kSplitFrom)
+};
 // Kernel groups of a decode step (the reference's ForwardProfile buckets, include/ef/model.h:89-94,
 // merged where this build fuses them): a step enqueues the groups its mask selects, so a profile
 // can capture and time each group's launches on their own.
@@ -45,6 +48,10 @@ enum StepGroup : unsigned {
   kGPick = 1u << EF_HIP_PROF_PICK,
   kAllGroups = (1u << EF_HIP_PROF_GROUPS) - 1u,
 };
+// Decode positions from which a step uses the position-split attention (when the engine has its
+// workspace): below, the single-pass kernels are faster (measured crossover: about 130 positions at
+// B = 1, 210 at B = 16, TinyLlama shapes).
+constexpr size_t kSplitFrom = 192;
 // Rows (sequences x positions) of one batched prefill launch; longer prompts go in chunks.
 constexpr size_t kPrefillRows = 4096;
 }  // namespace
@@ -63,6 +70,10 @@ struct ef_hip_engine_s {
   float* rope_now = nullptr;  // RoPE's cos / sin rows at the step's position (written by embed_at)
   int32_t *hist = nullptr, *hist_len = nullptr, *next_tok = nullptr, *pos = nullptr, *n_prompt = nullptr;
   uint32_t* step_counter = nullptr;  // zero between steps (argmax_finish re-arms it)
+  // position-split decode attention (long caches, few sequences): partial results, or null when
+  // the step does not split
+  float* attn_part = nullptr;
+  int attn_splits = 1, attn_span = 0;
   int32_t* out_tokens = nullptr;
   void* sample_ws = nullptr;
   void* gemv_ws = nullptr;  // prepared activation fragments of the batched GEMVs (B > 1)
@@ -152,7 +163,7 @@ int put_tokens(ef_hip_engine e, size_t pos, size_t n) {
                           static_cast<int>(n), e->B, e->stream);
 }
 
-AttnArgs attn_args(ef_hip_engine e) {
+AttnArgs attn_args(ef_hip_engine e, bool split) {
   const ef_hip_model_config& c = e->c;
   AttnArgs a{};
   a.q = e->q;
@@ -169,6 +180,9 @@ AttnArgs attn_args(ef_hip_engine e) {
   a.hd = static_cast<int>(c.hd);
   a.max_seq = static_cast<int>(e->max_seq);
   a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.hd)));  // src/kernels.cpp:158
+  a.part = split ? e->attn_part : nullptr;
+  a.splits = e->attn_splits;
+  a.span = e->attn_span;
   return a;
 }
 
@@ -292,7 +306,7 @@ int build_staged(ef_hip_engine e) {
 }
 
 // The layers of a several-sequence step over staged tables.
-int enqueue_staged_layers(ef_hip_engine e, unsigned groups) {
+int enqueue_staged_layers(ef_hip_engine e, unsigned groups, bool split) {
   const ef_hip_model_config& c = e->c;
   const int B = e->B;
   const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
@@ -304,7 +318,7 @@ int enqueue_staged_layers(ef_hip_engine e, unsigned groups) {
     EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
                            e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now, &em));
   }
-  AttnArgs a = attn_args(e);
+  AttnArgs a = attn_args(e, split);
   const bool group_attn = attention_uses_group(a, B);
   for (size_t l = 0; l < c.L; ++l) {
     const ef_hip_layer& w = e->layers[l];
@@ -347,13 +361,13 @@ int enqueue_step(ef_hip_engine e, int mode, unsigned groups = kAllGroups) {
   const size_t D = c.D, F = c.F, kvd = e->kvd, S = e->max_seq;
   hipStream_t s = e->stream;
   if (e->staged) {
-    EFH_RC(enqueue_staged_layers(e, groups));
+    EFH_RC(enqueue_staged_layers(e, groups, (mode & kSplit) != 0));
     return enqueue_tail(e, mode, groups, true);
   }
   if (groups & kGEmbed)
     EFH_RC(launch_embed_at(e->embed, e->hist, static_cast<long>(S), e->pos, B, e->x, static_cast<long>(D), s,
                            e->cos_t, e->sin_t, static_cast<int>(c.hd / 2), e->rope_now));
-  AttnArgs a = attn_args(e);
+  AttnArgs a = attn_args(e, (mode & kSplit) != 0);
   for (size_t l = 0; l < c.L; ++l) {
     const ef_hip_layer& w = e->layers[l];
     const GemvJob qkv[3] = {{w.wq, nullptr, e->x, e->q, D, D},
@@ -563,6 +577,11 @@ int graph_for(ef_hip_engine e, int mode, hipGraphExec_t* out) {
   return EF_HIP_OK;
 }
 
+// The step mode for a decode step at position pos: with the split bit from kSplitFrom on.
+int at_pos(ef_hip_engine e, int mode, size_t pos) {
+  return e->attn_part != nullptr && pos >= kSplitFrom ? mode | kSplit : mode;
+}
+
 // Bounds the retired executables (a long chat that keeps changing sampler settings): past 256, the
 // older half is destroyed after the stream has drained.
 int trim_retired(ef_hip_engine e) {
@@ -719,6 +738,17 @@ int ef_hip_engine_create(const ef_hip_model_config* cfg, const ef_hip_layer* lay
     return cleanup_fail(fail(EF_HIP_ENOMEM, "engine sampler workspace"));
   e->allocs.push_back(ws);
   e->sample_ws = ws;
+  {
+    int splits = 1, span = 0;
+    size_t part = 0;
+    if (attention_split_plan(static_cast<int>(c.H), static_cast<int>(c.KV), static_cast<int>(c.hd),
+                             static_cast<int>(S), batch, &splits, &span, &part) &&
+        !attention_uses_group(attn_args(e, false), batch)) {
+      if ((rc = dev_alloc(e, &e->attn_part, part))) return cleanup_fail(rc);
+      e->attn_splits = splits;
+      e->attn_span = span;
+    }
+  }
   if (B > 1) {  // the largest workspace any of the step's batched GEMVs plans for
     size_t need = 0;
     for (size_t l = 0; l < c.L; ++l) {
@@ -814,7 +844,7 @@ int ef_hip_engine_forward(ef_hip_engine e, const int32_t* tokens, size_t pos, in
   e->stage[e->B] = static_cast<int32_t>(pos);
   EFH_RC(put_tokens(e, pos, 1));
   EFH_HIP(hipMemcpyAsync(e->pos, e->tok_dev + e->B, 4, hipMemcpyDeviceToDevice, e->stream));
-  EFH_RC(run_step(e, compute_logits ? kLogits : 0));
+  EFH_RC(run_step(e, at_pos(e, compute_logits ? kLogits : 0, pos)));
   EFH_HIP(hipStreamSynchronize(e->stream));
   e->cached = pos + 1;
   return EF_HIP_OK;
@@ -903,25 +933,31 @@ int ef_hip_engine_generate(ef_hip_engine e, const int32_t* prompt, size_t n_prom
   // product at once) or, with EF_HIP_PREFILL=serial, the reference's one position at a time
   // (src/model.cpp:290).  Graphs are instantiated before the clock starts.
   const bool batched = n_prompt >= 2 && batched_prefill_enabled();
-  hipGraphExec_t g_pre = nullptr, g_dec;
+  // step graphs for positions below and from kSplitFrom (the same graph when the engine does not
+  // split), instantiated before the clock starts
+  hipGraphExec_t g_pre[2] = {nullptr, nullptr}, g_dec[2];
   if (batched) {
     EFH_RC(run_prefill(e, n_prompt, kLogits | pick, true));
   } else {
-    EFH_RC(graph_for(e, kAdvance, &g_pre));
+    EFH_RC(graph_for(e, kAdvance, &g_pre[0]));
+    EFH_RC(graph_for(e, at_pos(e, kAdvance, S), &g_pre[1]));
   }
-  EFH_RC(graph_for(e, kLogits | pick, &g_dec));
+  EFH_RC(graph_for(e, kLogits | pick, &g_dec[0]));
+  EFH_RC(graph_for(e, at_pos(e, kLogits | pick, S), &g_dec[1]));
+  auto pre_at = [&](size_t p) { return g_pre[at_pos(e, 0, p) != 0]; };
+  auto dec_at = [&](size_t p) { return g_dec[at_pos(e, 0, p) != 0]; };
   EFH_HIP(hipStreamSynchronize(e->stream));
   using Clock = std::chrono::steady_clock;
   const auto t0 = Clock::now();
   if (batched) {
     EFH_RC(run_prefill(e, n_prompt, kLogits | pick, false));  // ends with logits and the first pick
   } else {
-    for (size_t p = 0; p + 1 < n_prompt; ++p) EFH_HIP(hipGraphLaunch(g_pre, e->stream));
-    EFH_HIP(hipGraphLaunch(g_dec, e->stream));  // last prompt position: logits and the first pick
+    for (size_t p = 0; p + 1 < n_prompt; ++p) EFH_HIP(hipGraphLaunch(pre_at(p), e->stream));
+    EFH_HIP(hipGraphLaunch(dec_at(n_prompt - 1), e->stream));  // last prompt position: logits and the first pick
   }
   EFH_HIP(hipStreamSynchronize(e->stream));
   const auto t1 = Clock::now();
-  for (size_t k = 1; k < n; ++k) EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+  for (size_t k = 1; k < n; ++k) EFH_HIP(hipGraphLaunch(dec_at(n_prompt - 1 + k), e->stream));
   EFH_HIP(hipStreamSynchronize(e->stream));
   const auto t2 = Clock::now();
   // [B][S] -> [B][n] on the device, then one contiguous copy to the caller
@@ -946,10 +982,10 @@ int ef_hip_engine_profile(ef_hip_engine e, const ef_hip_sampler_config* cfg, voi
     EFH_RC(set_sampler(e, *cfg, rng));
     pick = kSample;
   }
-  const int mode = kLogits | pick;
   // every group runs at position P (its token and cache rows are in bounds); only the pick group
   // moves the position, and it is put back after each group
   const int32_t P = static_cast<int32_t>(std::min(e->cached, e->max_seq - 1));
+  const int mode = at_pos(e, kLogits | pick, static_cast<size_t>(P));
   auto set_pos = [&]() -> int {
     EFH_HIP(hipStreamSynchronize(e->stream));
     e->stage[0] = P;
@@ -1135,9 +1171,11 @@ int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids, size_t n_ids, const
   const int mode = kLogits | kSample | kEos;
   const size_t n_pre = n_ids - lcp;
   const bool batched = n_pre >= 2 && batched_prefill_enabled();
-  hipGraphExec_t g_dec;
+  hipGraphExec_t g_dec[2];
   if (batched) EFH_RC(run_prefill(e, n_pre, mode, true));
-  EFH_RC(graph_for(e, mode, &g_dec));
+  EFH_RC(graph_for(e, mode, &g_dec[0]));
+  EFH_RC(graph_for(e, at_pos(e, mode, S), &g_dec[1]));
+  auto dec_at = [&](size_t p) { return g_dec[at_pos(e, 0, p) != 0]; };
   const size_t max_new = std::min(o->max_new, S - n_ids);
   const size_t window = static_cast<size_t>(std::max(1, o->steps_per_check));
   std::vector<int32_t> toks(max_new);
@@ -1153,8 +1191,8 @@ int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids, size_t n_ids, const
   if (batched) {
     EFH_RC(run_prefill(e, n_pre, mode, false));  // ends with the first pick
   } else {
-    for (size_t p = lcp; p + 1 < n_ids; ++p) EFH_RC(run_step(e, kAdvance));
-    EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+    for (size_t p = lcp; p + 1 < n_ids; ++p) EFH_RC(run_step(e, at_pos(e, kAdvance, p)));
+    EFH_HIP(hipGraphLaunch(dec_at(n_ids - 1), e->stream));
   }
   EFH_HIP(hipStreamSynchronize(e->stream));
   const auto t1 = Clock::now();
@@ -1162,7 +1200,7 @@ int ef_hip_engine_reply(ef_hip_engine e, const int32_t* ids, size_t n_ids, const
   int reason = 0;
   while (reason == 0) {
     const size_t w1 = std::min(max_new, w0 + window);
-    for (; picks < w1; ++picks) EFH_HIP(hipGraphLaunch(g_dec, e->stream));
+    for (; picks < w1; ++picks) EFH_HIP(hipGraphLaunch(dec_at(n_ids - 1 + picks), e->stream));
     EFH_HIP(hipMemcpyAsync(toks.data() + w0, e->out_tokens + w0, (w1 - w0) * 4, hipMemcpyDeviceToHost, e->stream));
     EFH_HIP(hipMemcpyAsync(peos.data() + w0, e->eos_out + w0, (w1 - w0) * 8, hipMemcpyDeviceToHost, e->stream));
     EFH_HIP(hipStreamSynchronize(e->stream));

@@ -23,6 +23,11 @@ struct AttnArgs {
   int pre_vrows;        // set by launch_attention: the first chunk's V rows have their own LDS
   int chunk;            // set by launch_attention: rows of the LDS staging buffer (>= 64)
   AEmit em;             // KV-group kernel: ctx also staged as the o-projection's tables (afrag.h)
+  // Position-split decode (attention_split_kernel, then attention_combine_kernel): `splits`
+  // workgroups per (sequence, KV group), each over `span` positions; part holds their partial
+  // results.  part == nullptr: no split.
+  float* part;
+  int splits, span;
 };
 
 // Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of
@@ -41,6 +46,11 @@ int launch_embed_at(const ef_hip_weight_s* W, const int32_t* hist, long hist_ld,
                     float* out, long ldo, hipStream_t s, const float* cos_t = nullptr, const float* sin_t = nullptr,
                     int half = 0, float* rope_now = nullptr, const AEmit* em = nullptr);
 size_t attention_lds_bytes(int hd, int max_seq);
+// The position split for a decode step of `batch` sequences: whether it applies (hd = 64, at most 8
+// query heads per KV head, more than one 64-position chunk of cache) and its splits / span (the
+// smallest multiple of 64 positions that needs no more splits than the combine takes: 64 up to
+// 2048 positions at 8 heads per KV head).  part_floats: the workspace it needs.
+bool attention_split_plan(int H, int KV, int hd, int max_seq, int batch, int* splits, int* span, size_t* part_floats);
 int launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 // Whether launch_attention runs the KV-group kernel (the one that can stage ctx as tables).
 bool attention_uses_group(const AttnArgs& a, int batch);

@@ -636,6 +636,344 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
   }
 }
 
+// Position-split decode attention (hd = 64, at most 8 query heads per KV head): workgroup
+// (j, g, b) takes positions [j span, (j + 1) span) of KV group g of sequence b, up to the current
+// position, for all of the group's query heads (the cache rows are read once per group).  Its
+// scores follow kern::dot_f32's order (src/kernels.cpp:27-43); with several splits active each one
+// keeps its own maximum m_j, float exp(s - m_j), their double sum l_j and the unnormalised
+// o_j[d] = sum_t e_t v_t[d] (positions in order) in a record, and attention_combine_kernel adds the
+// splits in index order: M = max m_j, w_j = exp(m_j - M), out[d] = (sum_j w_j o_j[d]) *
+// float(1 / sum_j w_j l_j).  The order is fixed, so results are reproducible; they differ from the
+// reference's single pass (src/kernels.cpp:153-174) by the rounding of the regrouped sums.  With
+// one split active (positions < span) the workgroup runs the reference's softmax_inplace and p.v
+// order itself and writes ctx directly.  Split 0 always has work and requests its rows before it
+// reads the position; the others read it first and leave at once when they have none.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitRows = 64;     // cache rows staged in LDS at a time (the span is a multiple)
+constexpr int kSplitHd = 64;
+constexpr int kSplitMaxHpg = 8;
+constexpr int kSplitRec = kSplitMaxHpg * kSplitHd + kSplitMaxHpg + 2 * kSplitMaxHpg;  // o, m, l (doubles)
+constexpr int kSplitLd = kSplitHd + 4;  // floats between staged rows
+constexpr int kSplitPerThread = 16;  // splits whose o columns one thread holds in the combine
+constexpr int kSplitMaxSplits = 64;  // splits of one (sequence, group): the combine's wave lanes
+// Combine kernel LDS: sums (doubles) and weights per (split, head), tpc x cols float4 sub-sums,
+// 1 / sum per head.
+constexpr size_t kCombineLds =
+    (2 * kSplitMaxSplits * kSplitMaxHpg + kSplitMaxSplits * kSplitMaxHpg + 4 * kSplitThreads + kSplitMaxHpg) *
+    sizeof(float);
+// The most splits the combine takes for hpg query heads per KV head (tpc threads per column).
+__host__ __device__ constexpr int split_max(int hpg) {
+  return kSplitPerThread * (kSplitThreads / (hpg * kSplitHd / 4)) < kSplitMaxSplits
+             ? kSplitPerThread * (kSplitThreads / (hpg * kSplitHd / 4))
+             : kSplitMaxSplits;
+}
+
+size_t attention_split_lds_bytes(int hpg, int span) {
+  return (static_cast<size_t>(hpg + 2) * kSplitHd + 2 * kSplitRows * kSplitLd + static_cast<size_t>(hpg) * span +
+          3 * kSplitMaxHpg) *
+         sizeof(float);
+}
+
+template <bool EAGER>
+__global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int j = blockIdx.x, g = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int hpg = a.H / a.KV, kvd = a.KV * kSplitHd, span = a.span;
+  float* qs = sm;                                 // [hpg][64] roped queries
+  float* kn = qs + hpg * kSplitHd;                // [64] roped new key
+  float* vn = kn + kSplitHd;                      // [64] new value
+  float* rows = vn + kSplitHd;                    // [64][kSplitLd] K rows (later sub-chunks: K or V)
+  float* vrows = rows + kSplitRows * kSplitLd;    // [64][kSplitLd] the first sub-chunk's V rows
+  float* sc = vrows + kSplitRows * kSplitLd;      // [hpg][span] scores, then exponentials
+  double* s_l = reinterpret_cast<double*>(sc + hpg * span);  // [8] sums (span, hpg: even offset)
+  float* s_m = reinterpret_cast<float*>(s_l + kSplitMaxHpg);  // [8] maxima
+  const long seq0 = static_cast<long>(b) * a.max_seq * kvd + g * kSplitHd;
+  const float* kc = a.kcache + seq0;
+  const float* vc = a.vcache + seq0;
+  const int c0 = j * span, n_first = min(kSplitRows, a.max_seq - c0);  // c0 < max_seq (host plan)
+
+  // Loads that do not need the position go first, behind the position itself (a vector load, so
+  // that waiting for it leaves the later ones in flight): the group's queries, RoPE's row at pos,
+  // the new k / v, and (split 0 always, every split with EAGER) the first sub-chunk's cache rows.
+  // Without EAGER, the other splits request their rows once the position shows they have work.
+  const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.pos_dev, 4u), 0u, 0u, 0);
+  const float* q = a.q + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
+  const float* k_new = a.knew + static_cast<long>(b) * kvd + g * kSplitHd;
+  const int hq = t >> 5, iq = t & 31;
+  float qa = 0.0f, qb = 0.0f, cq = 0.0f, sq = 0.0f, ka = 0.0f, kb = 0.0f, vnew = 0.0f;
+  if (t < hpg * (kSplitHd / 2)) {
+    qa = q[hq * kSplitHd + iq];
+    qb = q[hq * kSplitHd + iq + 32];
+  }
+  if (t < hpg * (kSplitHd / 2) || t < kSplitHd) {
+    cq = a.rope_now[iq];
+    sq = a.rope_now[kSplitHd / 2 + iq];
+  }
+  if (t < kSplitHd) {
+    ka = k_new[t & 31];
+    kb = k_new[(t & 31) + 32];
+    vnew = a.vnew[static_cast<long>(b) * kvd + g * kSplitHd + t];
+  }
+  float4 pk[4], pv[4];
+  auto prefetch = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = t + kSplitThreads * i, r = idx >> 4, c = idx & 15;
+      if (r < n_first) {
+        pk[i] = reinterpret_cast<const float4*>(kc + static_cast<long>(c0 + r) * kvd)[c];
+        pv[i] = reinterpret_cast<const float4*>(vc + static_cast<long>(c0 + r) * kvd)[c];
+      }
+    }
+  };
+  if (EAGER || j == 0) prefetch();
+  const int pos = __builtin_amdgcn_readfirstlane(pos_v);
+  if (j * span > pos) return;  // no positions for this split
+  if (!EAGER && j != 0) prefetch();
+  const int n_pos = pos + 1, n_act = (n_pos + span - 1) / span;
+  const bool last = j == n_act - 1;
+  const int n_loc = min(span, n_pos - c0);
+
+  // RoPE on the group's queries (one pair per thread) and, in the split holding pos, on the new
+  // key; that split publishes k / v at pos for later steps (src/kernels.cpp:133-146)
+  if (t < hpg * (kSplitHd / 2)) {
+    qs[hq * kSplitHd + iq] = qa * cq - qb * sq;
+    qs[hq * kSplitHd + iq + 32] = qb * cq + qa * sq;
+  }
+  if (last && t < kSplitHd) {
+    const float k = t < 32 ? ka * cq - kb * sq : kb * cq + ka * sq;
+    kn[t] = k;
+    vn[t] = vnew;
+    a.kcache[seq0 + static_cast<long>(pos) * kvd + t] = k;
+    a.vcache[seq0 + static_cast<long>(pos) * kvd + t] = vnew;
+  }
+  __syncthreads();
+  // staged rows past the split's last position are zeros: p.v runs over whole 64-row sub-chunks
+  // with p = 0 there (adding 0 * 0 leaves a sum unchanged)
+  const int n0 = min(kSplitRows, n_loc);
+  const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + kSplitThreads * i, r = idx >> 4, c = idx & 15;
+    float4 kv = zero4, vv = zero4;
+    if (r < n0) {
+      kv = pk[i];
+      vv = pv[i];
+      if (c0 + r == pos) {
+        kv = reinterpret_cast<const float4*>(kn)[c];
+        vv = reinterpret_cast<const float4*>(vn)[c];
+      }
+    }
+    reinterpret_cast<float4*>(rows + r * kSplitLd)[c] = kv;
+    reinterpret_cast<float4*>(vrows + r * kSplitLd)[c] = vv;
+  }
+  auto stage = [&](const float* cache, const float* cur_row, int s0, int n) {
+    for (int idx = t; idx < kSplitRows * 16; idx += kSplitThreads) {
+      const int r = idx >> 4, c = idx & 15, tp = c0 + s0 + r;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (r < n) v = reinterpret_cast<const float4*>(tp == pos ? cur_row : cache + static_cast<long>(tp) * kvd)[c];
+      reinterpret_cast<float4*>(rows + r * kSplitLd)[c] = v;
+    }
+  };
+
+  // scores: a wave per (head, 64 positions), positions across the lanes
+  for (int s0 = 0; s0 < n_loc; s0 += kSplitRows) {
+    const int n = min(kSplitRows, n_loc - s0);
+    if (s0 > 0) stage(kc, kn, s0, n);
+    __syncthreads();
+    for (int pr = t; pr < hpg * kSplitRows; pr += kSplitThreads) {
+      const int hh = pr >> 6, r = pr & 63;
+      if (r < n) sc[hh * span + s0 + r] = dot_f32_lds(qs + hh * kSplitHd, rows + r * kSplitLd, kSplitHd) * a.scale;
+    }
+    __syncthreads();
+  }
+  // softmax over the split's positions: a wave per head (max, float exp, double sum)
+  {
+    const int wave = t / kWave, lane = t & (kWave - 1);
+    for (int hh = wave; hh < hpg; hh += kSplitThreads / kWave) {
+      float* sh = sc + hh * span;
+      float mx = -INFINITY;
+      for (int p = lane; p < n_loc; p += kWave) mx = fmaxf(mx, sh[p]);
+      mx = wave_max_dpp(mx);
+      double l = 0.0;
+      for (int p = lane; p < n_loc; p += kWave) {
+        const float e = expf(sh[p] - mx);
+        sh[p] = e;
+        l += static_cast<double>(e);
+      }
+      l = wave_sum_d_dpp(l);
+      if (lane == 0) {
+        s_m[hh] = mx;
+        s_l[hh] = l;
+      }
+    }
+  }
+  __syncthreads();
+  // p.v: thread -> (head, dimension) outputs, positions in order; one split: p = e * float(1 / l)
+  // (softmax_inplace), several: the unnormalised e
+  float o[2] = {0.0f, 0.0f}, inv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int hh = (t + u * kSplitThreads) >> 6;
+    inv[u] = hh < hpg && n_act == 1 ? static_cast<float>(1.0 / s_l[hh]) : 1.0f;
+  }
+  // (a wave's outputs share one head: lane r holds p of row r, broadcast by readlane)
+  for (int s0 = 0; s0 < n_loc; s0 += kSplitRows) {
+    const int n = min(kSplitRows, n_loc - s0);
+    const float* vr = s0 == 0 ? vrows : rows;
+    if (s0 > 0) {
+      stage(vc, vn, s0, n);
+      __syncthreads();
+    }
+    const int lane = t & (kWave - 1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = t + u * kSplitThreads, hh = idx >> 6, d = idx & 63;
+      if (hh < hpg) {
+        const int pl = __float_as_int(lane < n ? sc[hh * span + s0 + lane] * inv[u] : 0.0f);
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r) {
+          const float p = __int_as_float(__builtin_amdgcn_readlane(pl, r));
+          o[u] += p * vr[r * kSplitLd + d];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
+  if (n_act == 1) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = t + u * kSplitThreads;
+      if (idx < hpg * kSplitHd) out[idx] = o[u];
+    }
+    return;
+  }
+  float* recs = a.part + static_cast<long>(b * a.KV + g) * a.splits * kSplitRec;
+  {
+    float* rec = recs + static_cast<long>(j) * kSplitRec;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = t + u * kSplitThreads;
+      if (idx < hpg * kSplitHd) rec[idx] = o[u];
+    }
+    if (t < hpg) {
+      rec[kSplitMaxHpg * kSplitHd + t] = s_m[t];
+      reinterpret_cast<double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[t] = s_l[t];
+    }
+  }
+}
+
+// The combine of the position-split attention: one workgroup per (KV group g, sequence b), after
+// the split kernel (the kernel boundary makes every split's record visible).  With one split
+// active the split kernel has written ctx itself and this returns at once.
+template <bool EAGER>
+__global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int hpg = a.H / a.KV;
+  const float* recs = a.part + static_cast<long>(b * a.KV + g) * a.splits * kSplitRec;
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
+  // Thread (sub, col) holds float4 column col of o for splits sub * per .. sub * per + per - 1
+  // (per from the split count, so the grouping does not depend on the position), all requested
+  // at once; the splits' maxima and sums go to LDS, a wave per head forms the weights (lanes =
+  // splits), each thread sums its splits in order, and the sub-sums are added in sub order.
+  // With EAGER the records are requested before the position is known (every record is in
+  // bounds; those of inactive splits are never used).
+  const int cols = hpg * kSplitHd / 4, tpc = kSplitThreads / cols, per = (a.splits + tpc - 1) / tpc;
+  const int col = t % cols, sub = t / cols;
+  const bool active = sub < tpc;
+  double* cl = reinterpret_cast<double*>(sm);                                  // [n_act][hpg] sums
+  float* cw = reinterpret_cast<float*>(cl + kSplitMaxSplits * kSplitMaxHpg);   // [n_act][hpg] maxima, then weights
+  float4* cred = reinterpret_cast<float4*>(cw + kSplitMaxSplits * kSplitMaxHpg);  // [tpc][cols] sub-sums
+  float* cinv = reinterpret_cast<float*>(cred + kSplitThreads);                 // [hpg] 1 / sum_j w_j l_j
+  float4 ov[kSplitPerThread];
+  auto fetch = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kSplitPerThread; ++q) {
+      const int sj = sub * per + q;
+      if (active && q < per && sj < a.splits)
+        ov[q] = reinterpret_cast<const float4*>(recs + static_cast<long>(sj) * kSplitRec)[col];
+    }
+  };
+  // the maxima and sums: (split, head) pairs t and t + 256 (at most 64 x 8 pairs)
+  float mv[2];
+  double lv[2];
+  auto fetch_ml = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = t + k * kSplitThreads, sj = i / hpg, hh = i - sj * hpg;
+      if (sj < a.splits) {
+        const float* rec = recs + static_cast<long>(sj) * kSplitRec;
+        mv[k] = rec[kSplitMaxHpg * kSplitHd + hh];
+        lv[k] = reinterpret_cast<const double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[hh];
+      }
+    }
+  };
+  const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.pos_dev, 4u), 0u, 0u, 0);
+  if (EAGER) {
+    fetch_ml();
+    fetch();
+  }
+  const int n_act = (__builtin_amdgcn_readfirstlane(pos_v) + a.span) / a.span;  // ceil((pos + 1) / span)
+  if (n_act == 1) return;  // the split kernel wrote ctx
+  if (!EAGER) {
+    fetch_ml();
+    fetch();
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = t + k * kSplitThreads;
+    if (i < n_act * hpg) {
+      cw[i] = mv[k];
+      cl[i] = lv[k];
+    }
+  }
+  __syncthreads();
+  {
+    const int wave = t / kWave, lane = t & (kWave - 1);
+    for (int hh = wave; hh < hpg; hh += kSplitThreads / kWave) {
+      const float m = lane < n_act ? cw[lane * hpg + hh] : -INFINITY;
+      const float M = wave_max_dpp(m);
+      const float w = lane < n_act ? expf(m - M) : 0.0f;
+      const double L = wave_sum_d_dpp(lane < n_act ? cl[lane * hpg + hh] * static_cast<double>(w) : 0.0);
+      if (lane < n_act) cw[lane * hpg + hh] = w;
+      if (lane == 0) cinv[hh] = static_cast<float>(1.0 / L);
+    }
+  }
+  __syncthreads();
+  const int hh = (col * 4) / kSplitHd;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int q = 0; q < kSplitPerThread; ++q) {
+    const int sj = sub * per + q;
+    if (active && q < per && sj < n_act) {
+      const float w = cw[sj * hpg + hh];
+      acc.x += ov[q].x * w;
+      acc.y += ov[q].y * w;
+      acc.z += ov[q].z * w;
+      acc.w += ov[q].w * w;
+    }
+  }
+  if (active) cred[sub * cols + col] = acc;
+  __syncthreads();
+  if (sub == 0) {
+    float4 r = cred[col];
+    for (int k = 1; k < tpc; ++k) {
+      const float4 v = cred[k * cols + col];
+      r.x += v.x;
+      r.y += v.y;
+      r.z += v.z;
+      r.w += v.w;
+    }
+    const float iv = cinv[hh];
+    r.x *= iv;
+    r.y *= iv;
+    r.z *= iv;
+    r.w *= iv;
+    reinterpret_cast<float4*>(out)[col] = r;
+  }
+}
+
 // Prefill, step 1: every row r = (sequence b, chunk index i) at position p = *pos_dev + i gets RoPE
 // on each query head in place and on each key head, and its roped key and its value row are
 // written into the cache at p (the decode kernel's rotation, operation for operation).
@@ -803,9 +1141,27 @@ int attention_choice() {
   const char* v = std::getenv("EF_HIP_ATTENTION");
   if (v == nullptr) return 0;
   if (std::strcmp(v, "head") == 0) return 1;
+  if (std::strcmp(v, "split") == 0) return 4;
   if (std::strcmp(v, "group") == 0) return 2;
   if (std::strcmp(v, "wave") == 0) return 3;
   return 0;
+}
+
+bool attention_split_plan(int H, int KV, int hd, int max_seq, int batch, int* splits, int* span, size_t* part_floats) {
+  *splits = 1;
+  *span = max_seq;
+  *part_floats = 0;
+  if (hd != kSplitHd || KV < 1 || H % KV != 0 || H / KV > kSplitMaxHpg || max_seq <= kSplitRows ||
+      attention_choice() == 1 || attention_choice() == 2 || attention_choice() == 3)
+    return false;
+  const long cap = static_cast<long>(kSplitRows) * split_max(H / KV);
+  const int sp = static_cast<int>(((max_seq + cap - 1) / cap) * kSplitRows);
+  const size_t lim = std::max<size_t>(ctx().lds_per_block, 65536);
+  if (attention_split_lds_bytes(H / KV, sp) > lim) return false;
+  *span = sp;
+  *splits = (max_seq + sp - 1) / sp;
+  *part_floats = static_cast<size_t>(batch) * KV * *splits * kSplitRec;
+  return true;
 }
 
 // Many sequences: one workgroup per (KV group, sequence) when that fills the chip (or is forced)
@@ -833,6 +1189,29 @@ int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
     return EF_HIP_OK;
   }
   EFH_CHECK(!a.em.on(), "attention: only the KV-group kernel stages its output as tables");
+  if (a.part != nullptr && a.rope_now != nullptr) {
+    EFH_CHECK(a.hd == kSplitHd && a.H % a.KV == 0 && a.H / a.KV <= kSplitMaxHpg && a.span % kSplitRows == 0 &&
+                  static_cast<long>(a.splits) * a.span >= a.max_seq && (a.splits - 1) * a.span < a.max_seq &&
+                  a.splits <= split_max(a.H / a.KV),
+              "attention: position split does not fit the shape");
+    // the rows of every split requested before the position is known when that costs at most
+    // 128 workgroups' worth (about 4 MB) of reads at short positions
+    const bool eager = static_cast<long>(a.splits) * a.KV * batch <= 128;
+    const size_t lds = attention_split_lds_bytes(a.H / a.KV, a.span);
+    if (eager) {
+      hipLaunchKernelGGL(attention_split_kernel<true>, dim3(a.splits, a.KV, batch), dim3(kSplitThreads), lds, s, a);
+    } else {
+      hipLaunchKernelGGL(attention_split_kernel<false>, dim3(a.splits, a.KV, batch), dim3(kSplitThreads), lds, s, a);
+    }
+    EFH_HIP(hipGetLastError());
+    if (eager) {
+      hipLaunchKernelGGL(attention_combine_kernel<true>, dim3(a.KV, batch), dim3(kSplitThreads), kCombineLds, s, a);
+    } else {
+      hipLaunchKernelGGL(attention_combine_kernel<false>, dim3(a.KV, batch), dim3(kSplitThreads), kCombineLds, s, a);
+    }
+    EFH_HIP(hipGetLastError());
+    return EF_HIP_OK;
+  }
   // hd = 64 with the step's RoPE row: one wave per (head, sequence), unless another kernel is forced
   if (a.hd == kWaveHd && a.rope_now != nullptr && a.H % a.KV == 0 && choice != 1 && choice != 2) {
     const size_t wlds = (2 * static_cast<size_t>(kWaveHd) + static_cast<size_t>(a.max_seq)) * sizeof(float);
