@@ -351,6 +351,22 @@ def main() -> int:
     eng.close()
     extra["sampled_b1_tok_s"] = round(K / sdec, 1)
     log(f"[bench] B=1 sampled decode (T 0.8, top-k 40, top-p 0.95, penalty 1.1): {K / sdec:.1f} tok/s")
+    # the reference's full context: a 2000-token prompt in a 2048-position cache, K greedy steps
+    # from position 2000 (src/model.cpp:165-167; attention over every cached position)
+    lc_prompt = rng.integers(0, TINYLLAMA.V, 2000).astype(np.int32)
+    lk = min(K, 2048 - 2000 - 1)
+    eng = Engine(model, max_seq=2048)
+    eng.generate([lc_prompt], 4)
+    _, lc_pre, lc_dec = eng.generate([lc_prompt], lk + 1)
+    lc_att = None
+    if not args.no_step_profile:
+        lc_att = round(eng.profile(reps=10)["attention"] * 1e3, 2)
+    eng.close()
+    extra["pos2000_b1_us_per_step"] = round(lc_dec / lk * 1e6, 1)
+    extra["pos2000_b1_attention_us_per_step"] = lc_att
+    extra["prefill_2000_b1_ms"] = round(lc_pre * 1e3, 2)
+    log(f"[bench] B=1 decode at positions 2000..{2000 + lk}: {lc_dec / lk * 1e6:.1f} us/step "
+        f"(attention {lc_att} us/step); 2000-position batched prefill {lc_pre * 1e3:.1f} ms")
     if args.batch64 > 0:
         B = args.batch64
         prompts = rng.integers(0, TINYLLAMA.V, size=(B, 23)).astype(np.int32)
