@@ -283,6 +283,10 @@ def main() -> int:
     ap.add_argument("--only-batched", action="store_true",
                     help="profiling mode: only the B=64 Q4_0 5632x2048 matvec launches (fragment preparation + "
                          "matrix-core GEMV) over rotating replicas; prints their average time")
+    ap.add_argument("--only-batched-shapes", action="store_true",
+                    help="profiling mode: every product shape of the B=64 step as a standalone batched matvec "
+                         "(q and o 2048x2048 Q4_0, k/v 256x2048 Q8_0, gate/up SwiGLU 2x5632x2048, down 2048x5632, "
+                         "Q8_0 lm_head 32000x2048) over rotating replicas; prints us per launch")
     ap.add_argument("--no-step-profile", action="store_true",
                     help="skip the per-group decode profile (ef_hip_engine_profile); implied under a profiler, where "
                          "that call has crashed the host")
@@ -326,6 +330,21 @@ def main() -> int:
     if args.only_batched:
         ms, nbytes = profile_plain(H, L, model, (1, "w_gate"), L.Q4_0, 18, batch=64, launches=200)
         print(json.dumps({"q4_0_5632x2048_b64_us": round(ms * 1e3, 3), "bytes_per_launch": nbytes}), flush=True)
+        return 0
+    if args.only_batched_shapes:
+        out = {}
+        for name, key, qt, blk in (("q_2048x2048_q4_0", (1, "wq"), L.Q4_0, 18),
+                                   ("v_256x2048_q8_0", (1, "wv"), L.Q8_0, 34),
+                                   ("o_2048x2048_q4_0", (1, "wo"), L.Q4_0, 18),
+                                   ("down_2048x5632_q4_0", (1, "w_down"), L.Q4_0, 18),
+                                   ("lm_head_32000x2048_q8_0", "lm_head", L.Q8_0, 34)):
+            ms, nb = profile_plain(H, L, model, key, qt, blk, batch=64, launches=100)
+            out[name] = {"us": round(ms * 1e3, 3), "bytes": nb}
+            log(f"[bench] B=64 {name}: {ms * 1e3:.2f} us/launch")
+        ms, nb, _ = profile_gate_up(H, L, model, batch=64, launches=100)
+        out["gate_up_swiglu_2x5632x2048_q4_0"] = {"us": round(ms * 1e3, 3), "bytes": nb}
+        log(f"[bench] B=64 gate/up SwiGLU: {ms * 1e3:.2f} us/launch")
+        print(json.dumps(out), flush=True)
         return 0
     rng = np.random.default_rng(23)
     prompt = rng.integers(0, TINYLLAMA.V, 23).astype(np.int32)
