@@ -154,37 +154,38 @@ __device__ const uint64_t kExpTable[256] = {
     0x3c5305c14160cc89ull, 0x3feff3c22b8f71f1ull,
 };
 
-__device__ __forceinline__ double exp_libm(double x) {
+// tab: kExpTable or a copy of it (LDS, stage_exp_table): a kernel that evaluates many terms per
+// thread reads the table from LDS.  The table index is formed before the special cases are
+// sorted out (it is in range for any x, NaN and infinities included), so the compiler can issue
+// the lookups of several calls together; the special cases reuse the same quantities.
+__device__ __forceinline__ double exp_libm(double x, const uint64_t* __restrict__ tab) {
 #pragma clang fp contract(off)
   const double kInvLn2N = 0x1.71547652b82fep0 * 128, kShift = 0x1.8p52;
   const double kNegLn2HiN = -0x1.62e42fefa0000p-8, kNegLn2LoN = -0x1.cf79abc9e3b3ap-47;
   const double kC2 = 0x1.ffffffffffdbdp-2, kC3 = 0x1.555555555543cp-3, kC4 = 0x1.55555cf172b91p-5,
                kC5 = 0x1.1111167a4d017p-7;
   const uint64_t ux = __double_as_longlong(x);
-  uint32_t abstop = static_cast<uint32_t>(ux >> 52) & 0x7ffu;
-  // |x| < 2^-54 (then 1 + x), or |x| >= 512 (the scale may leave the normal range)
-  if (abstop - 0x3c9u >= 0x408u - 0x3c9u) {
-    if (abstop - 0x3c9u >= 0x80000000u) return 1.0 + x;
-    if (abstop >= 0x409u) {  // |x| >= 1024, inf, nan
-      if (ux == 0xfff0000000000000ull) return 0.0;
-      if (abstop >= 0x7ffu) return 1.0 + x;
-      return (ux >> 63) ? 0.0 : __longlong_as_double(0x7ff0000000000000ll);
-    }
-    abstop = 0;
-  }
+  const uint32_t abstop = static_cast<uint32_t>(ux >> 52) & 0x7ffu;
   double kd = __builtin_fma(kInvLn2N, x, kShift);
   const uint64_t ki = __double_as_longlong(kd);
   kd -= kShift;
   const double r = __builtin_fma(kd, kNegLn2LoN, __builtin_fma(kd, kNegLn2HiN, x));
   const uint32_t idx = 2u * static_cast<uint32_t>(ki % 128u);
-  const double tail = __longlong_as_double(kExpTable[idx]);
-  uint64_t sbits = kExpTable[idx + 1] + (ki << 45);
+  const double tail = __longlong_as_double(tab[idx]);
+  const uint64_t sbits = tab[idx + 1] + (ki << 45);
   const double r2 = r * r;
   const double tmp = __builtin_fma(r2 * r2, __builtin_fma(r, kC5, kC4),
                                    __builtin_fma(r2, __builtin_fma(r, kC3, kC2), tail + r));
-  if (abstop != 0) {
+  // 2^-54 <= |x| < 512: the scale is a normal double
+  if (abstop - 0x3c9u < 0x408u - 0x3c9u) {
     const double scale = __longlong_as_double(sbits);
     return __builtin_fma(scale, tmp, scale);
+  }
+  if (abstop - 0x3c9u >= 0x80000000u) return 1.0 + x;  // |x| < 2^-54
+  if (abstop >= 0x409u) {                              // |x| >= 1024, inf, nan
+    if (ux == 0xfff0000000000000ull) return 0.0;
+    if (abstop >= 0x7ffu) return 1.0 + x;
+    return (ux >> 63) ? 0.0 : __longlong_as_double(0x7ff0000000000000ll);
   }
   if ((ki & 0x80000000u) == 0) {  // k > 0: the scale's exponent may have overflowed by <= 460
     const double scale = __longlong_as_double(sbits - (1009ull << 52));
@@ -200,6 +201,13 @@ __device__ __forceinline__ double exp_libm(double x) {
     if (y == 0.0) y = 0.0;
   }
   return 0x1p-1022 * y;
+}
+
+__device__ __forceinline__ double exp_libm(double x) { return exp_libm(x, kExpTable); }
+
+// The table copied into LDS by the calling block (256 words); the caller synchronises before use.
+__device__ __forceinline__ void stage_exp_table(uint64_t* lds) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) lds[i] = kExpTable[i];
 }
 
 }  // namespace efh

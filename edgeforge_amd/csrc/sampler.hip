@@ -486,7 +486,7 @@ struct SampleArgs {
 // P(id) under softmax of the raw logits, in double (prob_of, src/chat.cpp:35-42): max, then the sum
 // of exp(l - max) over the vocabulary (per-thread partial sums combined in a fixed order; the
 // reference adds left to right, a difference in the last bits of a double).  Thread 0 returns it.
-__device__ double softmax_prob(const float* lg, int V, int id, double* red) {
+__device__ double softmax_prob(const float* lg, int V, int id, double* red, const uint64_t* etab) {
   const int t = threadIdx.x, nw = blockDim.x / kWave;
   double m = -INFINITY;
   for (int i = t; i < V; i += blockDim.x) m = fmax(m, static_cast<double>(lg[i]));
@@ -497,7 +497,7 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
   for (int w = 1; w < nw; ++w) m = fmax(m, red[w]);
   __syncthreads();
   double s = 0.0;
-  for (int i = t; i < V; i += blockDim.x) s += exp_libm(static_cast<double>(lg[i]) - m);
+  for (int i = t; i < V; i += blockDim.x) s += exp_libm(static_cast<double>(lg[i]) - m, etab);
   s = wave_sum_d(s);
   if ((t & (kWave - 1)) == 0) red[t / kWave] = s;
   __syncthreads();
@@ -505,20 +505,22 @@ __device__ double softmax_prob(const float* lg, int V, int id, double* red) {
   for (int w = 0; w < nw; ++w) tot += red[w];
   __syncthreads();
   if (id < 0 || id >= V) return 0.0;
-  return exp_libm(static_cast<double>(lg[id]) - m) / tot;
+  return exp_libm(static_cast<double>(lg[id]) - m, etab) / tot;
 }
 
 // The sampler after the sort (src/sampler.cpp:42-69): softmax over the kept ids, the nucleus, the
 // draw and the CDF walk.  `sorted` holds the keys in descending order, `stage` 2 kStage doubles of LDS.
 __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, int keep, bool topk, double* prob,
-                            double* s_prob, double* stage, int& s_stop, double& s_sum, int& s_keep) {
+                            double* s_prob, double* stage, int& s_stop, double& s_sum, int& s_keep,
+                            const uint64_t* etab) {
   // softmax over the kept ids in double (src/sampler.cpp:42-49); with top-k the kept probabilities
   // live in LDS, otherwise the sequential loops below stage them through the sort buffer (free
   // once the keys are sorted)
   const bool in_lds = topk;
   if (topk) prob = s_prob;
   const float mx = key_value(sorted[0]);
-  for (int i = threadIdx.x; i < keep; i += blockDim.x) prob[i] = exp_libm(static_cast<double>(key_value(sorted[i]) - mx));
+  for (int i = threadIdx.x; i < keep; i += blockDim.x)
+    prob[i] = exp_libm(static_cast<double>(key_value(sorted[i]) - mx), etab);
   __threadfence_block();
   __syncthreads();
   {
@@ -633,10 +635,13 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));        // [V] (no top-k)
   uint64_t* keys = reinterpret_cast<uint64_t*>(ws + ((V * 4 + 255) & ~255) + prob_region_bytes(V));  // [npow2]
   const float* lg = a.logits + b * a.ld;
+  __shared__ uint64_t s_exp[256];  // exp_libm's table: P(eos) takes V / 1024 terms per thread
+  stage_exp_table(s_exp);
+  __syncthreads();
 
   if (a.eos_p != nullptr) {
     __shared__ double s_red[kThreads / kWave];
-    const double pe = softmax_prob(lg, V, a.eos_id, s_red);
+    const double pe = softmax_prob(lg, V, a.eos_id, s_red, s_exp);
     if (threadIdx.x == 0) a.eos_p[b] = pe;
   }
   // Sampled top-k with V <= kRegSlots * kThreads keeps the logits in registers (thread t holds ids
@@ -864,7 +869,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     sorted = keys;
   }
   static_assert(sizeof(s_keys) >= 2 * kStage * sizeof(double), "staging buffers");
-  sample_tail(a, b, sorted, keep, topk, prob, s_prob, reinterpret_cast<double*>(s_keys), s_stop, s_sum, s_keep);
+  sample_tail(a, b, sorted, keep, topk, prob, s_prob, reinterpret_cast<double*>(s_keys), s_stop, s_sum, s_keep,
+              s_exp);
 }
 
 // ---- the full sort across workgroups (no top-k, large vocabularies) ---------------------------------
@@ -1357,17 +1363,24 @@ __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
   __shared__ double s_stage[2 * kStage];
   __shared__ int s_stop, s_keep;
   __shared__ double s_sum;
+  __shared__ uint64_t s_exp[256];
   const int b = blockIdx.x, V = a.vocab;
+  stage_exp_table(s_exp);
+  __syncthreads();
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
   double* prob = reinterpret_cast<double*>(ws + ((V * 4 + 255) & ~255));
-  sample_tail(a, b, merged_of(a, b), tail_keep(a), false, prob, nullptr, s_stage, s_stop, s_sum, s_keep);
+  sample_tail(a, b, merged_of(a, b), tail_keep(a), false, prob, nullptr, s_stage, s_stop, s_sum, s_keep, s_exp);
 }
 
 // exp_libm over an array: the softmax-term call of the kernels above, for comparison with a host
 // libm.
 __global__ __launch_bounds__(256) void exp_kernel(const double* __restrict__ x, double* __restrict__ y, size_t n) {
+  __shared__ uint64_t s_exp[256];
+  stage_exp_table(s_exp);
+  __syncthreads();
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = exp_libm(x[i]);
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = exp_libm(x[i], s_exp);
 }
 
 }  // namespace
