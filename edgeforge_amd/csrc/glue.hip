@@ -1021,6 +1021,150 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(Prefill
                 a.a.ctx + static_cast<long>(r) * a.a.ldq + h * hd, nullptr);
 }
 
+// Prefill, step 2 for long prompts (hd = 64, at most 8 query heads per KV head): workgroup (x, g)
+// takes kPfRows consecutive rows of one sequence and KV group g, so each staged 64-position chunk of
+// K / V serves every (row, head) pair of the block instead of one.  Thread t owns pair t % 128
+// (row t % 128 / hpg, head t % 128 % hpg) with its roped query in registers, and half t / 128 of
+// each chunk's positions.  Scores follow kern::dot_f32's order (src/kernels.cpp:27-43).  Two passes
+// over the chunks: the row's maximum, then e = float exp(s - max), their double sum (each half in
+// position order, then the two halves) and o[d] = sum_t e_t v_t[d] over positions in increasing
+// order (thread: its pair, dimensions 32 (t / 128) ..); out = o * float(1 / sum).  The reference
+// scales each e by 1 / sum before the p.v sum (src/kernels.cpp:77-92,153-174): the results differ
+// by that rounding.  Rows, chunk rows past the block's last position and positions past a row's
+// own take no part (zero K / V rows, e = 0).
+constexpr int kPfRows = 16, kPfChunk = 64, kPfLd = 68, kPfPairs = 128, kPfPsLd = 65;
+constexpr int kPfTileFrom = 128;  // positions per sequence in a launch from which the tiled kernel runs
+
+size_t prefill_tile_lds_bytes() {
+  return (2 * kPfChunk * kPfLd + kPfPairs * kPfPsLd + 2 * kPfPairs) * sizeof(float) + 2 * kPfPairs * sizeof(double);
+}
+
+__global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs pa) {
+#pragma clang fp contract(off)
+  const AttnArgs& a = pa.a;
+  extern __shared__ float sm[];
+  float* ks = sm;                                           // [64][kPfLd] K rows of the chunk
+  float* vs = ks + kPfChunk * kPfLd;                        // [64][kPfLd] V rows
+  float* ps = vs + kPfChunk * kPfLd;                        // [128][kPfPsLd] exponentials of the chunk
+  float* mx2 = ps + kPfPairs * kPfPsLd;                     // [2][128] maxima per half
+  double* l2 = reinterpret_cast<double*>(mx2 + 2 * kPfPairs);  // [2][128] sums per half
+  const int nb = (pa.n + kPfRows - 1) / kPfRows;
+  const int b = blockIdx.x / nb, i0 = (blockIdx.x % nb) * kPfRows, g = blockIdx.y, t = threadIdx.x;
+  const int hpg = a.H / a.KV, kvd = a.KV * 64;
+  const int pair = t & (kPfPairs - 1), half = t >> 7;
+  const int il = pair / hpg, hh = pair - il * hpg, i = i0 + il;
+  const bool active = il < kPfRows && i < pa.n;
+  const int pos0 = *a.pos_dev;
+  const int prow = pos0 + i, plast = pos0 + min(i0 + kPfRows, pa.n) - 1;
+  const long r = static_cast<long>(b) * pa.n + i;
+  float q[64];
+  if (active) {
+    const float4* qp = reinterpret_cast<const float4*>(a.q + r * a.ldq + (g * hpg + hh) * 64);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float4 v = qp[k];
+      q[4 * k] = v.x;
+      q[4 * k + 1] = v.y;
+      q[4 * k + 2] = v.z;
+      q[4 * k + 3] = v.w;
+    }
+  }
+  const float* kc = a.kcache + static_cast<long>(b) * a.max_seq * kvd + g * 64;
+  const float* vc = a.vcache + static_cast<long>(b) * a.max_seq * kvd + g * 64;
+  auto stage = [&](float* dst, const float* src, int c0) {
+    for (int idx = t; idx < kPfChunk * 16; idx += 256) {
+      const int rr = idx >> 4, cc = idx & 15;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (c0 + rr <= plast) v = reinterpret_cast<const float4*>(src + static_cast<long>(c0 + rr) * kvd)[cc];
+      reinterpret_cast<float4*>(dst + rr * kPfLd)[cc] = v;
+    }
+  };
+  auto score = [&](int rr) -> float {
+    const float* kr = ks + rr * kPfLd;
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const float4 ka = *reinterpret_cast<const float4*>(kr + 8 * m);
+      const float4 kb = *reinterpret_cast<const float4*>(kr + 8 * m + 4);
+      p0 += q[8 * m] * ka.x;
+      p1 += q[8 * m + 1] * ka.y;
+      p2 += q[8 * m + 2] * ka.z;
+      p3 += q[8 * m + 3] * ka.w;
+      p4 += q[8 * m + 4] * kb.x;
+      p5 += q[8 * m + 5] * kb.y;
+      p6 += q[8 * m + 6] * kb.z;
+      p7 += q[8 * m + 7] * kb.w;
+    }
+    return (((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))) * a.scale;
+  };
+  const int nchunks = plast / kPfChunk + 1;
+  // pass 1: each row's maximum
+  float m = -INFINITY;
+  for (int c = 0; c < nchunks; ++c) {
+    stage(ks, kc, c * kPfChunk);
+    __syncthreads();
+    if (active) {
+      for (int j = 0; j < 32; ++j) {
+        const int rr = 32 * half + j;
+        if (c * kPfChunk + rr <= prow) m = fmaxf(m, score(rr));
+      }
+    }
+    __syncthreads();
+  }
+  mx2[half * kPfPairs + pair] = m;
+  __syncthreads();
+  const float M = fmaxf(mx2[pair], mx2[kPfPairs + pair]);
+  // pass 2: exponentials, their sum and the unnormalised p.v
+  double l = 0.0;
+  float o[32];
+#pragma unroll
+  for (int d = 0; d < 32; ++d) o[d] = 0.0f;
+  for (int c = 0; c < nchunks; ++c) {
+    stage(ks, kc, c * kPfChunk);
+    stage(vs, vc, c * kPfChunk);
+    __syncthreads();
+    for (int j = 0; j < 32; ++j) {
+      const int rr = 32 * half + j;
+      float e = 0.0f;
+      if (active && c * kPfChunk + rr <= prow) {
+        e = expf(score(rr) - M);
+        l += static_cast<double>(e);
+      }
+      ps[pair * kPfPsLd + rr] = e;
+    }
+    __syncthreads();
+    if (active) {
+      for (int rr = 0; rr < kPfChunk; ++rr) {
+        const float e = ps[pair * kPfPsLd + rr];
+        const float* vr = vs + rr * kPfLd + 32 * half;
+#pragma unroll
+        for (int d = 0; d < 32; d += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(vr + d);
+          o[d] += e * v.x;
+          o[d + 1] += e * v.y;
+          o[d + 2] += e * v.z;
+          o[d + 3] += e * v.w;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  l2[half * kPfPairs + pair] = l;
+  __syncthreads();
+  if (!active) return;
+  const float inv = static_cast<float>(1.0 / (l2[pair] + l2[kPfPairs + pair]));
+  float* out = a.ctx + r * a.ldq + (g * hpg + hh) * 64 + 32 * half;
+#pragma unroll
+  for (int d = 0; d < 32; d += 4) {
+    float4 v;
+    v.x = o[d] * inv;
+    v.y = o[d + 1] * inv;
+    v.z = o[d + 2] * inv;
+    v.w = o[d + 3] * inv;
+    reinterpret_cast<float4*>(out + d)[0] = v;
+  }
+}
+
 // x[r] = row hist[b][*pos_dev + i] of the embedding table for every prefill row r = (b, i).
 __global__ void embed_rows_kernel(const uint8_t* __restrict__ W, int qtype, long rows, long cols, long rb,
                                   const int32_t* __restrict__ hist, long hist_ld, const int32_t* __restrict__ pos_dev,
@@ -1108,6 +1252,22 @@ size_t attention_lds_bytes(int hd, int max_seq) {
 int launch_prefill_attention(const PrefillArgs& a, int rows, hipStream_t s) {
   hipLaunchKernelGGL(rope_store_kernel, dim3(rows), dim3(kAttnThreads), 0, s, a);
   EFH_HIP(hipGetLastError());
+  // long prompts (a launch of kPfTileFrom or more positions per sequence): the tiled kernel
+  const int hpg = a.a.KV > 0 ? a.a.H / a.a.KV : 0;
+  const char* forced = std::getenv("EF_HIP_PREFILL_ATTENTION");
+  const bool tiled_ok = a.a.hd == 64 && a.a.H % a.a.KV == 0 && hpg >= 1 && hpg * kPfRows <= kPfPairs &&
+                        a.a.ldq % 4 == 0;
+  // EF_HIP_PREFILL_ATTENTION=tiled / rows forces either kernel (tests)
+  const bool force_rows = forced != nullptr && std::strcmp(forced, "rows") == 0;
+  const bool force_tiled = forced != nullptr && std::strcmp(forced, "tiled") == 0;
+  if (tiled_ok && !force_rows && (force_tiled || a.n >= kPfTileFrom)) {
+    EFH_CHECK(rows % a.n == 0, "prefill attention: rows must be sequences x positions");
+    const int nb = (a.n + kPfRows - 1) / kPfRows;
+    hipLaunchKernelGGL(prefill_tile_kernel, dim3((rows / a.n) * nb, a.a.KV), dim3(256), prefill_tile_lds_bytes(), s,
+                       a);
+    EFH_HIP(hipGetLastError());
+    return EF_HIP_OK;
+  }
   const size_t lds = attention_lds_bytes(a.a.hd, a.a.max_seq);
   hipLaunchKernelGGL(prefill_attention_kernel, dim3(a.a.H, rows), dim3(kAttnThreads), lds, s, a);
   EFH_HIP(hipGetLastError());
