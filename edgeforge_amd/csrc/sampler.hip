@@ -290,9 +290,9 @@ __device__ void chunk_steps(uint64_t (&x)[kKeysPerThread], int base, int k, int 
     for (int u = 0; u < kKeysPerThread; ++u) {
       const int i = base + t + kThreads * u;
       const bool desc = (i & k) == 0, lower = (i & j) == 0;
-      // descending pair: the lower index keeps the larger key
+      // descending pair: the lower index keeps the larger key (keys are distinct, or equal padding)
       const bool take_max = desc == lower;
-      x[u] = take_max ? (x[u] > y[u] ? x[u] : y[u]) : (x[u] < y[u] ? x[u] : y[u]);
+      x[u] = (x[u] > y[u]) == take_max ? x[u] : y[u];
     }
   }
 }
@@ -481,6 +481,7 @@ struct SampleArgs {
   int eos_id;     // with eos_p: P(eos_id) under softmax(logits) per sequence
   double* eos_p;  // [batch] or null
   int phase;      // 0: one launch; 1: stop once the keys are written (the sort runs in other launches)
+  int fast;       // 1: nucleus_kernel ran first; the full-sort launches take only the sequences it left
 };
 
 // P(id) under softmax of the raw logits, in double (prob_of, src/chat.cpp:35-42): max, then the sum
@@ -613,18 +614,109 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
   if (threadIdx.x == 0) a.out[b] = static_cast<int>(key_id(sorted[pick]));
 }
 
+// The logits of ids t + kThreads j (t = threadIdx.x) in registers, the repetition penalty applied
+// to every in-range history id once (marked in an LDS bitmap, then each owner applies it) and the
+// temperature (src/sampler.cpp:16-27).  V <= kRegSlots * kThreads; s_seen holds (V + 31) / 32 words.
+__device__ void load_tempered(const SampleArgs& a, int b, float (&rv)[kRegSlots], uint32_t* s_seen) {
+  const int V = a.vocab;
+  const float* lg = a.logits + b * a.ld;
+#pragma unroll
+  for (int j = 0; j < kRegSlots; ++j) {
+    const int id = threadIdx.x + kThreads * j;
+    rv[j] = id < V ? lg[id] : 0.0f;
+  }
+  if (a.penalty != 1.0f) {
+    const int n = a.hist_len[b];
+    const int32_t* h = a.hist + b * a.hist_ld;
+    for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int t = h[i];
+      if (t >= 0 && t < V) atomicOr(&s_seen[t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) {
+      const int id = threadIdx.x + kThreads * j;
+      if (id < V && (s_seen[id >> 5] >> (id & 31) & 1u))
+        rv[j] = rv[j] > 0.0f ? __fdiv_rn(rv[j], a.penalty) : rv[j] * a.penalty;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRegSlots; ++j) rv[j] = __fdiv_rn(rv[j], a.temperature);
+}
+
+// The `need` largest keys by a radix select, 8 bits per pass from the top: on return the keys k
+// with (k & sh.mask) >= sh.prefix are exactly those (keys are unique).  for_each_key(f) calls f on
+// every key this thread owns.  Each wave counts into its own histogram (keys of similar logits
+// share their top digits, and one shared histogram serialises those atomics across the waves).
+// The digit d kept is the largest with S(d) = (keys still in play with digit >= d) >= need, found
+// by a parallel suffix sum; need then drops by S(d + 1).  Every thread of the block calls it.
+struct SelectShared {
+  uint32_t whist[kThreads / kWave * 256];
+  uint32_t hist[256], sfx[256];
+  uint64_t prefix, mask;
+  int need, done;
+};
+
+template <typename F>
+__device__ void radix_select(int need, F&& for_each_key, SelectShared& sh) {
+  constexpr int kWaves = kThreads / kWave;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  if (threadIdx.x == 0) {
+    sh.prefix = 0;
+    sh.mask = 0;
+    sh.need = need;
+    sh.done = 0;
+  }
+  __syncthreads();
+  for (int shift = 56; shift >= 0 && !sh.done; shift -= 8) {
+    for (int i = threadIdx.x; i < kWaves * 256; i += blockDim.x) sh.whist[i] = 0u;
+    __syncthreads();
+    const uint64_t prefix = sh.prefix, mask = sh.mask;
+    for_each_key([&](uint64_t k) {
+      if ((k & mask) == prefix) atomicAdd(&sh.whist[wave * 256 + ((k >> shift) & 255u)], 1u);
+    });
+    __syncthreads();
+    if (threadIdx.x < 256) {  // digit d = threadIdx.x: 4 waves of 64 digits
+      const int d = threadIdx.x;
+      uint32_t c = 0;
+      for (int w = 0; w < kWaves; ++w) c += sh.whist[w * 256 + d];
+      sh.hist[d] = c;
+      uint32_t sfx = c;  // suffix sum over the wave's digits >= d
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t v = __shfl_down(sfx, o, kWave);
+        if (lane + o < kWave) sfx += v;
+      }
+      sh.sfx[d] = sfx;
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int d = threadIdx.x, nd = sh.need;
+      uint32_t above = 0;  // the waves of higher digits
+      for (int w = d / kWave + 1; w < 4; ++w) above += sh.sfx[w * kWave];
+      const uint32_t S = sh.sfx[d] + above, S1 = S - sh.hist[d];  // S(d), S(d + 1)
+      if ((static_cast<int>(S) >= nd || d == 0) && static_cast<int>(S1) < nd) {
+        const int rest = nd - static_cast<int>(S1);
+        sh.need = rest;
+        sh.prefix = prefix | (static_cast<uint64_t>(d) << shift);
+        sh.mask = mask | (255ull << shift);
+        if (static_cast<int>(sh.hist[d]) == rest) sh.done = 1;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ uint64_t s_keys[2 * kChunk];  // 64 KB: top-k candidates / sort exchange buffers
   constexpr int kWaves = kThreads / kWave;
-  __shared__ uint32_t s_hist[256], s_sfx[256];
-  __shared__ uint32_t s_whist[kWaves * 256];  // per-wave histograms of the radix select
+  __shared__ SelectShared s_sel;
   __shared__ uint32_t s_floor[kWaves * kFloorMaxRank];  // each wave's largest lane maxima (order bits)
   __shared__ uint32_t s_floor_bits;
   __shared__ float s_val[kThreads / kWave];
   __shared__ int s_idx[kThreads / kWave];
   __shared__ int s_cnt, s_keep, s_stop;
-  __shared__ uint64_t s_prefix, s_mask;
-  __shared__ int s_need, s_done;
   __shared__ double s_sum;
   __shared__ uint32_t s_seen[(32768 + 31) / 32];
   __shared__ double s_prob[kMaxTopK];  // the kept probabilities of the top-k path
@@ -662,30 +754,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     }
   };
   if (reg) {
-#pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) {
-      const int id = threadIdx.x + kThreads * j;
-      rv[j] = id < V ? lg[id] : 0.0f;
-    }
-    if (a.penalty != 1.0f) {  // every id of the history once: mark them, then each owner applies it
-      const int n = a.hist_len[b];
-      const int32_t* h = a.hist + b * a.hist_ld;
-      for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
-      __syncthreads();
-      for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const int t = h[i];
-        if (t >= 0 && t < V) atomicOr(&s_seen[t >> 5], 1u << (t & 31));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < kRegSlots; ++j) {
-        const int id = threadIdx.x + kThreads * j;
-        if (id < V && (s_seen[id >> 5] >> (id & 31) & 1u))
-          rv[j] = rv[j] > 0.0f ? __fdiv_rn(rv[j], a.penalty) : rv[j] * a.penalty;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) rv[j] = __fdiv_rn(rv[j], a.temperature);
+    load_tempered(a, b, rv, s_seen);
   } else {
   for (int i = threadIdx.x; i < V; i += blockDim.x) work[i] = lg[i];
   __syncthreads();
@@ -733,13 +802,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   int keep = V;
   const uint64_t* sorted = nullptr;
   if (topk) {
-    if (threadIdx.x == 0) {
-      s_prefix = 0;
-      s_mask = 0;
-      s_need = a.top_k;
-      s_done = 0;
-      s_cnt = 0;
-    }
+    if (threadIdx.x == 0) s_cnt = 0;
     __syncthreads();
     const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
     // Candidates by a floor (k <= 64, logits in registers), on the keys' high halves (order bits):
@@ -797,48 +860,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       }
     }
     if (n_keys < 0) {
-    // radix select of the k-th largest key, 8 bits per pass from the top.
-    // Each wave counts into its own histogram (keys of similar logits share their top digits,
-    // and one shared histogram serialises those atomics across the waves).  The digit d kept is
-    // the largest with S(d) = (keys still in play with digit >= d) >= need, found by a parallel
-    // suffix sum; need then drops by S(d + 1).
-    for (int shift = 56; shift >= 0 && !s_done; shift -= 8) {
-      for (int i = threadIdx.x; i < kWaves * 256; i += blockDim.x) s_whist[i] = 0u;
-      __syncthreads();
-      const uint64_t prefix = s_prefix, mask = s_mask;
-      for_each_key([&](uint64_t k) {
-        if ((k & mask) == prefix) atomicAdd(&s_whist[wave * 256 + ((k >> shift) & 255u)], 1u);
-      });
-      __syncthreads();
-      if (threadIdx.x < 256) {  // digit d = threadIdx.x: 4 waves of 64 digits
-        const int d = threadIdx.x;
-        uint32_t c = 0;
-        for (int w = 0; w < kWaves; ++w) c += s_whist[w * 256 + d];
-        s_hist[d] = c;
-        uint32_t sfx = c;  // suffix sum over the wave's digits >= d
-        for (int o = 1; o < kWave; o <<= 1) {
-          const uint32_t v = __shfl_down(sfx, o, kWave);
-          if (lane + o < kWave) sfx += v;
-        }
-        s_sfx[d] = sfx;
-      }
-      __syncthreads();
-      if (threadIdx.x < 256) {
-        const int d = threadIdx.x, need = s_need;
-        uint32_t above = 0;  // the waves of higher digits
-        for (int w = d / kWave + 1; w < 4; ++w) above += s_sfx[w * kWave];
-        const uint32_t S = s_sfx[d] + above, S1 = S - s_hist[d];  // S(d), S(d + 1)
-        if ((static_cast<int>(S) >= need || d == 0) && static_cast<int>(S1) < need) {
-          const int rest = need - static_cast<int>(S1);
-          s_need = rest;
-          s_prefix = prefix | (static_cast<uint64_t>(d) << shift);
-          s_mask = mask | (255ull << shift);
-          if (static_cast<int>(s_hist[d]) == rest) s_done = 1;
-        }
-      }
-      __syncthreads();
-    }
-    const uint64_t prefix = s_prefix, mask = s_mask;
+    radix_select(a.top_k, for_each_key, s_sel);
+    const uint64_t prefix = s_sel.prefix, mask = s_sel.mask;
     for_each_key([&](uint64_t k) {
       if ((k & mask) >= prefix) {
         const int pos = atomicAdd(&s_cnt, 1);
@@ -886,6 +909,13 @@ __device__ __forceinline__ uint64_t* merged_of(const SampleArgs& a, int b) {
   return keys_of(a, b) + ((static_cast<size_t>(a.npow2) * 8 + 255) & ~size_t{255}) / 8;
 }
 
+// The last 256 bytes of a sequence's workspace: nucleus_kernel's verdict, 1 when the sequence still
+// needs the full sort (written on every call before the full-sort launches read it).
+__device__ __forceinline__ int32_t* full_sort_flag(const SampleArgs& a, int b) {
+  return reinterpret_cast<int32_t*>(a.ws + static_cast<size_t>(b) * a.ws_stride + a.ws_stride - 256);
+}
+__device__ __forceinline__ bool skip_full(const SampleArgs& a, int b) { return a.fast && *full_sort_flag(a, b) == 0; }
+
 // Each kChunk-key run of the keys sorted in place (descending), one workgroup per run.
 __global__ __launch_bounds__(kThreads) void chunk_sort_kernel(SampleArgs a) {
   __shared__ uint64_t s_keys[2 * kChunk];
@@ -901,6 +931,7 @@ __global__ __launch_bounds__(kThreads) void key_sort_kernel(SampleArgs a) {
   __shared__ uint64_t s_keys[2 * kChunk];
   __shared__ uint32_t s_seen[kChunk / 32];
   const int b = blockIdx.y, t = threadIdx.x, base = blockIdx.x * kChunk, V = a.vocab;
+  if (skip_full(a, b)) return;
   const float* lg = a.logits + b * a.ld;
   float v[kKeysPerThread];
 #pragma unroll
@@ -952,6 +983,7 @@ constexpr int kMaxRuns = 64;        // runs of kChunk keys: vocabularies up to 2
 __global__ __launch_bounds__(kMergeThreads) void rank_merge_kernel(SampleArgs a) {
   __shared__ uint64_t s_win[kMergeWindow];
   __shared__ int s_lo[kMaxRuns], s_hi[kMaxRuns], s_off[kMaxRuns];
+  if (skip_full(a, blockIdx.y)) return;
   const uint64_t* keys = keys_of(a, blockIdx.y);
   uint64_t* out = merged_of(a, blockIdx.y);
   const int t = threadIdx.x, e0 = blockIdx.x * kMergeThreads, e = e0 + t;
@@ -1113,15 +1145,16 @@ __device__ __forceinline__ double uniform_d(double v) {
 // as an inner loop that only the owner lane left, so the owner's wave never reached the step and
 // the other lanes repeated the round.)  A round either ends the scan or takes one step, so n + 1
 // rounds suffice; the bound makes every wave's exit certain.
-template <int MODE>
-__device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShared& sh, double* sum) {
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * kScanPer;
+template <int MODE, int PER = kScanPer, int HEAD = kScanHead>
+__device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& sh, double* sum) {
+  static_assert(HEAD <= kScanHead, "scan head");
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * PER;
   constexpr int kW = kThreads / kWave;
   auto pred = [&](double s) { return MODE == 1 ? s >= x : (MODE == 2 ? x < s : false); };
-  const int nh = min(n, kScanHead);
+  const int nh = min(n, HEAD);
   if (base < nh) {
 #pragma unroll
-    for (int i = 0; i < kScanPer; ++i)
+    for (int i = 0; i < PER; ++i)
       if (base + i < nh) sh.head[base + i] = t[i];
   }
   __syncthreads();
@@ -1181,12 +1214,12 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
       (void)frexp(s, &ex);
       const int sc = 53 - ex;
       const double M0 = ldexp(s, sc);
-      const bool mine = base + kScanPer > j0 && base < n;
+      const bool mine = base + PER > j0 && base < n;
       double T = 0.0;
       bool tie = false;
       if (mine) {
 #pragma unroll
-        for (int i = 0; i < kScanPer; ++i) {
+        for (int i = 0; i < PER; ++i) {
           const int j = base + i;
           if (j >= j0 && j < n) {
             const double y = ldexp(t[i], sc), k = rint(y);
@@ -1214,7 +1247,7 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
       if (walk) {
         bool stop = false;
 #pragma unroll
-        for (int i = 0; i < kScanPer; ++i) {
+        for (int i = 0; i < PER; ++i) {
           const int j = base + i;
           if (!stop && j >= j0 && j < n) {
             const double y = ldexp(t[i], sc), k = rint(y), Mp = M0 + K;  // s_{j-1} / u, exact
@@ -1268,10 +1301,10 @@ __device__ int exact_scan(const double (&t)[kScanPer], int n, double x, ScanShar
       }
     }
     const bool take = !usable || (jh >= jb && jb < n);  // wave-uniform
-    if (take && jb / kScanPer == tid) {  // the step at jb as the reference takes it
+    if (take && jb / PER == tid) {  // the step at jb as the reference takes it
       double tj = 0.0;
 #pragma unroll
-      for (int i = 0; i < kScanPer; ++i)
+      for (int i = 0; i < PER; ++i)
         if (base + i == jb) tj = t[i];
       const double sn = sp + tj;
       if (MODE != 0 && pred(sn)) {
@@ -1345,6 +1378,441 @@ __device__ void sample_tail_scan(const SampleArgs& a, int b, const uint64_t* sor
   if (tid == 0) a.out[b] = static_cast<int>(key_id(sorted[i < kp ? i : kp - 1]));
 }
 
+// ---- top-p without top-k: the nucleus from the kTopM largest keys ----------------------------------------
+// The reference sorts the whole vocabulary (src/sampler.cpp:36-38), adds every softmax term in that
+// order (:42-48), cuts the nucleus (:50-61) and walks it (:62-69).  When the nucleus ends within the
+// kTopM largest keys only those need their order: one workgroup per sequence selects them (radix
+// select on the keys in registers), sorts them in LDS and takes the head's sum, the cut and the
+// walk with exact_scan.  The other V - kTopM terms (the tail) join the sum by exact_scan's binade
+// argument, which needs no order: while the running sum s stays in [2^e, 2^(e+1)) a step adds
+// rint(t / u) u, u = 2^(e-52), unless t / u is halfway between integers (a tie, rounded by the
+// parity of s).  So the tail adds K u, K = the sum of rint(t / u) over it, when s / u + K < 2^53 and
+// no tail term is a tie.  When the sum leaves its binade inside the tail, the step that does it is
+// found without sorting: the largest tail key c at which s / u + (the sum of rint(t / u) over the
+// keys in [c, s's last key)) reaches 2^53, by a radix select weighted by rint(t / u) (the weights
+// are integers below 2^53, so their double sums are exact or, past 2^53, still compare correctly
+// with a bound below it); the steps before c are exact, c's step is the reference's plain add, and
+// the rest of the tail continues from there.  A tail tie, a term that is not finite, or a nucleus
+// that reaches past the head leaves the sequence to the full sort (the flag in its workspace), whose
+// launches follow and return at once for every other sequence.
+constexpr int kTopM = kChunk;              // the sorted head: one register chunk sort
+constexpr int kTopPer = kTopM / kThreads;  // head terms per thread in the scans (contiguous)
+constexpr int kMaxTailEvents = 64;         // binade exits taken in the tail before the full sort takes over
+
+// The logit whose order bits are u (the high half of a key).
+__device__ __forceinline__ float ob_value(uint32_t u) { return key_value(static_cast<uint64_t>(u) << 32); }
+
+// Bitonic sort of 4096 keys, descending, thread t holding positions 4t .. 4t + 3 in x: partners at
+// distance 1 and 2 are in the thread, 4 .. 128 in the wave (a shuffle), 256 .. 2048 in other waves
+// (one LDS exchange, double-buffered in buf's 2 x 4096 keys, one barrier).  Every thread calls it.
+__device__ void sort4096_desc(uint64_t (&x)[4], uint64_t* buf) {
+  static_assert(kThreads * 4 == 4096, "four keys per thread");
+  const int t = threadIdx.x;
+  int parity = 0;
+  for (int k = 2; k <= 4096; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint64_t y[4];
+      if (j >= 4 * kWave) {  // position 4t + u at u * kThreads + t: each access lane-contiguous
+        uint64_t* bb = buf + parity * 4096;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bb[u * kThreads + t] = x[u];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) y[u] = bb[u * kThreads + (t ^ (j >> 2))];
+        parity ^= 1;  // the next exchange writes the other buffer, so no second barrier is needed
+      } else if (j >= 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) y[u] = shfl_xor_u64(x[u], j >> 2);
+      } else if (j == 2) {
+        y[0] = x[2];
+        y[1] = x[3];
+        y[2] = x[0];
+        y[3] = x[1];
+      } else {
+        y[0] = x[1];
+        y[1] = x[0];
+        y[2] = x[3];
+        y[3] = x[2];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = 4 * t + u;
+        const bool take_max = ((i & k) == 0) == ((i & j) == 0);  // descending: the lower index keeps the larger
+        x[u] = (x[u] > y[u]) == take_max ? x[u] : y[u];
+      }
+    }
+  }
+}
+
+// Block-wide sum (every thread gets it, added in a fixed order); red: one double per wave.
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  v = wave_sum_d(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  double s = 0.0;
+  for (int w = 0; w < kThreads / kWave; ++w) s += red[w];
+  __syncthreads();
+  return uniform_d(s);
+}
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const uint64_t u = shfl_xor_u64(v, o);
+    v = u > v ? u : v;
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  uint64_t m = 0;
+  for (int w = 0; w < kThreads / kWave; ++w) m = red[w] > m ? red[w] : m;
+  __syncthreads();
+  return m;
+}
+
+// The tail's binade exits (see above).  Each round forms every id's key again from its logit (the
+// penalty marks still in s_seen) and the weight rint(t / u) of those below `above` (0 for the rest),
+// both into the (otherwise idle) sort buffers of the workspace, id t + kThreads j read back only by
+// thread t.  If the rest stays in the binade the sum is final; otherwise a radix select weighted by
+// them finds the key c whose step leaves it: the steps before c are exact, c's step is the
+// reference's add, and the next round starts below c.  Returns 1 with s the whole sum, or 0 (a tie,
+// or more than kMaxTailEvents exits) for the full sort.  hist: kWaves * 256 doubles of LDS.
+__device__ int tail_exits(const SampleArgs& a, int b, double& s, uint64_t above, float mx, const uint32_t* s_seen,
+                          const uint64_t* etab, uint64_t* hist_mem, uint32_t* s_cnt, double* s_dig, double* s_sfx,
+                          double* s_red, uint64_t* s_redk, double& s_before, int& s_digit) {
+  constexpr int kWaves = kThreads / kWave;
+  constexpr int kBatchExp = 4;  // logit loads issued together
+  const int tid = threadIdx.x, wave = tid / kWave, V = a.vocab;
+  const float* lg = a.logits + b * a.ld;
+  uint64_t* wk = keys_of(a, b);
+  double* wt = reinterpret_cast<double*>(merged_of(a, b));
+  double* hist = reinterpret_cast<double*>(hist_mem);
+  // every id's key and, for the tail, its term exp(v - max) (0 for the head): formed once
+  for (int j0 = 0; j0 < kRegSlots; j0 += kBatchExp) {  // the tempered logits again, as load_tempered forms them
+    float v[kBatchExp];
+#pragma unroll
+    for (int u = 0; u < kBatchExp; ++u) {
+      const int id = tid + kThreads * (j0 + u);
+      v[u] = id < V ? lg[id] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatchExp; ++u) {
+      const int id = tid + kThreads * (j0 + u);
+      if (id < V) {
+        float x = v[u];
+        if (a.penalty != 1.0f && (s_seen[id >> 5] >> (id & 31) & 1u))
+          x = x > 0.0f ? __fdiv_rn(x, a.penalty) : x * a.penalty;
+        x = __fdiv_rn(x, a.temperature);
+        const uint64_t k = make_key(x, static_cast<uint32_t>(id));
+        wk[id] = k;
+        wt[id] = k < above ? exp_libm(static_cast<double>(x - mx), etab) : 0.0;
+      }
+    }
+  }
+  // visit(sc, f): f(key, rint(t 2^sc)) for this thread's slots below `above` with the prefix and a
+  // nonzero weight
+  uint64_t prefix = 0, mask = 0;
+  auto visit = [&](int sc, auto&& f) {
+#pragma unroll 4
+    for (int j = 0; j < kRegSlots; ++j) {
+      const int id = tid + kThreads * j;
+      const double t = id < V ? wt[id] : 0.0;
+      const uint64_t k = id < V ? wk[id] : 0ull;
+      if (t != 0.0 && k < above && (k & mask) == prefix) {
+        const double r = rint(ldexp(t, sc));
+        if (r != 0.0) f(k, r);
+      }
+    }
+  };
+  for (int ev = 0; ev < kMaxTailEvents; ++ev) {
+    int ex;
+    (void)frexp(s, &ex);
+    const int sc = 53 - ex;
+    const double M0 = ldexp(s, sc);
+    double T = 0.0;
+    uint64_t tie = 0;
+    prefix = 0;
+    mask = 0;
+#pragma unroll 4
+    for (int j = 0; j < kRegSlots; ++j) {
+      const int id = tid + kThreads * j;
+      const double t = id < V ? wt[id] : 0.0;
+      const uint64_t k = id < V ? wk[id] : 0ull;
+      if (t != 0.0 && k < above) {
+        const double y = ldexp(t, sc), r = rint(y);
+        T += r;
+        if (fabs(y - r) == 0.5) tie = k > tie ? k : tie;
+      }
+    }
+    T = block_sum_d(T, s_red);
+    tie = block_max_u64(tie, s_redk);
+    if (tie != 0) return 0;
+    if (M0 + T < 0x1p53) {
+      s = ldexp(M0 + T, -sc);
+      return 1;
+    }
+    const double need = 0x1p53 - M0;  // exact
+    double before = 0.0;  // weights of the keys above the digit range in play (exact: below need)
+    for (int shift = 56; shift >= 0; shift -= 8) {
+      for (int i = tid; i < kWaves * 256; i += kThreads) hist[i] = 0.0;
+      if (tid < 256) s_cnt[tid] = 0u;
+      __syncthreads();
+      visit(sc, [&](uint64_t k, double r) {
+        const int d = static_cast<int>((k >> shift) & 255u);
+        atomicAdd(&hist[wave * 256 + d], r);
+        atomicAdd(&s_cnt[d], 1u);
+      });
+      __syncthreads();
+      // the digit d with W(d) >= need > W(d + 1), W(d) = before + the weights of digits >= d:
+      // suffix sums, a wave per 64 digits (W(d + 1) < need <= 2^52 is exact; a W(d) past 2^53 is
+      // rounded but still >= need, so exactly one digit qualifies; the sums are monotone in d)
+      if (tid < 256) {
+        double c = 0.0;
+        for (int w = 0; w < kWaves; ++w) c += hist[w * 256 + tid];
+        s_dig[tid] = c;
+        const int ln = tid & (kWave - 1);
+        double sfx = c;  // inclusive suffix over this wave's digits >= d
+        for (int o = 1; o < kWave; o <<= 1) {
+          const double v = __shfl_down(sfx, o, kWave);
+          if (ln + o < kWave) sfx += v;
+        }
+        s_sfx[tid] = sfx;
+      }
+      __syncthreads();
+      if (tid < 256) {
+        const int d = tid, ln = d & (kWave - 1);
+        double hi = before;  // before + the waves of higher digits
+        for (int w = d / kWave + 1; w < 4; ++w) hi += s_sfx[w * kWave];
+        const double w_d = hi + s_sfx[d], w_next = hi + (ln + 1 < kWave ? s_sfx[d + 1] : 0.0);
+        if ((w_d >= need || d == 0) && w_next < need) {
+          s_before = w_next;
+          s_digit = d;
+        }
+      }
+      __syncthreads();
+      before = uniform_d(s_before);
+      const int d = uniform_i(s_digit);
+      prefix |= static_cast<uint64_t>(d) << shift;
+      mask |= 255ull << shift;
+      const int alone = s_cnt[d] == 1u;
+      __syncthreads();
+      if (uniform_i(alone)) {  // one weighted key left in the bucket: its owner names it
+        visit(sc, [&](uint64_t k, double) { s_redk[0] = k; });
+        __syncthreads();
+        prefix = s_redk[0];
+        __syncthreads();
+        break;
+      }
+    }
+    // `prefix` is the exit's key: the steps before it are exact, its own is the reference's add
+    s = ldexp(M0 + before, -sc) + exp_libm(static_cast<double>(key_value(prefix) - mx), etab);
+    above = prefix;
+  }
+  return 0;
+}
+
+__global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
+  constexpr int kWaves = kThreads / kWave;
+  __shared__ uint64_t s_keys[2 * kChunk];  // the head's keys | the sort's exchange, then the weighted histograms
+  __shared__ ScanShared sh;
+  __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64 + kWave];
+  __shared__ int s_n[16];
+  __shared__ uint32_t s_seen[(kRegSlots * kThreads + 31) / 32];
+  __shared__ uint64_t s_exp[256];
+  __shared__ double s_red[kWaves], s_dig[256];
+  __shared__ uint64_t s_redk[kWaves];
+  __shared__ int s_bad, s_digit;
+  __shared__ double s_before, s_sfx[256];
+  const int b = blockIdx.x, V = a.vocab, tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  int32_t* flag = full_sort_flag(a, b);
+  stage_exp_table(s_exp);
+  __syncthreads();
+  if (a.eos_p != nullptr) {
+    const double pe = softmax_prob(a.logits + b * a.ld, V, a.eos_id, s_red, s_exp);
+    if (tid == 0) a.eos_p[b] = pe;
+  }
+  uint32_t ob[kRegSlots];  // the keys' high halves: order bits of the tempered logits
+  {
+    float rv[kRegSlots];
+    load_tempered(a, b, rv, s_seen);
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) ob[j] = tid + kThreads * j < V ? order_bits(rv[j]) : 0u;
+  }
+  auto key_of = [&](int j) {
+    return (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
+  };
+  // the maximum (a NaN or infinite one: the full sort's rule)
+  uint32_t om = 0;
+#pragma unroll
+  for (int j = 0; j < kRegSlots; ++j) om = max(om, ob[j]);
+  om = wave_max_u32_dpp(om);
+  if (lane == 0) s_wmax[wave] = om;
+  __syncthreads();
+  om = 0;
+  for (int w = 0; w < kWaves; ++w) om = max(om, s_wmax[w]);
+  const float mx = ob_value(om);
+  if (!isfinite(mx)) {
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  // The head: the keys whose logit is within some distance of the maximum, at most kTopM of them.
+  // One pass buckets the keys by floor(4 (max - v)) (clamped to 63; monotone in v, so a bucket
+  // bound is a logit bound and the head is a prefix of the sorted order), per-wave histograms;
+  // the bound kept is the largest whose buckets hold at most kTopM keys.
+  auto bucket = [&](int j, float m) {
+    const float d = (m - ob_value(ob[j])) * 4.0f;
+    return d < 63.0f ? static_cast<int>(d) : 63;
+  };
+  for (int i2 = tid; i2 < kWaves * 64; i2 += kThreads) s_bh[i2] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kRegSlots; ++j) {  // bucket 63 (the rest, never in the head) goes to a slot per lane
+    const int bk = bucket(j, mx);
+    if (tid + kThreads * j < V) atomicAdd(&s_bh[bk < 63 ? wave * 64 + bk : kWaves * 64 + lane], 1u);
+  }
+  __syncthreads();
+  if (wave == 0) {  // bucket `lane`: its count, the inclusive prefix over buckets <= lane
+    uint32_t c = 0;
+    for (int w = 0; w < kWaves; ++w) c += s_bh[w * 64 + lane];
+    uint32_t pre = c;
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t v = __shfl_up(pre, o, kWave);
+      if (lane >= o) pre += v;
+    }
+    const uint64_t fits = __ballot(lane < 63 && pre <= static_cast<uint32_t>(kTopM));
+    if (lane == 0) s_n[0] = fits == 0 ? -1 : 63 - __builtin_clzll(fits);  // prefix counts rise with the bucket
+  }
+  __syncthreads();
+  const int bmax = s_n[0];  // the head: buckets <= bmax
+  if (bmax < 0) {  // more than kTopM keys within a quarter of the maximum
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  uint32_t inh = 0;  // bit j: slot j is in the head (the buckets formed again, not kept from above)
+  {
+    float mb = mx;
+    asm volatile("" : "+v"(mb));
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j)
+      if (tid + kThreads * j < V && bucket(j, mb) <= bmax) inh |= 1u << j;
+  }
+  int M = 0;  // keys in the head
+  {
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) cnt += __popcll(__ballot(inh >> j & 1u));
+    if (lane == 0) s_n[wave] = cnt;
+    __syncthreads();
+    int pos = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      pos += w < wave ? s_n[w] : 0;
+      M += s_n[w];
+    }
+    if (M <= kTopM) {  // gathered in wave order, then slot order, then lane order
+#pragma unroll
+      for (int j = 0; j < kRegSlots; ++j) {
+        const bool in = inh >> j & 1u;
+        const uint64_t m = __ballot(in);
+        const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+        if (in) s_keys[pos + r] = key_of(j);
+        pos += __popcll(m);
+      }
+    }
+  }
+  if (M > kTopM || M == 0) {  // cannot happen: bmax keeps at most kTopM keys and bucket 0 holds the maximum
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  for (int i = M + tid; i < kTopM; i += kThreads) s_keys[i] = 0ull;  // below every key
+  __syncthreads();
+  {
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = s_keys[4 * tid + u];
+    __syncthreads();
+    sort4096_desc(x, s_keys);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s_keys[4 * tid + u] = x[u];
+  }
+  __syncthreads();
+  double tm[kTopPer];
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < kTopPer; ++i) {
+    const int p = kTopPer * tid + i;
+    tm[i] = p < M ? exp_libm(static_cast<double>(key_value(s_keys[p]) - mx), s_exp) : 0.0;
+    finite = finite && isfinite(tm[i]);
+  }
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  if (!finite) s_bad = 1;
+  __syncthreads();
+  if (uniform_i(s_bad)) {  // NaN terms: the full sort's rule
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  double s;
+  exact_scan<0, kTopPer, 32>(tm, M, 0.0, sh, &s);
+  // the tail: every key below the head's last one.  One pass over the registers decides the
+  // common case (the sum stays in its binade, no tie).
+  int ok = 0;
+  {
+    int ex;
+    (void)frexp(s, &ex);
+    const int sc = 53 - ex;  // s / u = s 2^sc, an integer in [2^52, 2^53)
+    const double M0 = ldexp(s, sc);
+    const uint64_t above = s_keys[M - 1];  // the tail: every key below the head's last
+    double T = 0.0;
+    uint64_t tie = 0;
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) {
+      if (tid + kThreads * j < V && !(inh >> j & 1u)) {
+        const double y = ldexp(exp_libm(static_cast<double>(ob_value(ob[j]) - mx), s_exp), sc), r = rint(y);
+        T += r;
+        if (fabs(y - r) == 0.5) tie = max(tie, key_of(j));
+      }
+    }
+    T = block_sum_d(T, s_red);
+    tie = block_max_u64(tie, s_redk);
+    if (!(T == T)) {  // a NaN logit in the tail: the full sort's rule
+    } else if (tie == 0 && M0 + T < 0x1p53) {
+      s = ldexp(M0 + T, -sc);
+      ok = 1;
+    } else if (tie == 0) {
+      // The sum leaves its binade in the tail: each exit is found and taken in turn.
+      ok = tail_exits(a, b, s, above, mx, s_seen, s_exp, s_keys + kTopM, s_bh, s_dig, s_sfx, s_red, s_redk, s_before,
+                      s_digit);
+    }
+  }
+  if (!ok) {
+    if (tid == 0) *flag = 1;
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < kTopPer; ++i) tm[i] = tm[i] / s;
+  double cum;
+  const int n = exact_scan<1, kTopPer, 32>(tm, M, static_cast<double>(a.top_p), sh, &cum);
+  if (n >= M) {  // the nucleus reaches past the head
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  const int kp = n + 1;
+#pragma unroll
+  for (int i = 0; i < kTopPer; ++i) tm[i] = tm[i] / cum;
+  if (tid == 0) {
+    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
+    sh.hit_sum = mt_uniform(st);
+  }
+  __syncthreads();
+  const double r = sh.hit_sum;
+  __syncthreads();
+  double c2;
+  const int i = exact_scan<2, kTopPer, 32>(tm, kp, r, sh, &c2);
+  if (tid == 0) {
+    a.out[b] = static_cast<int>(key_id(s_keys[i < kp ? i : kp - 1]));
+    *flag = 0;
+  }
+}
+
 __device__ __forceinline__ int tail_keep(const SampleArgs& a) {
   return a.top_k > 0 && a.top_k < a.vocab ? a.top_k : a.vocab;
 }
@@ -1355,6 +1823,7 @@ __device__ __forceinline__ int tail_keep(const SampleArgs& a) {
 __global__ __launch_bounds__(kThreads) void sample_scan_kernel(SampleArgs a) {
   __shared__ ScanShared sh;
   __shared__ int s_flag;
+  if (skip_full(a, blockIdx.x)) return;
   sample_tail_scan(a, blockIdx.x, merged_of(a, blockIdx.x), tail_keep(a), sh, s_flag);
 }
 
@@ -1365,6 +1834,7 @@ __global__ __launch_bounds__(kThreads) void sample_tail_kernel(SampleArgs a) {
   __shared__ double s_sum;
   __shared__ uint64_t s_exp[256];
   const int b = blockIdx.x, V = a.vocab;
+  if (skip_full(a, b)) return;
   stage_exp_table(s_exp);
   __syncthreads();
   uint8_t* ws = a.ws + static_cast<size_t>(b) * a.ws_stride;
@@ -1389,7 +1859,7 @@ size_t sample_workspace_stride(int vocab) {
   size_t n2 = 1;
   while (n2 < static_cast<size_t>(vocab)) n2 <<= 1;
   const size_t v = static_cast<size_t>(vocab);
-  return ((v * 4 + 255) & ~size_t{255}) + prob_region_bytes(v) + 2 * ((n2 * 8 + 255) & ~size_t{255});
+  return ((v * 4 + 255) & ~size_t{255}) + prob_region_bytes(v) + 2 * ((n2 * 8 + 255) & ~size_t{255}) + 256;
 }
 
 int launch_rng_seed(void* rng, const uint64_t* seeds_dev, int batch, hipStream_t s) {
@@ -1456,7 +1926,13 @@ int launch_sample(const float* logits, int vocab, int batch, long ld, const ef_h
   const bool topk_lds = cfg.top_k > 0 && cfg.top_k < vocab && cfg.top_k <= kMaxTopK;
   if (cfg.temperature > 0.0f && !topk_lds && n2 >= 2 * kChunk) {
     a.phase = 1;
-    if (eos_p != nullptr) {  // P(eos) needs the whole vocabulary: the one-workgroup key launch
+    // top-p without top-k over a vocabulary the registers hold: the nucleus from the sorted head
+    // first; the full sort then runs only for the sequences it leaves
+    a.fast = (cfg.top_k <= 0 || cfg.top_k >= vocab) && cfg.top_p < 1.0f && vocab <= kRegSlots * kThreads;
+    if (a.fast) {
+      hipLaunchKernelGGL(nucleus_kernel, dim3(batch), dim3(kThreads), 0, s, a);  // writes P(eos) too
+      hipLaunchKernelGGL(key_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
+    } else if (eos_p != nullptr) {  // P(eos) needs the whole vocabulary: the one-workgroup key launch
       hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, s, a);
       hipLaunchKernelGGL(chunk_sort_kernel, dim3(n2 / kChunk, batch), dim3(kThreads), 0, s, a);
     } else {

@@ -247,3 +247,128 @@ def test_sampler_other_vocab_sizes(hip, V, top_k, top_p):
                    hist_len=hip.DeviceArray.from_host(np.full(batch, 16, np.int32)), hist_ld=16, rng=rng, ws=ws)
         want = [cpu[b].sample(logits[b], hist[b]) for b in range(batch)]
         assert [int(v) for v in out.numpy()] == want, (V, top_k, top_p, step)
+
+
+HEAD = 4096  # the sorted head of the top-p-only path (nucleus_kernel)
+
+
+def _nucleus_facts(logits, cfg, hist=()):
+    """What decides the top-p-only path for one sequence, restated on the host in the reference's
+    operations (src/sampler.cpp:16-61: penalty and temperature in float, descending sort with ties
+    by id, exp(double(l - max)) from the host libm, left-to-right double sums): the number of kept
+    ids, and how many binades the softmax sum enters after the head's 4096 terms."""
+    lv = np.asarray(logits, np.float32).copy()
+    V = lv.size
+    pen = np.float32(cfg["repetition_penalty"])
+    if pen != np.float32(1.0):
+        for t in sorted({int(h) for h in hist if 0 <= h < V}):
+            lv[t] = lv[t] / pen if lv[t] > 0 else lv[t] * pen
+    lv = (lv / np.float32(cfg["temperature"])).astype(np.float32)
+    order = np.lexsort((np.arange(V), -lv))
+    ls = lv[order]
+    t = O.exp_array((ls - ls[0]).astype(np.float32).astype(np.float64)).tolist()
+    s, s_head = 0.0, None
+    for i, v in enumerate(t):
+        s += v
+        if i == HEAD - 1:
+            s_head = s
+    cum, keep = 0.0, V
+    for i, v in enumerate(t):
+        cum += v / s
+        if cum >= cfg["top_p"]:
+            keep = i + 1
+            break
+    exits = int(np.floor(np.log2(s))) - int(np.floor(np.log2(s_head)))
+    return keep, exits
+
+
+def _designed_tail(g, V, c, decay, lo, hi):
+    """Logits whose sorted softmax terms are 1, then c exp(-i / decay) for the other 4095 head ids,
+    then V - 4096 tail terms uniform in [lo, hi) (below the head's last), ids shuffled."""
+    i = np.arange(1, HEAD)
+    head = c * np.exp(-i / decay)
+    assert hi < head[-1]
+    tail = g.uniform(lo, hi, V - HEAD)
+    vals = np.concatenate([[1.0], head, tail])
+    return np.log(vals).astype(np.float32)[g.permutation(V)]
+
+
+def _check_against_oracle(H, logits, cfg, steps, seeds, hist=None):
+    batch, V = logits.shape
+    rng = H.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    if hist is None:
+        hist = np.zeros((batch, 1), np.int32)
+        hlen = np.zeros(batch, np.int32)
+    else:
+        hlen = np.full(batch, hist.shape[1], np.int32)
+    ws = H.DeviceArray((EL.lib().ef_hip_sample_workspace_bytes(V, batch),), np.uint8)
+    out = H.DeviceArray((batch,), np.int32)
+    dl, dh, dn = H.DeviceArray.from_host(logits), H.DeviceArray.from_host(hist), H.DeviceArray.from_host(hlen)
+    for step in range(steps):
+        H.sample(dl, V, cfg, out, batch=batch, hist=dh, hist_len=dn, hist_ld=hist.shape[1], rng=rng, ws=ws)
+        want = [cpu[b].sample(logits[b], hist[b][:hlen[b]]) for b in range(batch)]
+        assert [int(v) for v in out.numpy()] == want, step
+
+
+@pytest.mark.parametrize("layout", ["one_tail_exit", "two_tail_exits", "no_tail_exit"])
+def test_sampler_nucleus_head_tail_exits(hip, layout):
+    """Top-p without top-k from the sorted head of 4096 keys: the rest of the vocabulary joins the
+    softmax sum unsorted, and when the sum enters a new binade inside it the device finds that step
+    by a weighted radix select and takes it as the reference does (src/sampler.cpp:42-48).  The
+    logits are built so that the host restatement shows the intended number of exits and a nucleus
+    inside the head; ids must equal the reference's over several draws."""
+    V, batch = 32000, 6
+    print(f"[case] sampler nucleus head layout={layout}", flush=True)
+    g = D.rng(4100 + len(layout))
+    if layout == "one_tail_exit":  # head sum about 14 in [8, 16), the tail takes it past 16
+        rows = [_designed_tail(g, V, 0.0133, 1000.0, 1.0e-4, 2.2e-4) for _ in range(batch)]
+        cfg, want_exits = dict(temperature=1.0, top_k=0, top_p=0.7, repetition_penalty=1.0), 1
+    elif layout == "two_tail_exits":  # head sum about 6 in [4, 8), the tail takes it past 8 and 16
+        rows = [_designed_tail(g, V, 0.00195, 4000.0, 3.0e-4, 7.0e-4) for _ in range(batch)]
+        cfg, want_exits = dict(temperature=1.0, top_k=0, top_p=0.25, repetition_penalty=1.0), 2
+    else:  # peaked: the sum settles inside the head
+        rows = [(g.standard_normal(V, dtype=np.float32) * np.float32(4.0)).astype(np.float32) for _ in range(batch)]
+        cfg, want_exits = dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.0), 0
+    logits = np.stack(rows)
+    for b in range(batch):
+        keep, exits = _nucleus_facts(logits[b], cfg)
+        assert keep < HEAD and exits == want_exits, (b, keep, exits)
+    _check_against_oracle(hip, logits, cfg, 4, [71 + b for b in range(batch)])
+
+
+def test_sampler_nucleus_mixed_batch(hip):
+    """One call whose sequences split between the head path and the full sort (flat rows whose
+    nucleus reaches past 4096 ids, a row with a +inf logit, peaked rows), with penalties: every
+    sequence's id equals its own reference Sampler's, call after call (src/sampler.cpp:13-70)."""
+    V, batch = 32000, 8
+    print("[case] sampler nucleus mixed batch", flush=True)
+    g = D.rng(4242)
+    scales = [3.0, 1.0, 4.0, 0.5, 3.0, 1.0, 2.5, 3.0]
+    logits = np.stack([(g.standard_normal(V, dtype=np.float32) * np.float32(sc)).astype(np.float32)
+                       for sc in scales])
+    logits[6, 123] = np.float32(np.inf)
+    hist = g.integers(0, V, size=(batch, 32)).astype(np.int32)
+    cfg = dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.1)
+    heads = []
+    for b in range(batch):
+        if b != 6:
+            keep, _ = _nucleus_facts(logits[b], cfg, hist[b])
+            heads.append(keep < HEAD)
+    assert any(heads) and not all(heads), heads
+    _check_against_oracle(hip, logits, cfg, 4, [300 + b for b in range(batch)], hist=hist)
+
+
+def test_sampler_nucleus_bench_logits(hip):
+    """The bench's top-p-only sampler input (seeded N(0, 3) logits, T 0.8, repetition penalty 1.1,
+    64-token histories, B = 64): some rows' sums enter their last binade after the head.  Ids equal
+    the reference's (src/sampler.cpp:13-70)."""
+    V, batch = 32000, 64
+    print("[case] sampler nucleus bench logits B=64", flush=True)
+    g = np.random.default_rng(5)
+    logits = (g.standard_normal((batch, V), dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    hist = g.integers(0, V, size=(batch, 64)).astype(np.int32)
+    cfg = dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.1)
+    facts = [_nucleus_facts(logits[b], cfg, hist[b]) for b in range(batch)]
+    assert all(k < HEAD for k, _ in facts) and any(e > 0 for _, e in facts)
+    _check_against_oracle(hip, logits, cfg, 3, [7 + b for b in range(batch)], hist=hist)
