@@ -96,6 +96,33 @@ __device__ __forceinline__ float dot_f32_lds(const float* qv, const float* kv, i
   return ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7));
 }
 
+// dot_f32_lds for a compile-time length: the same partials and tree, every read issued first.
+template <int HD>
+__device__ __forceinline__ float dot_f32_lds_n(const float* qv, const float* kv) {
+  static_assert(HD % 8 == 0, "whole groups of eight");
+  float4 qa[HD / 8], qb[HD / 8], ka[HD / 8], kb[HD / 8];
+#pragma unroll
+  for (int i = 0; i < HD / 8; ++i) {
+    qa[i] = *reinterpret_cast<const float4*>(qv + 8 * i);
+    qb[i] = *reinterpret_cast<const float4*>(qv + 8 * i + 4);
+    ka[i] = *reinterpret_cast<const float4*>(kv + 8 * i);
+    kb[i] = *reinterpret_cast<const float4*>(kv + 8 * i + 4);
+  }
+  float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f, p5 = 0.0f, p6 = 0.0f, p7 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < HD / 8; ++i) {
+    p0 += qa[i].x * ka[i].x;
+    p1 += qa[i].y * ka[i].y;
+    p2 += qa[i].z * ka[i].z;
+    p3 += qa[i].w * ka[i].w;
+    p4 += qb[i].x * kb[i].x;
+    p5 += qb[i].y * kb[i].y;
+    p6 += qb[i].z * kb[i].z;
+    p7 += qb[i].w * kb[i].w;
+  }
+  return ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7));
+}
+
 __device__ __forceinline__ void stage_rows(float* dst, const float* cache, long kvd, const float* cur, int pos,
                                            int c0, int n, int hd) {
   // rows c0 .. c0+n-1 (n <= kAttnChunk) of one KV head, row `pos` from `cur`
@@ -552,7 +579,10 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
     __syncthreads();
     for (int pr = t; pr < hpg * kAttnChunk; pr += kGroupThreads) {
       const int hh = pr / kAttnChunk, r = pr - hh * kAttnChunk;
-      if (r < n) sc[hh * sp + c0 + r] = dot_f32_lds(qs + hh * hd, rows + r * ld, hd) * a.scale;
+      if (r < n)
+        sc[hh * sp + c0 + r] = (hd == 64 ? dot_f32_lds_n<64>(qs + hh * hd, rows + r * ld)
+                                         : dot_f32_lds(qs + hh * hd, rows + r * ld, hd)) *
+                               a.scale;
     }
     __syncthreads();
   }
@@ -615,7 +645,22 @@ __global__ __launch_bounds__(kGroupThreads) void attention_group_kernel(AttnArgs
       const int idx = t + u * kGroupThreads, hh = idx / hd, d = idx - hh * hd;
       if (hh < hpg) {
         const float* ph = sc + hh * sp + c0;
-        for (int r = 0; r < n; ++r) {
+        // eight positions' reads issued before their multiply-adds (the adds stay in order)
+        int r = 0;
+        for (; r + 8 <= n; r += 8) {
+          float pp[8], vv[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            pp[k] = ph[r + k];
+            vv[k] = vr[(r + k) * ld + d];
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float pv_ = pp[k] * inv[u];
+            o[u] += pv_ * vv[k];
+          }
+        }
+        for (; r < n; ++r) {
           const float pv_ = ph[r] * inv[u];
           o[u] += pv_ * vr[r * ld + d];
         }
