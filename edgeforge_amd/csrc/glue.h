@@ -28,6 +28,7 @@ struct AttnArgs {
   // results.  part == nullptr: no split.
   float* part;
   int splits, span;
+  int split_hpw;  // set by launch_attention: query heads per split workgroup (all of a group's, or half)
 };
 
 // Prefill of n positions per sequence at once: rows r = b * n + i hold position *pos_dev + i of

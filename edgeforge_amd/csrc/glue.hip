@@ -701,16 +701,14 @@ constexpr int kSplitRec = kSplitMaxHpg * kSplitHd + kSplitMaxHpg + 2 * kSplitMax
 constexpr int kSplitLd = kSplitHd + 4;  // floats between staged rows
 constexpr int kSplitPerThread = 16;  // splits whose o columns one thread holds in the combine
 constexpr int kSplitMaxSplits = 64;  // splits of one (sequence, group): the combine's wave lanes
-// Combine kernel LDS: sums (doubles) and weights per (split, head), tpc x cols float4 sub-sums,
-// 1 / sum per head.
-constexpr size_t kCombineLds =
-    (2 * kSplitMaxSplits * kSplitMaxHpg + kSplitMaxSplits * kSplitMaxHpg + 4 * kSplitThreads + kSplitMaxHpg) *
-    sizeof(float);
-// The most splits the combine takes for hpg query heads per KV head (tpc threads per column).
-__host__ __device__ constexpr int split_max(int hpg) {
-  return kSplitPerThread * (kSplitThreads / (hpg * kSplitHd / 4)) < kSplitMaxSplits
-             ? kSplitPerThread * (kSplitThreads / (hpg * kSplitHd / 4))
-             : kSplitMaxSplits;
+// Combine kernel LDS (one query head per workgroup): sums (doubles) and weights per split, tpc x
+// cols float4 sub-sums, 1 / sum.
+constexpr size_t kCombineLds = (2 * kSplitMaxSplits + kSplitMaxSplits + 4 * kSplitThreads + 1) * sizeof(float);
+// The most splits the combine takes (one wave's lanes form the weights; each thread holds up to
+// kSplitPerThread of them for its column).
+__host__ __device__ constexpr int split_max(int) {
+  return kSplitPerThread * (kSplitThreads / (kSplitHd / 4)) < kSplitMaxSplits ? kSplitPerThread * (kSplitThreads / (kSplitHd / 4))
+                                                                               : kSplitMaxSplits;
 }
 
 size_t attention_split_lds_bytes(int hpg, int span) {
@@ -722,8 +720,9 @@ size_t attention_split_lds_bytes(int hpg, int span) {
 template <bool EAGER>
 __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs a) {
   extern __shared__ float sm[];
-  const int j = blockIdx.x, g = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
-  const int hpg = a.H / a.KV, kvd = a.KV * kSplitHd, span = a.span;
+  const int hpg = a.split_hpw, parts = a.H / a.KV / hpg;  // this workgroup's query heads: h0 .. h0 + hpg - 1
+  const int j = blockIdx.x, g = blockIdx.y / parts, h0 = (blockIdx.y - g * parts) * hpg, b = blockIdx.z, t = threadIdx.x;
+  const int kvd = a.KV * kSplitHd, span = a.span;
   float* qs = sm;                                 // [hpg][64] roped queries
   float* kn = qs + hpg * kSplitHd;                // [64] roped new key
   float* vn = kn + kSplitHd;                      // [64] new value
@@ -742,7 +741,7 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs
   // the new k / v, and (split 0 always, every split with EAGER) the first sub-chunk's cache rows.
   // Without EAGER, the other splits request their rows once the position shows they have work.
   const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.pos_dev, 4u), 0u, 0u, 0);
-  const float* q = a.q + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
+  const float* q = a.q + static_cast<long>(b) * a.ldq + (g * hpg * parts + h0) * kSplitHd;
   const float* k_new = a.knew + static_cast<long>(b) * kvd + g * kSplitHd;
   const int hq = t >> 5, iq = t & 31;
   float qa = 0.0f, qb = 0.0f, cq = 0.0f, sq = 0.0f, ka = 0.0f, kb = 0.0f, vnew = 0.0f;
@@ -788,8 +787,10 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs
     const float k = t < 32 ? ka * cq - kb * sq : kb * cq + ka * sq;
     kn[t] = k;
     vn[t] = vnew;
-    a.kcache[seq0 + static_cast<long>(pos) * kvd + t] = k;
-    a.vcache[seq0 + static_cast<long>(pos) * kvd + t] = vnew;
+    if (h0 == 0) {
+      a.kcache[seq0 + static_cast<long>(pos) * kvd + t] = k;
+      a.vcache[seq0 + static_cast<long>(pos) * kvd + t] = vnew;
+    }
   }
   __syncthreads();
   // staged rows past the split's last position are zeros: p.v runs over whole 64-row sub-chunks
@@ -884,7 +885,7 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs
     }
     __syncthreads();
   }
-  float* out = a.ctx + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + (g * hpg * parts + h0) * kSplitHd;
   if (n_act == 1) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -899,59 +900,53 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(AttnArgs
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int idx = t + u * kSplitThreads;
-      if (idx < hpg * kSplitHd) rec[idx] = o[u];
+      if (idx < hpg * kSplitHd) rec[h0 * kSplitHd + idx] = o[u];
     }
     if (t < hpg) {
-      rec[kSplitMaxHpg * kSplitHd + t] = s_m[t];
-      reinterpret_cast<double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[t] = s_l[t];
+      rec[kSplitMaxHpg * kSplitHd + h0 + t] = s_m[t];
+      reinterpret_cast<double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[h0 + t] = s_l[t];
     }
   }
 }
 
-// The combine of the position-split attention: one workgroup per (KV group g, sequence b), after
+// The combine of the position-split attention: one workgroup per (query head, sequence b), after
 // the split kernel (the kernel boundary makes every split's record visible).  With one split
 // active the split kernel has written ctx itself and this returns at once.
 template <bool EAGER>
 __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(AttnArgs a) {
   extern __shared__ float sm[];
-  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-  const int hpg = a.H / a.KV;
+  const int hpg = a.H / a.KV, g = blockIdx.x / hpg, hh = blockIdx.x - g * hpg, b = blockIdx.y, t = threadIdx.x;
   const float* recs = a.part + static_cast<long>(b * a.KV + g) * a.splits * kSplitRec;
-  float* out = a.ctx + static_cast<long>(b) * a.ldq + g * hpg * kSplitHd;
-  // Thread (sub, col) holds float4 column col of o for splits sub * per .. sub * per + per - 1
-  // (per from the split count, so the grouping does not depend on the position), all requested
-  // at once; the splits' maxima and sums go to LDS, a wave per head forms the weights (lanes =
-  // splits), each thread sums its splits in order, and the sub-sums are added in sub order.
-  // With EAGER the records are requested before the position is known (every record is in
-  // bounds; those of inactive splits are never used).
-  const int cols = hpg * kSplitHd / 4, tpc = kSplitThreads / cols, per = (a.splits + tpc - 1) / tpc;
+  float* out = a.ctx + static_cast<long>(b) * a.ldq + (g * hpg + hh) * kSplitHd;
+  // One query head per workgroup.  Thread (sub, col) holds float4 column col of the head's o for
+  // splits sub * per .. sub * per + per - 1 (per from the split count, so the grouping does not
+  // depend on the position), all requested at once; the splits' maxima and sums go to LDS, one
+  // wave forms the weights (lanes = splits), each thread sums its splits in order, and the
+  // sub-sums are added in sub order.  With EAGER the records are requested before the position is
+  // known (every record is in bounds; those of inactive splits are never used).
+  constexpr int cols = kSplitHd / 4, tpc = kSplitThreads / cols;
+  const int per = (a.splits + tpc - 1) / tpc;
   const int col = t % cols, sub = t / cols;
-  const bool active = sub < tpc;
-  double* cl = reinterpret_cast<double*>(sm);                                  // [n_act][hpg] sums
-  float* cw = reinterpret_cast<float*>(cl + kSplitMaxSplits * kSplitMaxHpg);   // [n_act][hpg] maxima, then weights
-  float4* cred = reinterpret_cast<float4*>(cw + kSplitMaxSplits * kSplitMaxHpg);  // [tpc][cols] sub-sums
-  float* cinv = reinterpret_cast<float*>(cred + kSplitThreads);                 // [hpg] 1 / sum_j w_j l_j
+  double* cl = reinterpret_cast<double*>(sm);                 // [splits] sums
+  float* cw = reinterpret_cast<float*>(cl + kSplitMaxSplits);  // [splits] maxima, then weights
+  float4* cred = reinterpret_cast<float4*>(cw + kSplitMaxSplits);  // [tpc][cols] sub-sums
+  float* cinv = reinterpret_cast<float*>(cred + kSplitThreads);    // 1 / sum_j w_j l_j
   float4 ov[kSplitPerThread];
   auto fetch = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < kSplitPerThread; ++q) {
       const int sj = sub * per + q;
-      if (active && q < per && sj < a.splits)
-        ov[q] = reinterpret_cast<const float4*>(recs + static_cast<long>(sj) * kSplitRec)[col];
+      if (q < per && sj < a.splits)
+        ov[q] = reinterpret_cast<const float4*>(recs + static_cast<long>(sj) * kSplitRec + hh * kSplitHd)[col];
     }
   };
-  // the maxima and sums: (split, head) pairs t and t + 256 (at most 64 x 8 pairs)
-  float mv[2];
-  double lv[2];
+  float mv = 0.0f;
+  double lv = 0.0;
   auto fetch_ml = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = t + k * kSplitThreads, sj = i / hpg, hh = i - sj * hpg;
-      if (sj < a.splits) {
-        const float* rec = recs + static_cast<long>(sj) * kSplitRec;
-        mv[k] = rec[kSplitMaxHpg * kSplitHd + hh];
-        lv[k] = reinterpret_cast<const double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[hh];
-      }
+    if (t < a.splits) {
+      const float* rec = recs + static_cast<long>(t) * kSplitRec;
+      mv = rec[kSplitMaxHpg * kSplitHd + hh];
+      lv = reinterpret_cast<const double*>(rec + kSplitMaxHpg * kSplitHd + kSplitMaxHpg)[hh];
     }
   };
   const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.pos_dev, 4u), 0u, 0u, 0);
@@ -965,41 +960,28 @@ __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(AttnAr
     fetch_ml();
     fetch();
   }
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = t + k * kSplitThreads;
-    if (i < n_act * hpg) {
-      cw[i] = mv[k];
-      cl[i] = lv[k];
-    }
+  if (t < kWave) {  // the weights: lane = split
+    const float m = t < n_act ? mv : -INFINITY;
+    const float M = wave_max_dpp(m);
+    const float w = t < n_act ? expf(m - M) : 0.0f;
+    const double L = wave_sum_d_dpp(t < n_act ? lv * static_cast<double>(w) : 0.0);
+    cw[t] = w;
+    if (t == 0) cinv[0] = static_cast<float>(1.0 / L);
   }
   __syncthreads();
-  {
-    const int wave = t / kWave, lane = t & (kWave - 1);
-    for (int hh = wave; hh < hpg; hh += kSplitThreads / kWave) {
-      const float m = lane < n_act ? cw[lane * hpg + hh] : -INFINITY;
-      const float M = wave_max_dpp(m);
-      const float w = lane < n_act ? expf(m - M) : 0.0f;
-      const double L = wave_sum_d_dpp(lane < n_act ? cl[lane * hpg + hh] * static_cast<double>(w) : 0.0);
-      if (lane < n_act) cw[lane * hpg + hh] = w;
-      if (lane == 0) cinv[hh] = static_cast<float>(1.0 / L);
-    }
-  }
-  __syncthreads();
-  const int hh = (col * 4) / kSplitHd;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
   for (int q = 0; q < kSplitPerThread; ++q) {
     const int sj = sub * per + q;
-    if (active && q < per && sj < n_act) {
-      const float w = cw[sj * hpg + hh];
+    if (q < per && sj < n_act) {
+      const float w = cw[sj];
       acc.x += ov[q].x * w;
       acc.y += ov[q].y * w;
       acc.z += ov[q].z * w;
       acc.w += ov[q].w * w;
     }
   }
-  if (active) cred[sub * cols + col] = acc;
+  cred[sub * cols + col] = acc;
   __syncthreads();
   if (sub == 0) {
     float4 r = cred[col];
@@ -1010,7 +992,7 @@ __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(AttnAr
       r.z += v.z;
       r.w += v.w;
     }
-    const float iv = cinv[hh];
+    const float iv = cinv[0];
     r.x *= iv;
     r.y *= iv;
     r.z *= iv;
@@ -1400,19 +1382,26 @@ int launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
                   a.splits <= split_max(a.H / a.KV),
               "attention: position split does not fit the shape");
     // the rows of every split requested before the position is known when that costs at most
-    // 128 workgroups' worth (about 4 MB) of reads at short positions
+    // 128 workgroups' worth (about 4 MB) of reads at short positions; then each (split, group)
+    // also splits its query heads over two workgroups (both stage the same rows) so that the
+    // launch reaches every CU
     const bool eager = static_cast<long>(a.splits) * a.KV * batch <= 128;
-    const size_t lds = attention_split_lds_bytes(a.H / a.KV, a.span);
+    AttnArgs sa = a;
+    const int hpg = a.H / a.KV, parts = eager && hpg % 2 == 0 ? 2 : 1;
+    sa.split_hpw = hpg / parts;
+    const size_t lds = attention_split_lds_bytes(sa.split_hpw, a.span);
     if (eager) {
-      hipLaunchKernelGGL(attention_split_kernel<true>, dim3(a.splits, a.KV, batch), dim3(kSplitThreads), lds, s, a);
+      hipLaunchKernelGGL(attention_split_kernel<true>, dim3(a.splits, a.KV * parts, batch), dim3(kSplitThreads), lds, s,
+                         sa);
     } else {
-      hipLaunchKernelGGL(attention_split_kernel<false>, dim3(a.splits, a.KV, batch), dim3(kSplitThreads), lds, s, a);
+      hipLaunchKernelGGL(attention_split_kernel<false>, dim3(a.splits, a.KV * parts, batch), dim3(kSplitThreads), lds,
+                         s, sa);
     }
     EFH_HIP(hipGetLastError());
     if (eager) {
-      hipLaunchKernelGGL(attention_combine_kernel<true>, dim3(a.KV, batch), dim3(kSplitThreads), kCombineLds, s, a);
+      hipLaunchKernelGGL(attention_combine_kernel<true>, dim3(a.H, batch), dim3(kSplitThreads), kCombineLds, s, a);
     } else {
-      hipLaunchKernelGGL(attention_combine_kernel<false>, dim3(a.KV, batch), dim3(kSplitThreads), kCombineLds, s, a);
+      hipLaunchKernelGGL(attention_combine_kernel<false>, dim3(a.H, batch), dim3(kSplitThreads), kCombineLds, s, a);
     }
     EFH_HIP(hipGetLastError());
     return EF_HIP_OK;
