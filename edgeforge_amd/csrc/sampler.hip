@@ -1378,26 +1378,22 @@ __device__ void sample_tail_scan(const SampleArgs& a, int b, const uint64_t* sor
   if (tid == 0) a.out[b] = static_cast<int>(key_id(sorted[i < kp ? i : kp - 1]));
 }
 
-// ---- top-p without top-k: the nucleus from the kTopM largest keys ----------------------------------------
+// ---- top-p without top-k: the nucleus from the head of the order --------------------------------------
 // The reference sorts the whole vocabulary (src/sampler.cpp:36-38), adds every softmax term in that
 // order (:42-48), cuts the nucleus (:50-61) and walks it (:62-69).  When the nucleus ends within the
-// kTopM largest keys only those need their order: one workgroup per sequence selects them (radix
-// select on the keys in registers), sorts them in LDS and takes the head's sum, the cut and the
-// walk with exact_scan.  The other V - kTopM terms (the tail) join the sum by exact_scan's binade
+// head of the order only the head needs its order: one workgroup per sequence takes the keys within
+// a bucket bound of the maximum (at most kTopM), sorts them in LDS and takes the head's sum, the cut
+// and the walk with exact_scan.  The other terms (the tail) join the sum by exact_scan's binade
 // argument, which needs no order: while the running sum s stays in [2^e, 2^(e+1)) a step adds
 // rint(t / u) u, u = 2^(e-52), unless t / u is halfway between integers (a tie, rounded by the
 // parity of s).  So the tail adds K u, K = the sum of rint(t / u) over it, when s / u + K < 2^53 and
-// no tail term is a tie.  When the sum leaves its binade inside the tail, the step that does it is
-// found without sorting: the largest tail key c at which s / u + (the sum of rint(t / u) over the
-// keys in [c, s's last key)) reaches 2^53, by a radix select weighted by rint(t / u) (the weights
-// are integers below 2^53, so their double sums are exact or, past 2^53, still compare correctly
-// with a bound below it); the steps before c are exact, c's step is the reference's plain add, and
-// the rest of the tail continues from there.  A tail tie, a term that is not finite, or a nucleus
-// that reaches past the head leaves the sequence to the full sort (the flag in its workspace), whose
+// no tail term is a tie.  When the sum leaves its binade in the tail, the next buckets (at most
+// kTopM - 1 keys) are sorted and added in order after the head's sum, and the rest is checked
+// again.  A sum that still leaves its binade, a tie, a term that is not finite, or a nucleus that
+// reaches past the head leaves the sequence to the full sort (the flag in its workspace), whose
 // launches follow and return at once for every other sequence.
 constexpr int kTopM = kChunk;              // the sorted head: one register chunk sort
 constexpr int kTopPer = kTopM / kThreads;  // head terms per thread in the scans (contiguous)
-constexpr int kMaxTailEvents = 64;         // binade exits taken in the tail before the full sort takes over
 
 // The logit whose order bits are u (the high half of a key).
 __device__ __forceinline__ float ob_value(uint32_t u) { return key_value(static_cast<uint64_t>(u) << 32); }
@@ -1467,159 +1463,96 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   return m;
 }
 
-// The tail's binade exits (see above).  Each round forms every id's key again from its logit (the
-// penalty marks still in s_seen) and the weight rint(t / u) of those below `above` (0 for the rest),
-// both into the (otherwise idle) sort buffers of the workspace, id t + kThreads j read back only by
-// thread t.  If the rest stays in the binade the sum is final; otherwise a radix select weighted by
-// them finds the key c whose step leaves it: the steps before c are exact, c's step is the
-// reference's add, and the next round starts below c.  Returns 1 with s the whole sum, or 0 (a tie,
-// or more than kMaxTailEvents exits) for the full sort.  hist: kWaves * 256 doubles of LDS.
-__device__ int tail_exits(const SampleArgs& a, int b, double& s, uint64_t above, float mx, const uint32_t* s_seen,
-                          const uint64_t* etab, uint64_t* hist_mem, uint32_t* s_cnt, double* s_dig, double* s_sfx,
-                          double* s_red, uint64_t* s_redk, double& s_before, int& s_digit) {
-  constexpr int kWaves = kThreads / kWave;
-  constexpr int kBatchExp = 4;  // logit loads issued together
-  const int tid = threadIdx.x, wave = tid / kWave, V = a.vocab;
-  const float* lg = a.logits + b * a.ld;
-  uint64_t* wk = keys_of(a, b);
-  double* wt = reinterpret_cast<double*>(merged_of(a, b));
-  double* hist = reinterpret_cast<double*>(hist_mem);
-  // every id's key and, for the tail, its term exp(v - max) (0 for the head): formed once
-  for (int j0 = 0; j0 < kRegSlots; j0 += kBatchExp) {  // the tempered logits again, as load_tempered forms them
-    float v[kBatchExp];
+
+// The keys of the slots whose bit is set in `in` (slot j of thread t: id t + kThreads j, order bits
+// ob[j]) into keys[0, n) in wave order, then slot order, then lane order, keys[n, kTopM) zeros
+// (below every key), sorted descending (keys[0, 2 kTopM) is the sort's exchange).  Returns n; more
+// than kTopM keys gather nothing.  s_cnt: one int per wave.  Every thread calls it.
+__device__ __forceinline__ int gather_sort(const uint32_t (&ob)[kRegSlots], uint32_t in, uint64_t* keys, int* s_cnt) {
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  int cnt = 0;
 #pragma unroll
-    for (int u = 0; u < kBatchExp; ++u) {
-      const int id = tid + kThreads * (j0 + u);
-      v[u] = id < V ? lg[id] : 0.0f;
-    }
+  for (int j = 0; j < kRegSlots; ++j) cnt += __popcll(__ballot(in >> j & 1u));
+  if (lane == 0) s_cnt[wave] = cnt;
+  __syncthreads();
+  int pos = 0, n = 0;
+  for (int w = 0; w < kThreads / kWave; ++w) {
+    pos += w < wave ? s_cnt[w] : 0;
+    n += s_cnt[w];
+  }
+  __syncthreads();  // s_cnt is reused by the caller
+  if (n > kTopM) return n;
 #pragma unroll
-    for (int u = 0; u < kBatchExp; ++u) {
-      const int id = tid + kThreads * (j0 + u);
-      if (id < V) {
-        float x = v[u];
-        if (a.penalty != 1.0f && (s_seen[id >> 5] >> (id & 31) & 1u))
-          x = x > 0.0f ? __fdiv_rn(x, a.penalty) : x * a.penalty;
-        x = __fdiv_rn(x, a.temperature);
-        const uint64_t k = make_key(x, static_cast<uint32_t>(id));
-        wk[id] = k;
-        wt[id] = k < above ? exp_libm(static_cast<double>(x - mx), etab) : 0.0;
-      }
-    }
+  for (int j = 0; j < kRegSlots; ++j) {
+    const bool take = in >> j & 1u;
+    const uint64_t m = __ballot(take);
+    const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+    if (take)
+      keys[pos + r] = (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
+    pos += __popcll(m);
   }
-  // visit(sc, f): f(key, rint(t 2^sc)) for this thread's slots below `above` with the prefix and a
-  // nonzero weight
-  uint64_t prefix = 0, mask = 0;
-  auto visit = [&](int sc, auto&& f) {
-#pragma unroll 4
-    for (int j = 0; j < kRegSlots; ++j) {
-      const int id = tid + kThreads * j;
-      const double t = id < V ? wt[id] : 0.0;
-      const uint64_t k = id < V ? wk[id] : 0ull;
-      if (t != 0.0 && k < above && (k & mask) == prefix) {
-        const double r = rint(ldexp(t, sc));
-        if (r != 0.0) f(k, r);
-      }
-    }
-  };
-  for (int ev = 0; ev < kMaxTailEvents; ++ev) {
-    int ex;
-    (void)frexp(s, &ex);
-    const int sc = 53 - ex;
-    const double M0 = ldexp(s, sc);
-    double T = 0.0;
-    uint64_t tie = 0;
-    prefix = 0;
-    mask = 0;
-#pragma unroll 4
-    for (int j = 0; j < kRegSlots; ++j) {
-      const int id = tid + kThreads * j;
-      const double t = id < V ? wt[id] : 0.0;
-      const uint64_t k = id < V ? wk[id] : 0ull;
-      if (t != 0.0 && k < above) {
-        const double y = ldexp(t, sc), r = rint(y);
-        T += r;
-        if (fabs(y - r) == 0.5) tie = k > tie ? k : tie;
-      }
-    }
-    T = block_sum_d(T, s_red);
-    tie = block_max_u64(tie, s_redk);
-    if (tie != 0) return 0;
-    if (M0 + T < 0x1p53) {
-      s = ldexp(M0 + T, -sc);
-      return 1;
-    }
-    const double need = 0x1p53 - M0;  // exact
-    double before = 0.0;  // weights of the keys above the digit range in play (exact: below need)
-    for (int shift = 56; shift >= 0; shift -= 8) {
-      for (int i = tid; i < kWaves * 256; i += kThreads) hist[i] = 0.0;
-      if (tid < 256) s_cnt[tid] = 0u;
-      __syncthreads();
-      visit(sc, [&](uint64_t k, double r) {
-        const int d = static_cast<int>((k >> shift) & 255u);
-        atomicAdd(&hist[wave * 256 + d], r);
-        atomicAdd(&s_cnt[d], 1u);
-      });
-      __syncthreads();
-      // the digit d with W(d) >= need > W(d + 1), W(d) = before + the weights of digits >= d:
-      // suffix sums, a wave per 64 digits (W(d + 1) < need <= 2^52 is exact; a W(d) past 2^53 is
-      // rounded but still >= need, so exactly one digit qualifies; the sums are monotone in d)
-      if (tid < 256) {
-        double c = 0.0;
-        for (int w = 0; w < kWaves; ++w) c += hist[w * 256 + tid];
-        s_dig[tid] = c;
-        const int ln = tid & (kWave - 1);
-        double sfx = c;  // inclusive suffix over this wave's digits >= d
-        for (int o = 1; o < kWave; o <<= 1) {
-          const double v = __shfl_down(sfx, o, kWave);
-          if (ln + o < kWave) sfx += v;
-        }
-        s_sfx[tid] = sfx;
-      }
-      __syncthreads();
-      if (tid < 256) {
-        const int d = tid, ln = d & (kWave - 1);
-        double hi = before;  // before + the waves of higher digits
-        for (int w = d / kWave + 1; w < 4; ++w) hi += s_sfx[w * kWave];
-        const double w_d = hi + s_sfx[d], w_next = hi + (ln + 1 < kWave ? s_sfx[d + 1] : 0.0);
-        if ((w_d >= need || d == 0) && w_next < need) {
-          s_before = w_next;
-          s_digit = d;
-        }
-      }
-      __syncthreads();
-      before = uniform_d(s_before);
-      const int d = uniform_i(s_digit);
-      prefix |= static_cast<uint64_t>(d) << shift;
-      mask |= 255ull << shift;
-      const int alone = s_cnt[d] == 1u;
-      __syncthreads();
-      if (uniform_i(alone)) {  // one weighted key left in the bucket: its owner names it
-        visit(sc, [&](uint64_t k, double) { s_redk[0] = k; });
-        __syncthreads();
-        prefix = s_redk[0];
-        __syncthreads();
-        break;
-      }
-    }
-    // `prefix` is the exit's key: the steps before it are exact, its own is the reference's add
-    s = ldexp(M0 + before, -sc) + exp_libm(static_cast<double>(key_value(prefix) - mx), etab);
-    above = prefix;
+  for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
+  __syncthreads();
+  uint64_t x[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) x[u] = keys[4 * tid + u];
+  __syncthreads();
+  sort4096_desc(x, keys);
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) keys[4 * tid + u] = x[u];
+  __syncthreads();
+  return n;
+}
+
+// The nucleus cut, its renormalisation, the draw and the walk (src/sampler.cpp:49-69) over the
+// sorted head keys[0, M) with S the whole softmax sum; a cut past the head sets the flag for the
+// full sort (no draw).  Thread t holds head terms kTopPer t .. kTopPer t + kTopPer - 1.
+__device__ __forceinline__ void nucleus_finish(const SampleArgs& a, int b, const uint64_t* keys, int M, float mx, double S,
+                               const uint64_t* etab, ScanShared& sh, int32_t* flag) {
+  const int tid = threadIdx.x;
+  double tm[kTopPer];
+#pragma unroll
+  for (int i = 0; i < kTopPer; ++i) {
+    const int p = kTopPer * tid + i;
+    tm[i] = p < M ? exp_libm(static_cast<double>(key_value(keys[p]) - mx), etab) / S : 0.0;
   }
-  return 0;
+  double cum;
+  const int n = exact_scan<1, kTopPer, 32>(tm, M, static_cast<double>(a.top_p), sh, &cum);
+  if (n >= M) {  // the nucleus reaches past the head
+    if (tid == 0) *flag = 1;
+    return;
+  }
+  const int kp = n + 1;
+#pragma unroll
+  for (int i = 0; i < kTopPer; ++i) tm[i] = tm[i] / cum;
+  if (tid == 0) {
+    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
+    sh.hit_sum = mt_uniform(st);
+  }
+  __syncthreads();
+  const double r = sh.hit_sum;
+  __syncthreads();
+  double c2;
+  const int i = exact_scan<2, kTopPer, 32>(tm, kp, r, sh, &c2);
+  if (tid == 0) {
+    a.out[b] = static_cast<int>(key_id(keys[i < kp ? i : kp - 1]));
+    *flag = 0;
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   constexpr int kWaves = kThreads / kWave;
-  __shared__ uint64_t s_keys[2 * kChunk];  // the head's keys | the sort's exchange, then the weighted histograms
+  __shared__ uint64_t s_keys[2 * kChunk];  // the head's keys, and the sort's exchange buffers
   __shared__ ScanShared sh;
   __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64 + kWave];
   __shared__ int s_n[16];
   __shared__ uint32_t s_seen[(kRegSlots * kThreads + 31) / 32];
   __shared__ uint64_t s_exp[256];
-  __shared__ double s_red[kWaves], s_dig[256];
+  __shared__ double s_red[kWaves];
   __shared__ uint64_t s_redk[kWaves];
-  __shared__ int s_bad, s_digit;
-  __shared__ double s_before, s_sfx[256];
+  __shared__ int s_bad;
   const int b = blockIdx.x, V = a.vocab, tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   int32_t* flag = full_sort_flag(a, b);
   stage_exp_table(s_exp);
@@ -1635,9 +1568,6 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
 #pragma unroll
     for (int j = 0; j < kRegSlots; ++j) ob[j] = tid + kThreads * j < V ? order_bits(rv[j]) : 0u;
   }
-  auto key_of = [&](int j) {
-    return (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
-  };
   // the maximum (a NaN or infinite one: the full sort's rule)
   uint32_t om = 0;
 #pragma unroll
@@ -1693,47 +1623,11 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
     for (int j = 0; j < kRegSlots; ++j)
       if (tid + kThreads * j < V && bucket(j, mb) <= bmax) inh |= 1u << j;
   }
-  int M = 0;  // keys in the head
-  {
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) cnt += __popcll(__ballot(inh >> j & 1u));
-    if (lane == 0) s_n[wave] = cnt;
-    __syncthreads();
-    int pos = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      pos += w < wave ? s_n[w] : 0;
-      M += s_n[w];
-    }
-    if (M <= kTopM) {  // gathered in wave order, then slot order, then lane order
-#pragma unroll
-      for (int j = 0; j < kRegSlots; ++j) {
-        const bool in = inh >> j & 1u;
-        const uint64_t m = __ballot(in);
-        const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-        if (in) s_keys[pos + r] = key_of(j);
-        pos += __popcll(m);
-      }
-    }
-  }
+  const int M = gather_sort(ob, inh, s_keys, s_n);  // the head, sorted
   if (M > kTopM || M == 0) {  // cannot happen: bmax keeps at most kTopM keys and bucket 0 holds the maximum
     if (tid == 0) *flag = 1;
     return;
   }
-  for (int i = M + tid; i < kTopM; i += kThreads) s_keys[i] = 0ull;  // below every key
-  __syncthreads();
-  {
-    uint64_t x[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = s_keys[4 * tid + u];
-    __syncthreads();
-    sort4096_desc(x, s_keys);
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) s_keys[4 * tid + u] = x[u];
-  }
-  __syncthreads();
   double tm[kTopPer];
   bool finite = true;
 #pragma unroll
@@ -1752,65 +1646,85 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   }
   double s;
   exact_scan<0, kTopPer, 32>(tm, M, 0.0, sh, &s);
-  // the tail: every key below the head's last one.  One pass over the registers decides the
-  // common case (the sum stays in its binade, no tie).
-  int ok = 0;
-  {
+  // The tail: the slots not yet summed.  One pass over the registers: 1 when the rest stays in
+  // the sum's binade with no tie (the sum is then final), 2 when it leaves the binade, 0 for a tie
+  // or a NaN term (the full sort's rule).
+  auto tail = [&](uint32_t done, double& sum) {
     int ex;
-    (void)frexp(s, &ex);
-    const int sc = 53 - ex;  // s / u = s 2^sc, an integer in [2^52, 2^53)
-    const double M0 = ldexp(s, sc);
-    const uint64_t above = s_keys[M - 1];  // the tail: every key below the head's last
+    (void)frexp(sum, &ex);
+    const int sc = 53 - ex;  // sum / u = sum 2^sc, an integer in [2^52, 2^53)
+    const double M0 = ldexp(sum, sc);
     double T = 0.0;
     uint64_t tie = 0;
 #pragma unroll
     for (int j = 0; j < kRegSlots; ++j) {
-      if (tid + kThreads * j < V && !(inh >> j & 1u)) {
+      if (tid + kThreads * j < V && !(done >> j & 1u)) {
         const double y = ldexp(exp_libm(static_cast<double>(ob_value(ob[j]) - mx), s_exp), sc), r = rint(y);
         T += r;
-        if (fabs(y - r) == 0.5) tie = max(tie, key_of(j));
+        if (fabs(y - r) == 0.5) tie = 1;
       }
     }
     T = block_sum_d(T, s_red);
     tie = block_max_u64(tie, s_redk);
-    if (!(T == T)) {  // a NaN logit in the tail: the full sort's rule
-    } else if (tie == 0 && M0 + T < 0x1p53) {
-      s = ldexp(M0 + T, -sc);
-      ok = 1;
-    } else if (tie == 0) {
-      // The sum leaves its binade in the tail: each exit is found and taken in turn.
-      ok = tail_exits(a, b, s, above, mx, s_seen, s_exp, s_keys + kTopM, s_bh, s_dig, s_sfx, s_red, s_redk, s_before,
-                      s_digit);
+    if (!(T == T) || tie != 0) return 0;
+    if (M0 + T < 0x1p53) {
+      sum = ldexp(M0 + T, -sc);
+      return 1;
+    }
+    return 2;
+  };
+  int st = tail(inh, s);
+  if (st == 2) {
+    // The sum leaves its binade after the head: the next buckets (at most kTopM - 1 keys) sorted
+    // and added in order after the head's sum (a leading term s: 0 + s = s), then the rest again.
+    // The head's keys wait in the workspace meanwhile.
+    if (wave == 0) {
+      uint32_t c = 0;
+      for (int w = 0; w < kWaves; ++w) c += s_bh[w * 64 + lane];
+      uint32_t pre = c;
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t v = __shfl_up(pre, o, kWave);
+        if (lane >= o) pre += v;
+      }
+      const uint64_t fits = __ballot(lane < 63 && lane > bmax && pre - static_cast<uint32_t>(M) < kTopM);
+      if (lane == 0) s_n[0] = fits == 0 ? -1 : 63 - __builtin_clzll(fits);
+    }
+    __syncthreads();
+    const int bmax2 = s_n[0];
+    __syncthreads();
+    if (bmax2 < 0) {
+      st = 0;
+    } else {
+      uint64_t* hk = keys_of(a, b);
+      for (int p = tid; p < M; p += kThreads) hk[p] = s_keys[p];
+      uint32_t in2 = 0;
+      {
+        float mb = mx;
+        asm volatile("" : "+v"(mb));
+#pragma unroll
+        for (int j = 0; j < kRegSlots; ++j) {
+          const int bk = bucket(j, mb);
+          if (tid + kThreads * j < V && bk > bmax && bk <= bmax2) in2 |= 1u << j;
+        }
+      }
+      const int M2 = gather_sort(ob, in2, s_keys, s_n);
+      double t2[kTopPer];
+#pragma unroll
+      for (int i = 0; i < kTopPer; ++i) {
+        const int p = kTopPer * tid + i;
+        t2[i] = p == 0 ? s : (p - 1 < M2 ? exp_libm(static_cast<double>(key_value(s_keys[p - 1]) - mx), s_exp) : 0.0);
+      }
+      exact_scan<0, kTopPer, 32>(t2, M2 + 1, 0.0, sh, &s);
+      st = tail(inh | in2, s);
+      for (int p = tid; p < M; p += kThreads) s_keys[p] = hk[p];
+      __syncthreads();
     }
   }
-  if (!ok) {
+  if (st != 1) {
     if (tid == 0) *flag = 1;
     return;
   }
-#pragma unroll
-  for (int i = 0; i < kTopPer; ++i) tm[i] = tm[i] / s;
-  double cum;
-  const int n = exact_scan<1, kTopPer, 32>(tm, M, static_cast<double>(a.top_p), sh, &cum);
-  if (n >= M) {  // the nucleus reaches past the head
-    if (tid == 0) *flag = 1;
-    return;
-  }
-  const int kp = n + 1;
-#pragma unroll
-  for (int i = 0; i < kTopPer; ++i) tm[i] = tm[i] / cum;
-  if (tid == 0) {
-    MtState* st = reinterpret_cast<MtState*>(a.rng + static_cast<size_t>(b) * kRngStateBytes);
-    sh.hit_sum = mt_uniform(st);
-  }
-  __syncthreads();
-  const double r = sh.hit_sum;
-  __syncthreads();
-  double c2;
-  const int i = exact_scan<2, kTopPer, 32>(tm, kp, r, sh, &c2);
-  if (tid == 0) {
-    a.out[b] = static_cast<int>(key_id(s_keys[i < kp ? i : kp - 1]));
-    *flag = 0;
-  }
+  nucleus_finish(a, b, s_keys, M, mx, s, s_exp, sh, flag);
 }
 
 __device__ __forceinline__ int tail_keep(const SampleArgs& a) {
