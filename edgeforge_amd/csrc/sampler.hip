@@ -1607,11 +1607,19 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
       if (lane >= o) pre += v;
     }
     const uint64_t fits = __ballot(lane < 63 && pre <= static_cast<uint32_t>(kTopM));
-    if (lane == 0) s_n[0] = fits == 0 ? -1 : 63 - __builtin_clzll(fits);  // prefix counts rise with the bucket
+    const int bm = fits == 0 ? -1 : 63 - __builtin_clzll(fits);  // prefix counts rise with the bucket
+    // A nucleus that certainly reaches past the head goes to the full sort now: bucket b's terms
+    // lie in (e^-(b+1)/4, e^-b/4], so the head holds at most the first sum of the mass and the
+    // vocabulary at least the second (bucket 63 counted as 0); a 2% margin covers the float
+    // arithmetic of the bounds.
+    const float hi = lane <= bm ? static_cast<float>(c) * expf(-0.25f * static_cast<float>(lane)) : 0.0f;
+    const float lo = lane < 63 ? static_cast<float>(c) * expf(-0.25f * static_cast<float>(lane + 1)) : 0.0f;
+    const float head_hi = wave_sum(hi), all_lo = wave_sum(lo);
+    if (lane == 0) s_n[0] = bm >= 0 && head_hi < 0.98f * a.top_p * all_lo ? -2 : bm;
   }
   __syncthreads();
   const int bmax = s_n[0];  // the head: buckets <= bmax
-  if (bmax < 0) {  // more than kTopM keys within a quarter of the maximum
+  if (bmax < 0) {  // more than kTopM keys within a quarter of the maximum, or a nucleus past the head
     if (tid == 0) *flag = 1;
     return;
   }
