@@ -1146,7 +1146,7 @@ __device__ __forceinline__ double uniform_d(double v) {
 // the other lanes repeated the round.)  A round either ends the scan or takes one step, so n + 1
 // rounds suffice; the bound makes every wave's exit certain.
 template <int MODE, int PER = kScanPer, int HEAD = kScanHead>
-__device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& sh, double* sum) {
+__device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& sh, double* sum, double init = 0.0) {
   static_assert(HEAD <= kScanHead, "scan head");
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * PER;
   constexpr int kW = kThreads / kWave;
@@ -1162,7 +1162,7 @@ __device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& s
     // groups of eight: the next group's LDS reads issued before this group's chain of adds, the
     // running sums read off the chain for the predicate (terms past the head are exact zeros,
     // which leave a nonnegative sum unchanged)
-    double s = 0.0, hs = 0.0;
+    double s = init, hs = 0.0;
     int hit = n;
     double v[8];
 #pragma unroll
@@ -1465,43 +1465,106 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 
 
 // The keys of the slots whose bit is set in `in` (slot j of thread t: id t + kThreads j, order bits
-// ob[j]) into keys[0, n) in wave order, then slot order, then lane order, keys[n, kTopM) zeros
-// (below every key), sorted descending (keys[0, 2 kTopM) is the sort's exchange).  Returns n; more
-// than kTopM keys gather nothing.  s_cnt: one int per wave.  Every thread calls it.
-__device__ __forceinline__ int gather_sort(const uint32_t (&ob)[kRegSlots], uint32_t in, uint64_t* keys, int* s_cnt) {
+// ob[j]) sorted descending into keys[0, n), keys[n, kTopM) zeros (below every key); keys[0, 2 kTopM)
+// is the working space.  Returns n; more than kTopM keys sort nothing.  A bucket sort: fine bins
+// of the logit, floor(64 (max - v)) (monotone in v, so bin order is key order), counted, their
+// exclusive prefix giving each bin's place, the keys scattered to their bins, and each key's place
+// inside its bin counted among the bin's keys.  A bin of more than kFineMax keys (many equal or
+// nearly equal logits) takes the bitonic sort instead.  s_bin, s_start: 1024 and 1025 words of
+// LDS; s_cnt: one int per wave.  Every thread calls it.
+constexpr int kFineBins = 1024;  // covers max - v < 16, past every head bucket
+constexpr int kFineMax = 256;
+
+__device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t in, float mx, uint64_t* keys,
+                                           uint32_t* s_bin, uint32_t* s_start, int* s_cnt) {
+  static_assert(kFineBins == kThreads, "one bin per thread");
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  auto fine = [&](float v) {
+    const float d = (mx - v) * 64.0f;
+    return d < static_cast<float>(kFineBins - 1) ? static_cast<int>(d) : kFineBins - 1;
+  };
+  auto key_at = [&](int j) {
+    return (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
+  };
+  s_bin[tid] = 0u;
   int cnt = 0;
 #pragma unroll
   for (int j = 0; j < kRegSlots; ++j) cnt += __popcll(__ballot(in >> j & 1u));
   if (lane == 0) s_cnt[wave] = cnt;
   __syncthreads();
-  int pos = 0, n = 0;
+  int n = 0, wpos = 0;
   for (int w = 0; w < kThreads / kWave; ++w) {
-    pos += w < wave ? s_cnt[w] : 0;
+    wpos += w < wave ? s_cnt[w] : 0;
     n += s_cnt[w];
   }
-  __syncthreads();  // s_cnt is reused by the caller
-  if (n > kTopM) return n;
+  if (n > kTopM) {
+    __syncthreads();  // s_cnt is reused by the caller
+    return n;
+  }
 #pragma unroll
-  for (int j = 0; j < kRegSlots; ++j) {
-    const bool take = in >> j & 1u;
-    const uint64_t m = __ballot(take);
-    const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-    if (take)
-      keys[pos + r] = (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
-    pos += __popcll(m);
+  for (int j = 0; j < kRegSlots; ++j)
+    if (in >> j & 1u) atomicAdd(&s_bin[fine(ob_value(ob[j]))], 1u);
+  __syncthreads();
+  // each bin's place: exclusive prefix over the bins (a wave per 64 bins, then the waves in order)
+  const uint32_t c = s_bin[tid];
+  uint32_t inc = c;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += v;
+  }
+  const uint32_t wmax = wave_max_u32_dpp(c);
+  __syncthreads();  // every wave has read s_cnt
+  if (lane == kWave - 1) s_cnt[wave] = static_cast<int>(inc);
+  if (lane == 0) s_start[kFineBins + 1 + wave] = wmax;  // scratch past the prefix: the waves' largest bins
+  __syncthreads();
+  uint32_t below = 0, big = 0;
+  for (int w = 0; w < kThreads / kWave; ++w) {
+    below += w < wave ? static_cast<uint32_t>(s_cnt[w]) : 0u;
+    big = max(big, s_start[kFineBins + 1 + w]);
+  }
+  const uint32_t start = below + inc - c;
+  s_start[tid] = start;
+  if (tid == 0) s_start[kFineBins] = static_cast<uint32_t>(n);
+  s_bin[tid] = start;  // the scatter's cursor
+  __syncthreads();
+  if (big > kFineMax) {  // the bitonic sort: gathered in wave, slot and lane order
+    int pos = wpos;
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) {
+      const bool take = in >> j & 1u;
+      const uint64_t m = __ballot(take);
+      const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+      if (take) keys[pos + r] = key_at(j);
+      pos += __popcll(m);
+    }
+    for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
+    __syncthreads();
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = keys[4 * tid + u];
+    __syncthreads();
+    sort4096_desc(x, keys);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) keys[4 * tid + u] = x[u];
+    __syncthreads();
+    return n;
+  }
+  uint64_t* scat = keys + kTopM;  // the keys grouped by bin
+#pragma unroll
+  for (int j = 0; j < kRegSlots; ++j)
+    if (in >> j & 1u) scat[atomicAdd(&s_bin[fine(ob_value(ob[j]))], 1u)] = key_at(j);
+  __syncthreads();
+  for (int p = tid; p < n; p += kThreads) {
+    const uint64_t k = scat[p];
+    const int fb = fine(key_value(k));
+    const int b0 = static_cast<int>(s_start[fb]), b1 = static_cast<int>(s_start[fb + 1]);
+    int r = 0;
+    for (int q = b0; q < b1; ++q) r += scat[q] > k ? 1 : 0;
+    keys[b0 + r] = k;
   }
   for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
-  __syncthreads();
-  uint64_t x[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) x[u] = keys[4 * tid + u];
-  __syncthreads();
-  sort4096_desc(x, keys);
-  __syncthreads();
-#pragma unroll
-  for (int u = 0; u < 4; ++u) keys[4 * tid + u] = x[u];
   __syncthreads();
   return n;
 }
@@ -1548,7 +1611,8 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   __shared__ ScanShared sh;
   __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64 + kWave];
   __shared__ int s_n[16];
-  __shared__ uint32_t s_seen[(kRegSlots * kThreads + 31) / 32];
+  __shared__ uint32_t s_seen[(kRegSlots * kThreads + 31) / 32];  // the history marks, then the fine bins
+  __shared__ uint32_t s_start[kFineBins + 1 + kWaves];
   __shared__ uint64_t s_exp[256];
   __shared__ double s_red[kWaves];
   __shared__ uint64_t s_redk[kWaves];
@@ -1631,29 +1695,6 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
     for (int j = 0; j < kRegSlots; ++j)
       if (tid + kThreads * j < V && bucket(j, mb) <= bmax) inh |= 1u << j;
   }
-  const int M = gather_sort(ob, inh, s_keys, s_n);  // the head, sorted
-  if (M > kTopM || M == 0) {  // cannot happen: bmax keeps at most kTopM keys and bucket 0 holds the maximum
-    if (tid == 0) *flag = 1;
-    return;
-  }
-  double tm[kTopPer];
-  bool finite = true;
-#pragma unroll
-  for (int i = 0; i < kTopPer; ++i) {
-    const int p = kTopPer * tid + i;
-    tm[i] = p < M ? exp_libm(static_cast<double>(key_value(s_keys[p]) - mx), s_exp) : 0.0;
-    finite = finite && isfinite(tm[i]);
-  }
-  if (tid == 0) s_bad = 0;
-  __syncthreads();
-  if (!finite) s_bad = 1;
-  __syncthreads();
-  if (uniform_i(s_bad)) {  // NaN terms: the full sort's rule
-    if (tid == 0) *flag = 1;
-    return;
-  }
-  double s;
-  exact_scan<0, kTopPer, 32>(tm, M, 0.0, sh, &s);
   // The tail: the slots not yet summed.  One pass over the registers: 1 when the rest stays in
   // the sum's binade with no tie (the sum is then final), 2 when it leaves the binade, 0 for a tie
   // or a NaN term (the full sort's rule).
@@ -1681,20 +1722,55 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
     }
     return 2;
   };
-  int st = tail(inh, s);
-  if (st == 2) {
-    // The sum leaves its binade after the head: the next buckets (at most kTopM - 1 keys) sorted
-    // and added in order after the head's sum (a leading term s: 0 + s = s), then the rest again.
-    // The head's keys wait in the workspace meanwhile.
-    if (wave == 0) {
-      uint32_t c = 0;
-      for (int w = 0; w < kWaves; ++w) c += s_bh[w * 64 + lane];
-      uint32_t pre = c;
+  // Chunk 0 is the head: sorted, summed from 0, then the tail checked.  When the sum leaves its
+  // binade after the head, chunk 1 (the next buckets, at most kTopM keys) is sorted and added
+  // in order from the head's sum and the rest checked again; the
+  // head's keys wait in the workspace meanwhile.  (One loop, not two copies: the second copy made
+  // the kernel spill.)
+  int M = 0, st = 0;
+  double s = 0.0;
+  uint32_t done = 0, mask = inh;
+  uint64_t* hk = keys_of(a, b);
+#pragma unroll 1
+  for (int c = 0; c < 2; ++c) {
+    // keys, bins and terms are formed again in each chunk (hoisted out of the loop, they spill)
+#pragma unroll
+    for (int j = 0; j < kRegSlots; ++j) asm volatile("" : "+v"(ob[j]));
+    const int n = gather_sort(ob, mask, mx, s_keys, s_seen, s_start, s_n);
+    if (c == 0) M = n;
+    if (n > kTopM || (c == 0 && n == 0)) {  // cannot happen: the buckets were chosen to fit
+      st = 0;
+      break;
+    }
+    double tm[kTopPer];
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < kTopPer; ++i) {
+      const int p = kTopPer * tid + i;
+      tm[i] = p < n ? exp_libm(static_cast<double>(key_value(s_keys[p]) - mx), s_exp) : 0.0;
+      finite = finite && isfinite(tm[i]);
+    }
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    if (!finite) s_bad = 1;
+    __syncthreads();
+    if (uniform_i(s_bad)) {  // NaN terms: the full sort's rule
+      st = 0;
+      break;
+    }
+    exact_scan<0, kTopPer, 32>(tm, n, 0.0, sh, &s, s);  // chunk 1 continues from the head's sum
+    done |= mask;
+    st = tail(done, s);
+    if (st != 2 || c == 1) break;
+    if (wave == 0) {  // chunk 1: the buckets after the head's whose keys fit
+      uint32_t cb = 0;
+      for (int w = 0; w < kWaves; ++w) cb += s_bh[w * 64 + lane];
+      uint32_t pre = cb;
       for (int o = 1; o < kWave; o <<= 1) {
         const uint32_t v = __shfl_up(pre, o, kWave);
         if (lane >= o) pre += v;
       }
-      const uint64_t fits = __ballot(lane < 63 && lane > bmax && pre - static_cast<uint32_t>(M) < kTopM);
+      const uint64_t fits = __ballot(lane < 63 && lane > bmax && pre - static_cast<uint32_t>(M) <= kTopM);
       if (lane == 0) s_n[0] = fits == 0 ? -1 : 63 - __builtin_clzll(fits);
     }
     __syncthreads();
@@ -1702,35 +1778,25 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
     __syncthreads();
     if (bmax2 < 0) {
       st = 0;
-    } else {
-      uint64_t* hk = keys_of(a, b);
-      for (int p = tid; p < M; p += kThreads) hk[p] = s_keys[p];
-      uint32_t in2 = 0;
-      {
-        float mb = mx;
-        asm volatile("" : "+v"(mb));
+      break;
+    }
+    for (int p = tid; p < M; p += kThreads) hk[p] = s_keys[p];
+    float mb = mx;
+    asm volatile("" : "+v"(mb));
+    mask = 0;
 #pragma unroll
-        for (int j = 0; j < kRegSlots; ++j) {
-          const int bk = bucket(j, mb);
-          if (tid + kThreads * j < V && bk > bmax && bk <= bmax2) in2 |= 1u << j;
-        }
-      }
-      const int M2 = gather_sort(ob, in2, s_keys, s_n);
-      double t2[kTopPer];
-#pragma unroll
-      for (int i = 0; i < kTopPer; ++i) {
-        const int p = kTopPer * tid + i;
-        t2[i] = p == 0 ? s : (p - 1 < M2 ? exp_libm(static_cast<double>(key_value(s_keys[p - 1]) - mx), s_exp) : 0.0);
-      }
-      exact_scan<0, kTopPer, 32>(t2, M2 + 1, 0.0, sh, &s);
-      st = tail(inh | in2, s);
-      for (int p = tid; p < M; p += kThreads) s_keys[p] = hk[p];
-      __syncthreads();
+    for (int j = 0; j < kRegSlots; ++j) {
+      const int bk = bucket(j, mb);
+      if (tid + kThreads * j < V && bk > bmax && bk <= bmax2) mask |= 1u << j;
     }
   }
   if (st != 1) {
     if (tid == 0) *flag = 1;
     return;
+  }
+  if (done != inh) {  // the head back from the workspace
+    for (int p = tid; p < M; p += kThreads) s_keys[p] = hk[p];
+    __syncthreads();
   }
   nucleus_finish(a, b, s_keys, M, mx, s, s_exp, sh, flag);
 }
