@@ -311,13 +311,14 @@ def _check_against_oracle(H, logits, cfg, steps, seeds, hist=None):
         assert [int(v) for v in out.numpy()] == want, step
 
 
-@pytest.mark.parametrize("layout", ["one_tail_exit", "two_tail_exits", "no_tail_exit"])
+@pytest.mark.parametrize("layout", ["one_tail_exit", "two_tail_exits", "no_tail_exit", "crowded_bin"])
 def test_sampler_nucleus_head_tail_exits(hip, layout):
-    """Top-p without top-k from the sorted head of 4096 keys: the rest of the vocabulary joins the
-    softmax sum unsorted, and when the sum enters a new binade inside it the device finds that step
-    by a weighted radix select and takes it as the reference does (src/sampler.cpp:42-48).  The
-    logits are built so that the host restatement shows the intended number of exits and a nucleus
-    inside the head; ids must equal the reference's over several draws."""
+    """Top-p without top-k from the sorted head of at most 4096 keys: the rest of the vocabulary
+    joins the softmax sum unsorted, and when the sum enters a new binade after the head the next
+    keys are sorted and added in order first (a second exit goes to the full sort); a crowded bin of
+    equal logits takes the head's bitonic sort (src/sampler.cpp:36-48).  The logits are built so
+    that the host restatement shows the intended number of exits and a nucleus inside the head;
+    ids must equal the reference's over several draws."""
     V, batch = 32000, 6
     print(f"[case] sampler nucleus head layout={layout}", flush=True)
     g = D.rng(4100 + len(layout))
@@ -327,6 +328,13 @@ def test_sampler_nucleus_head_tail_exits(hip, layout):
     elif layout == "two_tail_exits":  # head sum about 6 in [4, 8), the tail takes it past 8 and 16
         rows = [_designed_tail(g, V, 0.00195, 4000.0, 3.0e-4, 7.0e-4) for _ in range(batch)]
         cfg, want_exits = dict(temperature=1.0, top_k=0, top_p=0.25, repetition_penalty=1.0), 2
+    elif layout == "crowded_bin":  # 300 equal logits inside the nucleus: the head's bitonic sort
+        rows = []
+        for _ in range(batch):
+            r = (g.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+            r[g.choice(V, size=300, replace=False)] = np.sort(r)[-40]
+            rows.append(r)
+        cfg, want_exits = dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.0), 0
     else:  # peaked: the sum settles inside the head
         rows = [(g.standard_normal(V, dtype=np.float32) * np.float32(4.0)).astype(np.float32) for _ in range(batch)]
         cfg, want_exits = dict(temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.0), 0
