@@ -1466,35 +1466,37 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 
 // The keys of the slots whose bit is set in `in` (slot j of thread t: id t + kThreads j, order bits
 // ob[j]) sorted descending into keys[0, n), keys[n, kTopM) zeros (below every key); keys[0, 2 kTopM)
-// is the working space.  Returns n; more than kTopM keys sort nothing.  A bucket sort: fine bins
-// of the logit, floor(64 (max - v)) (monotone in v, so bin order is key order), counted, their
-// exclusive prefix giving each bin's place, the keys scattered to their bins, and each key's place
-// inside its bin counted among the bin's keys.  A bin of more than kFineMax keys (many equal or
-// nearly equal logits) takes the bitonic sort instead.  s_bin, s_start: 1024 and 1025 words of
-// LDS; s_cnt: one int per wave.  Every thread calls it.
-constexpr int kFineBins = 1024;  // covers max - v < 16, past every head bucket
+// is the working space.  Returns n; more than kTopM keys sort nothing.  The keys are first gathered
+// into keys[0, n) (in wave, slot and lane order), then each thread takes four of them: a bucket
+// sort by fine bins of the logit, floor(256 (max - v)) (monotone in v, so bin order is key order),
+// counted, their exclusive prefix giving each bin's place, the keys scattered to their bins, and
+// each key's place inside its bin counted among the bin's keys.  A bin of more than kFineMax keys
+// (many equal or nearly equal logits) takes the bitonic sort instead.  s_bin, s_start: kFineBins
+// and kFineBins + 1 + kThreads / kWave words of LDS; s_cnt: one int per wave.  Every thread calls it.
+constexpr int kFineBins = 4096;  // covers max - v < 16, past every head bucket
 constexpr int kFineMax = 256;
 
 __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t in, float mx, uint64_t* keys,
                                            uint32_t* s_bin, uint32_t* s_start, int* s_cnt) {
-  static_assert(kFineBins == kThreads, "one bin per thread");
+  static_assert(kFineBins == 4 * kThreads && kTopM == 4 * kThreads, "four bins and four keys per thread");
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   auto fine = [&](float v) {
-    const float d = (mx - v) * 64.0f;
+    const float d = (mx - v) * 256.0f;
     return d < static_cast<float>(kFineBins - 1) ? static_cast<int>(d) : kFineBins - 1;
   };
   auto key_at = [&](int j) {
     return (static_cast<uint64_t>(ob[j]) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - (tid + kThreads * j));
   };
-  s_bin[tid] = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_bin[4 * tid + i] = 0u;
   int cnt = 0;
 #pragma unroll
   for (int j = 0; j < kRegSlots; ++j) cnt += __popcll(__ballot(in >> j & 1u));
   if (lane == 0) s_cnt[wave] = cnt;
   __syncthreads();
-  int n = 0, wpos = 0;
+  int n = 0, pos = 0;
   for (int w = 0; w < kThreads / kWave; ++w) {
-    wpos += w < wave ? s_cnt[w] : 0;
+    pos += w < wave ? s_cnt[w] : 0;
     n += s_cnt[w];
   }
   if (n > kTopM) {
@@ -1502,18 +1504,38 @@ __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t i
     return n;
   }
 #pragma unroll
-  for (int j = 0; j < kRegSlots; ++j)
-    if (in >> j & 1u) atomicAdd(&s_bin[fine(ob_value(ob[j]))], 1u);
+  for (int j = 0; j < kRegSlots; ++j) {
+    const bool take = in >> j & 1u;
+    const uint64_t m = __ballot(take);
+    const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+    if (take) keys[pos + r] = key_at(j);
+    pos += __popcll(m);
+  }
+  for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
+  __syncthreads();  // also: every wave has read s_cnt
+  uint64_t x[4];  // positions 4t .. 4t + 3
+#pragma unroll
+  for (int u = 0; u < 4; ++u) x[u] = keys[4 * tid + u];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (4 * tid + u < n) atomicAdd(&s_bin[fine(key_value(x[u]))], 1u);
   __syncthreads();
-  // each bin's place: exclusive prefix over the bins (a wave per 64 bins, then the waves in order)
-  const uint32_t c = s_bin[tid];
-  uint32_t inc = c;
+  // each bin's place: an exclusive prefix over the bins (four per thread, a wave per 256 bins, then
+  // the waves in order), and the largest bin
+  uint32_t c[4], tot = 0, cmax = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = s_bin[4 * tid + i];
+    tot += c[i];
+    cmax = max(cmax, c[i]);
+  }
+  uint32_t inc = tot;
   for (int o = 1; o < kWave; o <<= 1) {
     const uint32_t v = __shfl_up(inc, o, kWave);
     if (lane >= o) inc += v;
   }
-  const uint32_t wmax = wave_max_u32_dpp(c);
-  __syncthreads();  // every wave has read s_cnt
+  const uint32_t wmax = wave_max_u32_dpp(cmax);
   if (lane == kWave - 1) s_cnt[wave] = static_cast<int>(inc);
   if (lane == 0) s_start[kFineBins + 1 + wave] = wmax;  // scratch past the prefix: the waves' largest bins
   __syncthreads();
@@ -1522,28 +1544,16 @@ __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t i
     below += w < wave ? static_cast<uint32_t>(s_cnt[w]) : 0u;
     big = max(big, s_start[kFineBins + 1 + w]);
   }
-  const uint32_t start = below + inc - c;
-  s_start[tid] = start;
+  uint32_t st = below + inc - tot;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s_start[4 * tid + i] = st;
+    s_bin[4 * tid + i] = st;  // the scatter's cursor
+    st += c[i];
+  }
   if (tid == 0) s_start[kFineBins] = static_cast<uint32_t>(n);
-  s_bin[tid] = start;  // the scatter's cursor
   __syncthreads();
-  if (big > kFineMax) {  // the bitonic sort: gathered in wave, slot and lane order
-    int pos = wpos;
-#pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) {
-      const bool take = in >> j & 1u;
-      const uint64_t m = __ballot(take);
-      const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-      if (take) keys[pos + r] = key_at(j);
-      pos += __popcll(m);
-    }
-    for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
-    __syncthreads();
-    uint64_t x[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = keys[4 * tid + u];
-    __syncthreads();
+  if (big > kFineMax) {  // the bitonic sort of the gathered keys (zeros after them)
     sort4096_desc(x, keys);
     __syncthreads();
 #pragma unroll
@@ -1553,10 +1563,10 @@ __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t i
   }
   uint64_t* scat = keys + kTopM;  // the keys grouped by bin
 #pragma unroll
-  for (int j = 0; j < kRegSlots; ++j)
-    if (in >> j & 1u) scat[atomicAdd(&s_bin[fine(ob_value(ob[j]))], 1u)] = key_at(j);
+  for (int u = 0; u < 4; ++u)
+    if (4 * tid + u < n) scat[atomicAdd(&s_bin[fine(key_value(x[u]))], 1u)] = x[u];
   __syncthreads();
-  for (int p = tid; p < n; p += kThreads) {
+  for (int p = tid; p < n; p += kThreads) {  // consecutive threads on one bin: similar loop lengths
     const uint64_t k = scat[p];
     const int fb = fine(key_value(k));
     const int b0 = static_cast<int>(s_start[fb]), b1 = static_cast<int>(s_start[fb + 1]);
@@ -1564,7 +1574,6 @@ __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t i
     for (int q = b0; q < b1; ++q) r += scat[q] > k ? 1 : 0;
     keys[b0 + r] = k;
   }
-  for (int i = n + tid; i < kTopM; i += kThreads) keys[i] = 0ull;
   __syncthreads();
   return n;
 }
@@ -1611,7 +1620,7 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   __shared__ ScanShared sh;
   __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64 + kWave];
   __shared__ int s_n[16];
-  __shared__ uint32_t s_seen[(kRegSlots * kThreads + 31) / 32];  // the history marks, then the fine bins
+  __shared__ uint32_t s_seen[kFineBins];  // the history marks ((V + 31) / 32 words), then the fine bins
   __shared__ uint32_t s_start[kFineBins + 1 + kWaves];
   __shared__ uint64_t s_exp[256];
   __shared__ double s_red[kWaves];
@@ -1650,9 +1659,30 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   // One pass buckets the keys by floor(4 (max - v)) (clamped to 63; monotone in v, so a bucket
   // bound is a logit bound and the head is a prefix of the sorted order), per-wave histograms;
   // the bound kept is the largest whose buckets hold at most kTopM keys.
+  auto bucket_of = [&](uint32_t u) {
+    const float d = (mx - ob_value(u)) * 4.0f;
+    return d < 63.0f ? static_cast<int>(d) : 63;
+  };
   auto bucket = [&](int j, float m) {
     const float d = (m - ob_value(ob[j])) * 4.0f;
     return d < 63.0f ? static_cast<int>(d) : 63;
+  };
+  // The least order bits u with bucket_of(u) <= bk (bk < 63), by one wave: bucket_of does not rise
+  // with u (u = 0, a NaN, is in bucket 63 and the maximum's om in bucket 0), so the answer lies in
+  // (lo, hi] and each round splits the range into 64 parts, one per lane.  So a key is in buckets
+  // <= bk exactly when its order bits are at least the answer.
+  auto bucket_threshold = [&](int bk) {
+    uint64_t lo = 0, hi = om;
+    while (hi - lo > 1) {
+      const uint64_t step = (hi - lo + kWave - 1) / kWave;
+      const uint64_t c = min(lo + static_cast<uint64_t>(lane + 1) * step, hi);
+      const uint64_t ok = __ballot(bucket_of(static_cast<uint32_t>(c)) <= bk);  // lane 63 (c = hi) holds
+      const int f = __builtin_ctzll(ok);
+      const uint64_t below = __shfl(c, f > 0 ? f - 1 : 0, kWave);
+      hi = __shfl(c, f, kWave);
+      lo = f > 0 ? below : lo;
+    }
+    return static_cast<uint32_t>(hi);
   };
   for (int i2 = tid; i2 < kWaves * 64; i2 += kThreads) s_bh[i2] = 0u;
   __syncthreads();
@@ -1679,22 +1709,23 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
     const float hi = lane <= bm ? static_cast<float>(c) * expf(-0.25f * static_cast<float>(lane)) : 0.0f;
     const float lo = lane < 63 ? static_cast<float>(c) * expf(-0.25f * static_cast<float>(lane + 1)) : 0.0f;
     const float head_hi = wave_sum(hi), all_lo = wave_sum(lo);
-    if (lane == 0) s_n[0] = bm >= 0 && head_hi < 0.98f * a.top_p * all_lo ? -2 : bm;
+    const uint32_t thr = bm >= 0 ? bucket_threshold(bm) : 0u;
+    if (lane == 0) {
+      s_n[0] = bm >= 0 && head_hi < 0.98f * a.top_p * all_lo ? -2 : bm;
+      s_n[1] = static_cast<int>(thr);
+    }
   }
   __syncthreads();
   const int bmax = s_n[0];  // the head: buckets <= bmax
+  const uint32_t thr = static_cast<uint32_t>(s_n[1]);
   if (bmax < 0) {  // more than kTopM keys within a quarter of the maximum, or a nucleus past the head
     if (tid == 0) *flag = 1;
     return;
   }
-  uint32_t inh = 0;  // bit j: slot j is in the head (the buckets formed again, not kept from above)
-  {
-    float mb = mx;
-    asm volatile("" : "+v"(mb));
+  uint32_t inh = 0;  // bit j: slot j is in the head (ids past V have order bits 0, below thr)
 #pragma unroll
-    for (int j = 0; j < kRegSlots; ++j)
-      if (tid + kThreads * j < V && bucket(j, mb) <= bmax) inh |= 1u << j;
-  }
+  for (int j = 0; j < kRegSlots; ++j)
+    if (ob[j] >= thr) inh |= 1u << j;
   // The tail: the slots not yet summed.  One pass over the registers: 1 when the rest stays in
   // the sum's binade with no tie (the sum is then final), 2 when it leaves the binade, 0 for a tie
   // or a NaN term (the full sort's rule).
@@ -1771,24 +1802,26 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
         if (lane >= o) pre += v;
       }
       const uint64_t fits = __ballot(lane < 63 && lane > bmax && pre - static_cast<uint32_t>(M) <= kTopM);
-      if (lane == 0) s_n[0] = fits == 0 ? -1 : 63 - __builtin_clzll(fits);
+      const int bm2 = fits == 0 ? -1 : 63 - __builtin_clzll(fits);
+      const uint32_t thr2 = bm2 >= 0 ? bucket_threshold(bm2) : 0u;
+      if (lane == 0) {
+        s_n[0] = bm2;
+        s_n[1] = static_cast<int>(thr2);
+      }
     }
     __syncthreads();
     const int bmax2 = s_n[0];
+    const uint32_t thr2 = static_cast<uint32_t>(s_n[1]);
     __syncthreads();
     if (bmax2 < 0) {
       st = 0;
       break;
     }
     for (int p = tid; p < M; p += kThreads) hk[p] = s_keys[p];
-    float mb = mx;
-    asm volatile("" : "+v"(mb));
-    mask = 0;
+    mask = 0;  // buckets (bmax, bmax2]
 #pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) {
-      const int bk = bucket(j, mb);
-      if (tid + kThreads * j < V && bk > bmax && bk <= bmax2) mask |= 1u << j;
-    }
+    for (int j = 0; j < kRegSlots; ++j)
+      if (ob[j] < thr && ob[j] >= thr2) mask |= 1u << j;
   }
   if (st != 1) {
     if (tid == 0) *flag = 1;
