@@ -1148,7 +1148,10 @@ __device__ __forceinline__ double uniform_d(double v) {
 template <int MODE, int PER = kScanPer, int HEAD = kScanHead>
 __device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& sh, double* sum, double init = 0.0) {
   static_assert(HEAD <= kScanHead, "scan head");
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1), base = tid * PER;
+  // wave in a scalar register: a per-lane copy (the LDS addresses of the wave totals) was spilled
+  // and reloaded inside every round
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid & (kWave - 1),
+            base = tid * PER;
   constexpr int kW = kThreads / kWave;
   auto pred = [&](double s) { return MODE == 1 ? s >= x : (MODE == 2 ? x < s : false); };
   const int nh = min(n, HEAD);
@@ -1479,7 +1482,7 @@ constexpr int kFineMax = 256;
 __device__ __forceinline__ int gather_sort(uint32_t (&ob)[kRegSlots], uint32_t in, float mx, uint64_t* keys,
                                            uint32_t* s_bin, uint32_t* s_start, int* s_cnt) {
   static_assert(kFineBins == 4 * kThreads && kTopM == 4 * kThreads, "four bins and four keys per thread");
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid & (kWave - 1);
   auto fine = [&](float v) {
     const float d = (mx - v) * 256.0f;
     return d < static_cast<float>(kFineBins - 1) ? static_cast<int>(d) : kFineBins - 1;
@@ -1626,7 +1629,8 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   __shared__ double s_red[kWaves];
   __shared__ uint64_t s_redk[kWaves];
   __shared__ int s_bad;
-  const int b = blockIdx.x, V = a.vocab, tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int b = blockIdx.x, V = a.vocab, tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave),
+            lane = tid & (kWave - 1);
   int32_t* flag = full_sort_flag(a, b);
   stage_exp_table(s_exp);
   __syncthreads();
