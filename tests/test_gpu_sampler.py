@@ -367,6 +367,43 @@ def test_sampler_nucleus_mixed_batch(hip):
     _check_against_oracle(hip, logits, cfg, 4, [300 + b for b in range(batch)], hist=hist)
 
 
+def test_sampler_nucleus_bucket_edges(hip):
+    """Logits that sit on the head's bucket edges: many ids exactly k / 4 below the maximum (the
+    order-bit threshold of the head's last bucket must keep or drop each of them as the bucket
+    formula does), values near +-3e38 whose distance to the maximum overflows to infinity, large
+    offsets where the float spacing is coarse (many equal logits), and a maximum repeated.  Ids equal
+    the reference's call after call (src/sampler.cpp:13-70)."""
+    V, batch = 32000, 6
+    print("[case] sampler nucleus bucket edges", flush=True)
+    g = D.rng(4343)
+    rows = []
+    r = (g.standard_normal(V, dtype=np.float32) * np.float32(2.0)).astype(np.float32)
+    r[:] = np.minimum(r, np.float32(9.0))
+    ids = g.permutation(V)
+    r[ids[0]] = np.float32(10.0)
+    for k in range(1, 60):  # 60 ids at each quarter step below the maximum
+        r[ids[k * 60:(k + 1) * 60]] = np.float32(10.0 - k / 4.0)
+    rows.append(r)
+    r = (g.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    r[ids[:3000]] = np.float32(-3.0e38)
+    r[ids[3000:3005]] = np.float32(3.0e38) - np.float32(2.0 ** 103) * np.arange(5, dtype=np.float32)
+    rows.append(r)
+    rows.append((np.float32(1.0e6) + g.standard_normal(V, dtype=np.float32) * np.float32(4.0)).astype(np.float32))
+    r = (g.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    r[ids[100:140]] = r.max()
+    rows.append(r)
+    r = (g.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    r[ids[:5000]] = np.float32(-np.inf)
+    rows.append(r)
+    rows.append(np.float32(-1.0e6) + (g.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32))
+    logits = np.stack(rows).astype(np.float32)
+    for temperature in (1.0, 0.8):  # at 0.8 the 3e38 logits overflow to +inf: the full sort's rule
+        cfg = dict(temperature=temperature, top_k=0, top_p=0.9, repetition_penalty=1.0)
+        if temperature == 1.0:
+            print("[case]   nucleus sizes", [_nucleus_facts(logits[b], cfg)[0] for b in range(batch)], flush=True)
+        _check_against_oracle(hip, logits, cfg, 3, [910 + b for b in range(batch)])
+
+
 def test_sampler_nucleus_bench_logits(hip):
     """The bench's top-p-only sampler input (seeded N(0, 3) logits, T 0.8, repetition penalty 1.1,
     64-token histories, B = 64): some rows' sums enter their last binade after the head.  Ids equal
