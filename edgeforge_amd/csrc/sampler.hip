@@ -615,8 +615,9 @@ __device__ void sample_tail(const SampleArgs& a, int b, const uint64_t* sorted, 
 }
 
 // The logits of ids t + kThreads j (t = threadIdx.x) in registers, the repetition penalty applied
-// to every in-range history id once (marked in an LDS bitmap, then each owner applies it) and the
-// temperature (src/sampler.cpp:16-27).  V <= kRegSlots * kThreads; s_seen holds (V + 31) / 32 words.
+// to every in-range history id once and the temperature (src/sampler.cpp:16-27).  A history id
+// t' + kThreads j' sets bit j' of its owner t''s word in s_seen (kThreads words), so each thread
+// reads one word for its 32 slots.  V <= kRegSlots * kThreads.
 __device__ void load_tempered(const SampleArgs& a, int b, float (&rv)[kRegSlots], uint32_t* s_seen) {
   const int V = a.vocab;
   const float* lg = a.logits + b * a.ld;
@@ -628,19 +629,17 @@ __device__ void load_tempered(const SampleArgs& a, int b, float (&rv)[kRegSlots]
   if (a.penalty != 1.0f) {
     const int n = a.hist_len[b];
     const int32_t* h = a.hist + b * a.hist_ld;
-    for (int i = threadIdx.x; i < (V + 31) / 32; i += blockDim.x) s_seen[i] = 0u;
+    s_seen[threadIdx.x] = 0u;
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
       const int t = h[i];
-      if (t >= 0 && t < V) atomicOr(&s_seen[t >> 5], 1u << (t & 31));
+      if (t >= 0 && t < V) atomicOr(&s_seen[t % kThreads], 1u << (t / kThreads));
     }
     __syncthreads();
+    const uint32_t marks = s_seen[threadIdx.x];
 #pragma unroll
-    for (int j = 0; j < kRegSlots; ++j) {
-      const int id = threadIdx.x + kThreads * j;
-      if (id < V && (s_seen[id >> 5] >> (id & 31) & 1u))
-        rv[j] = rv[j] > 0.0f ? __fdiv_rn(rv[j], a.penalty) : rv[j] * a.penalty;
-    }
+    for (int j = 0; j < kRegSlots; ++j)
+      if (marks >> j & 1u) rv[j] = rv[j] > 0.0f ? __fdiv_rn(rv[j], a.penalty) : rv[j] * a.penalty;
   }
 #pragma unroll
   for (int j = 0; j < kRegSlots; ++j) rv[j] = __fdiv_rn(rv[j], a.temperature);
