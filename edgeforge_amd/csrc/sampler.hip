@@ -1620,7 +1620,7 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   constexpr int kWaves = kThreads / kWave;
   __shared__ uint64_t s_keys[2 * kChunk];  // the head's keys, and the sort's exchange buffers
   __shared__ ScanShared sh;
-  __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64 + kWave];
+  __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64];
   __shared__ int s_n[16];
   __shared__ uint32_t s_seen[kFineBins];  // the history marks ((V + 31) / 32 words), then the fine bins
   __shared__ uint32_t s_start[kFineBins + 1 + kWaves];
@@ -1660,8 +1660,9 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   }
   // The head: the keys whose logit is within some distance of the maximum, at most kTopM of them.
   // One pass buckets the keys by floor(4 (max - v)) (clamped to 63; monotone in v, so a bucket
-  // bound is a logit bound and the head is a prefix of the sorted order), per-wave histograms;
-  // the bound kept is the largest whose buckets hold at most kTopM keys.
+  // bound is a logit bound and the head is a prefix of the sorted order), per-wave histograms of
+  // buckets 0..62 (bucket 63 is never part of the head or of the bounds below); the bound kept is
+  // the largest whose buckets hold at most kTopM keys.
   auto bucket_of = [&](uint32_t u) {
     const float d = (mx - ob_value(u)) * 4.0f;
     return d < 63.0f ? static_cast<int>(d) : 63;
@@ -1690,9 +1691,9 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   for (int i2 = tid; i2 < kWaves * 64; i2 += kThreads) s_bh[i2] = 0u;
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kRegSlots; ++j) {  // bucket 63 (the rest, never in the head) goes to a slot per lane
-    const int bk = bucket(j, mx);
-    if (tid + kThreads * j < V) atomicAdd(&s_bh[bk < 63 ? wave * 64 + bk : kWaves * 64 + lane], 1u);
+  for (int j = 0; j < kRegSlots; ++j) {  // bucket 63 (the rest, never in the head) is not counted:
+    const int bk = bucket(j, mx);        // ids past V have order bits 0, a NaN, so they fall there
+    if (bk < 63) atomicAdd(&s_bh[wave * 64 + bk], 1u);
   }
   __syncthreads();
   if (wave == 0) {  // bucket `lane`: its count, the inclusive prefix over buckets <= lane
