@@ -1390,7 +1390,7 @@ __device__ void sample_tail_scan(const SampleArgs& a, int b, const uint64_t* sor
 // rint(t / u) u, u = 2^(e-52), unless t / u is halfway between integers (a tie, rounded by the
 // parity of s).  So the tail adds K u, K = the sum of rint(t / u) over it, when s / u + K < 2^53 and
 // no tail term is a tie.  When the sum leaves its binade in the tail, the next buckets (at most
-// kTopM - 1 keys) are sorted and added in order after the head's sum, and the rest is checked
+// kTopM keys) are sorted and added in order after the head's sum, and the rest is checked
 // again.  A sum that still leaves its binade, a tie, a term that is not finite, or a nucleus that
 // reaches past the head leaves the sequence to the full sort (the flag in its workspace), whose
 // launches follow and return at once for every other sequence.
