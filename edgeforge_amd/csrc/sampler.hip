@@ -1218,18 +1218,20 @@ __device__ int exact_scan(const double (&t)[PER], int n, double x, ScanShared& s
       const double M0 = ldexp(s, sc);
       const bool mine = base + PER > j0 && base < n;
       double T = 0.0;
-      bool tie = false;
+      uint32_t tie_u = 0;
       if (mine) {
+        // branch-free (a select per term, the tie as an integer): per-term branches cost scalar
+        // exec-mask instructions, and the CU's one scalar unit serves all sixteen waves
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const int j = base + i;
-          if (j >= j0 && j < n) {
-            const double y = ldexp(t[i], sc), k = rint(y);
-            T += k;
-            tie = tie || fabs(y - k) == 0.5;
-          }
+          const uint32_t in = static_cast<uint32_t>(j - j0) < static_cast<uint32_t>(n - j0) ? 1u : 0u;
+          const double y = ldexp(t[i], sc), k = rint(y);
+          T += in ? k : 0.0;
+          tie_u |= in & (fabs(y - k) == 0.5 ? 1u : 0u);
         }
       }
+      const bool tie = tie_u != 0;
       // exclusive prefix of the thread totals: lanes below this one, then the waves below (a
       // thread after the first inexact step may hold huge totals; they never enter the prefix of
       // a thread before it)
