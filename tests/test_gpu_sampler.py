@@ -103,12 +103,13 @@ def test_sampler_ids_bit_exact_over_steps(hip, ci, batch):
         hist = g.integers(0, V, size=(batch, 64)).astype(np.int32)
         hist[:, 0] = -1  # out-of-range ids are skipped
         hist[:, 1] = hist[:, 2]  # repeated ids penalised once
-        hlen = np.full(batch, 64, np.int32)
+        hist[:, 3], hist[:, 4], hist[:, 5] = V, V - 1, 32767  # past the vocabulary; the last id
+        hlen = np.array([64 - 13 * (b % 5) for b in range(batch)], np.int32)
         out = hip.DeviceArray((batch,), np.int32)
         hip.sample(hip.DeviceArray.from_host(logits), V, cfg, out, batch=batch, hist=hip.DeviceArray.from_host(hist),
                    hist_len=hip.DeviceArray.from_host(hlen), hist_ld=64, rng=rng, ws=ws)
         got = out.numpy()
-        want = [cpu[b].sample(logits[b], hist[b]) for b in range(batch)]
+        want = [cpu[b].sample(logits[b], hist[b][:hlen[b]]) for b in range(batch)]
         assert [int(v) for v in got] == want, (step, cfg)
 
 
@@ -402,6 +403,31 @@ def test_sampler_nucleus_bucket_edges(hip):
         if temperature == 1.0:
             print("[case]   nucleus sizes", [_nucleus_facts(logits[b], cfg)[0] for b in range(batch)], flush=True)
         _check_against_oracle(hip, logits, cfg, 3, [910 + b for b in range(batch)])
+
+
+@pytest.mark.parametrize("top_k", [0, 40])
+def test_sampler_long_history(hip, top_k):
+    """Histories longer than a workgroup (2000 entries, hist_ld 2048, some past the vocabulary and
+    many repeated): the penalty marks take several passes per thread; ids equal the reference's on
+    the register path with and without top-k (src/sampler.cpp:16-24)."""
+    V, batch, L = 32000, 4, 2048
+    print(f"[case] sampler long history top_k={top_k}", flush=True)
+    g = D.rng(5150 + top_k)
+    logits = (g.standard_normal((batch, V), dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    hist = g.integers(-10, V + 10, size=(batch, L)).astype(np.int32)
+    hist[:, 1500:] = hist[:, :L - 1500]  # repeats
+    hlen = np.array([2000, 1025, 1024, 1], np.int32)
+    cfg = dict(temperature=0.8, top_k=top_k, top_p=0.95, repetition_penalty=1.3)
+    seeds = [60 + b for b in range(batch)]
+    rng = hip.RngStates(seeds)
+    cpu = [O.Sampler(seed=s, **cfg) for s in seeds]
+    ws = hip.DeviceArray((EL.lib().ef_hip_sample_workspace_bytes(V, batch),), np.uint8)
+    out = hip.DeviceArray((batch,), np.int32)
+    dl, dh, dn = hip.DeviceArray.from_host(logits), hip.DeviceArray.from_host(hist), hip.DeviceArray.from_host(hlen)
+    for step in range(3):
+        hip.sample(dl, V, cfg, out, batch=batch, hist=dh, hist_len=dn, hist_ld=L, rng=rng, ws=ws)
+        want = [cpu[b].sample(logits[b], hist[b][:hlen[b]]) for b in range(batch)]
+        assert [int(v) for v in out.numpy()] == want, step
 
 
 def test_sampler_nucleus_bench_logits(hip):
