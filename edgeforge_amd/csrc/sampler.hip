@@ -717,7 +717,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ int s_idx[kThreads / kWave];
   __shared__ int s_cnt, s_keep, s_stop;
   __shared__ double s_sum;
-  __shared__ uint32_t s_seen[(32768 + 31) / 32];
+  __shared__ uint32_t s_seen[(32768 + 31) / 32];  // history marks: a bitmap (V <= 32768), or a word per thread
   __shared__ double s_prob[kMaxTopK];  // the kept probabilities of the top-k path
 
   const int b = blockIdx.x, V = a.vocab;
@@ -1624,7 +1624,7 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleArgs a) {
   __shared__ ScanShared sh;
   __shared__ uint32_t s_wmax[kWaves], s_bh[kWaves * 64];
   __shared__ int s_n[16];
-  __shared__ uint32_t s_seen[kFineBins];  // the history marks ((V + 31) / 32 words), then the fine bins
+  __shared__ uint32_t s_seen[kFineBins];  // the history marks (one word per thread), then the fine bins
   __shared__ uint32_t s_start[kFineBins + 1 + kWaves];
   __shared__ uint64_t s_exp[256];
   __shared__ double s_red[kWaves];
